@@ -1,0 +1,217 @@
+// Row movement for the offload tiers: gather / copy of KV rows with 16-byte coalesced loads, the per-token split
+// of selected rows into the HBM hot-row tier and the host tier, and the prefill compact stage.
+//
+// References: LayerOffload.gather / _gather_rows_kernel (dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:
+// 293-306, 1157-1163: invalid row -> zero row); the hit / miss resolution of the row cache (offload_fill.py:204-248,
+// sparse_offload.py:454-456: a row lives in an HBM line or is read from host memory); compact_stage
+// (dsa_sm89.py:27-35: distinct selected positions, sorted, and the selection remapped into them).
+//
+// Rows are moved in 16-byte chunks, one chunk per thread: a warp-free, fully coalesced pattern that works the same
+// for HBM sources and for pinned host memory mapped into the device address space (reads then cross PCIe).
+#include "spmla_common.h"
+
+namespace spmla {
+namespace gth {
+
+// dst row i = src row rows[i] (0 <= rows[i] < R), zero row otherwise; row_bytes % 16 == 0.
+__global__ void gather_kernel(const uint8_t* src, long long R, int row_bytes, const long long* rows, int n,
+                              uint8_t* dst, long long dst_stride) {
+  const int chunks = row_bytes >> 4;
+  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= (long long)n * chunks) return;
+  const int i = (int)(g / chunks), c = (int)(g % chunks);
+  const long long r = rows[i];
+  u32x4 v = u32x4{0, 0, 0, 0};
+  if (r >= 0 && r < R) v = *(const u32x4*)(src + r * row_bytes + c * 16);
+  *(u32x4*)(dst + (long long)i * dst_stride + c * 16) = v;
+}
+
+// dst row dst_rows[i] = src row src_rows[i]; pairs with an invalid side are skipped.
+__global__ void copy_kernel(const uint8_t* src, long long R_src, const long long* src_rows, uint8_t* dst,
+                            long long R_dst, const long long* dst_rows, int row_bytes, int n) {
+  const int chunks = row_bytes >> 4;
+  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= (long long)n * chunks) return;
+  const int i = (int)(g / chunks), c = (int)(g % chunks);
+  const long long s = src_rows[i], d = dst_rows[i];
+  if (s < 0 || s >= R_src || d < 0 || d >= R_dst) return;
+  *(u32x4*)(dst + d * row_bytes + c * 16) = *(const u32x4*)(src + s * row_bytes + c * 16);
+}
+
+// Per token (one 256-thread block): entries of idx[t] in order; a valid host row h with rowmap[h] >= 0 goes to
+// the HBM tier as line rowmap[h], other valid rows to the host tier as h. Both lists are compacted stably and padded
+// with -1 to K; counts[t] = number of entries of each list.
+__global__ void __launch_bounds__(256) tier_split_kernel(const int* idx, long long idx_st, int K, const int* rowmap,
+                                                         long long R, int* hbm, long long hbm_st, int* hcnt,
+                                                         int* host, long long host_st, int* scnt) {
+  __shared__ uint32_t wsum[2][5];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int* ir = idx + (long long)t * idx_st;
+  int* hr = hbm + (long long)t * hbm_st;
+  int* sr = host + (long long)t * host_st;
+  uint32_t nh = 0, ns = 0;
+  for (int k0 = 0; k0 < K; k0 += 256) {
+    const int k = k0 + tid;
+    int h = k < K ? ir[k] : -1;
+    const bool valid = h >= 0 && (long long)h < R;
+    const int line = valid ? rowmap[h] : -1;
+    const bool isH = valid && line >= 0, isS = valid && line < 0;
+    const unsigned long long bh = __ballot(isH), bs = __ballot(isS);
+    const unsigned long long lm = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const uint32_t ph = __popcll(bh & lm), ps = __popcll(bs & lm);
+    if (lane == 0) { wsum[0][wv] = __popcll(bh); wsum[1][wv] = __popcll(bs); }
+    __syncthreads();
+    uint32_t oh = 0, os = 0, th = 0, ts = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (w < wv) { oh += wsum[0][w]; os += wsum[1][w]; }
+      th += wsum[0][w]; ts += wsum[1][w];
+    }
+    if (isH) hr[nh + oh + ph] = line;
+    if (isS) sr[ns + os + ps] = h;
+    nh += th; ns += ts;
+    __syncthreads();
+  }
+  for (int k = nh + tid; k < K; k += 256) hr[k] = -1;
+  for (int k = ns + tid; k < K; k += 256) sr[k] = -1;
+  if (tid == 0) { hcnt[t] = (int)nh; scnt[t] = (int)ns; }
+}
+
+// ---- compact stage: bitmap of selected positions -> ranks
+__global__ void zero_u32(uint32_t* p, long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+__global__ void mark_kernel(const int* sidx, long long s_st, int M, int K, int tot, uint32_t* bits) {
+  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= (long long)M * K) return;
+  const int m = (int)(g / K), k = (int)(g % K);
+  const int p = sidx[(long long)m * s_st + k];
+  if (p >= 0 && p < tot) atomicOr(&bits[p >> 5], 1u << (p & 31));
+}
+
+// one 1024-thread block: exclusive prefix of popcounts over W words -> woff[W], total -> *U
+__global__ void __launch_bounds__(1024) scan_kernel(const uint32_t* bits, int W, uint32_t* woff, int* U) {
+  __shared__ uint32_t part[1024];
+  __shared__ uint32_t wsum[17];
+  const int tid = threadIdx.x;
+  const int per = (W + 1023) / 1024;
+  const int w0 = tid * per;
+  uint32_t s = 0;
+  for (int i = 0; i < per && w0 + i < W; ++i) s += __popc(bits[w0 + i]);
+  // block exclusive scan of s
+  const int lane = tid & 63, wv = tid >> 6;
+  uint32_t inc = s;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) wsum[wv] = inc;
+  __syncthreads();
+  if (wv == 0) {
+    const uint32_t w = lane < 16 ? wsum[lane] : 0u;
+    uint32_t wi = w;
+    for (int o = 1; o < 16; o <<= 1) {
+      const uint32_t t = __shfl_up(wi, o, 64);
+      if (lane >= o) wi += t;
+    }
+    if (lane < 16) wsum[lane] = wi - w;
+    if (lane == 15) wsum[16] = wi;
+  }
+  __syncthreads();
+  uint32_t run = wsum[wv] + inc - s;
+  for (int i = 0; i < per && w0 + i < W; ++i) {
+    woff[w0 + i] = run;
+    run += __popc(bits[w0 + i]);
+  }
+  if (tid == 0) *U = (int)wsum[16];
+  (void)part;
+}
+
+__device__ inline uint32_t rank_of(const uint32_t* bits, const uint32_t* woff, int p) {
+  const uint32_t w = bits[p >> 5];
+  return woff[p >> 5] + __popc(w & ((1u << (p & 31)) - 1u));
+}
+
+__global__ void emit_kernel(const uint32_t* bits, const uint32_t* woff, int tot, const long long* rows,
+                            long long* sel) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= tot) return;
+  if (bits[p >> 5] & (1u << (p & 31))) sel[rank_of(bits, woff, p)] = rows[p];
+}
+
+__global__ void remap_kernel(const int* sidx, long long s_st, int M, int K, int tot, const uint32_t* bits,
+                             const uint32_t* woff, int* sidx2, long long s2_st) {
+  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= (long long)M * K) return;
+  const int m = (int)(g / K), k = (int)(g % K);
+  const int p = sidx[(long long)m * s_st + k];
+  sidx2[(long long)m * s2_st + k] = (p >= 0 && p < tot) ? (int)rank_of(bits, woff, p) : -1;
+}
+
+}  // namespace gth
+}  // namespace spmla
+
+using namespace spmla;
+
+extern "C" {
+
+int spmla_gather(const void* src, long long R, int row_bytes, const long long* rows, int n, void* dst,
+                 long long dst_stride, void* stream) {
+  if (n < 0 || R < 0 || row_bytes <= 0 || (row_bytes & 15)) return SPMLA_EARG;
+  if (n == 0) return SPMLA_OK;
+  if (!src || !rows || !dst) return SPMLA_EARG;
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < row_bytes) return SPMLA_EALIGN;
+  const long long work = (long long)n * (row_bytes >> 4);
+  hipLaunchKernelGGL(gth::gather_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)src, R, row_bytes, rows, n, (uint8_t*)dst, dst_stride);
+  return (int)hipGetLastError();
+}
+
+int spmla_copy_rows(const void* src, long long R_src, const long long* src_rows, void* dst, long long R_dst,
+                    const long long* dst_rows, int row_bytes, int n, void* stream) {
+  if (n < 0 || R_src < 0 || R_dst < 0 || row_bytes <= 0 || (row_bytes & 15)) return SPMLA_EARG;
+  if (n == 0) return SPMLA_OK;
+  if (!src || !dst || !src_rows || !dst_rows) return SPMLA_EARG;
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15)) return SPMLA_EALIGN;
+  const long long work = (long long)n * (row_bytes >> 4);
+  hipLaunchKernelGGL(gth::copy_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)src, R_src, src_rows, (uint8_t*)dst, R_dst, dst_rows, row_bytes, n);
+  return (int)hipGetLastError();
+}
+
+int spmla_tier_split(const int* idx, long long idx_st, int T, int K, const int* rowmap, long long R, int* hbm_idx,
+                     long long hbm_st, int* hbm_cnt, int* host_idx, long long host_st, int* host_cnt, void* stream) {
+  if (T < 0 || K < 0 || R < 0) return SPMLA_EARG;
+  if (T == 0) return SPMLA_OK;
+  if (!idx || !rowmap || !hbm_idx || !hbm_cnt || !host_idx || !host_cnt) return SPMLA_EARG;
+  hipLaunchKernelGGL(gth::tier_split_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, idx, idx_st, K, rowmap, R,
+                     hbm_idx, hbm_st, hbm_cnt, host_idx, host_st, host_cnt);
+  return (int)hipGetLastError();
+}
+
+// workspace: 2 * ceil(tot / 32) uint32 words (bitmap + word offsets), caller-owned.
+int spmla_compact_stage(const long long* rows, int tot, const int* sidx, long long s_st, int M, int K, void* workspace,
+                        long long* sel, int* U, int* sidx2, long long s2_st, void* stream) {
+  if (tot < 0 || M < 0 || K < 0) return SPMLA_EARG;
+  if (!U || (tot > 0 && (!rows || !workspace || !sel)) || (M > 0 && K > 0 && (!sidx || !sidx2))) return SPMLA_EARG;
+  hipStream_t s = (hipStream_t)stream;
+  const int W = (tot + 31) / 32;
+  uint32_t* bits = (uint32_t*)workspace;
+  uint32_t* woff = bits + W;
+  if (W > 0)
+    hipLaunchKernelGGL(gth::zero_u32, dim3((W + 255) / 256), dim3(256), 0, s, bits, (long long)W);
+  const long long mk = (long long)M * K;
+  if (mk > 0 && W > 0)
+    hipLaunchKernelGGL(gth::mark_kernel, dim3((unsigned)((mk + 255) / 256)), dim3(256), 0, s, sidx, s_st, M, K, tot, bits);
+  hipLaunchKernelGGL(gth::scan_kernel, dim3(1), dim3(1024), 0, s, bits, W, woff, U);
+  if (tot > 0)
+    hipLaunchKernelGGL(gth::emit_kernel, dim3((tot + 255) / 256), dim3(256), 0, s, bits, woff, tot, rows, sel);
+  if (mk > 0)
+    hipLaunchKernelGGL(gth::remap_kernel, dim3((unsigned)((mk + 255) / 256)), dim3(256), 0, s, sidx, s_st, M, K, tot,
+                       bits, woff, sidx2, s2_st);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

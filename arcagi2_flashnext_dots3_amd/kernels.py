@@ -1,0 +1,210 @@
+"""Tensor-level wrappers of the C-ABI entry points (include/spmla.h): argument checks, strides, the caller's stream.
+
+Each wrapper mirrors the Python side of the reference kernel it replaces (offload_cuda2.attend,
+offload_cuda.split_partials, fast_topk.local/merge, ShardStore.write/logits, LayerOffload.gather), raises
+RuntimeError on a failed launch and never falls back to a CPU path.
+"""
+import torch
+
+from . import _lib
+
+D_LAT, D_ROPE, D_QK = 512, 64, 576
+ROW656, ROW576, KEYROW = 656, 576, 132
+LOG2E = 1.4426950408889634
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _need(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+# ---------------------------------------------------------------------------------------------- cache write
+def cache_write(kv_c, k_pe, slots, cache, fmt=0, kv_scale=1.0, block_size=None, block_stride=None):
+    """kv_c [n, 512] bf16, k_pe [n, 64] or [n, 1, 64] bf16, slots [n] int64 -> rows of `cache` (uint8, Row656
+    (fmt 0) or Row576 (fmt 1)). cache is [R, row] or paged [blocks, block_size, row] (block stride may be padded)."""
+    kpe = k_pe.reshape(k_pe.shape[0], -1)
+    n = min(kv_c.shape[0], slots.shape[0])
+    rowb = ROW656 if fmt == 0 else ROW576
+    _need(kv_c.dtype == torch.bfloat16 and kpe.dtype == torch.bfloat16, "kv_c / k_pe must be bf16")
+    _need(kv_c.shape[1] == D_LAT and kpe.shape[1] == D_ROPE and kv_c.stride(1) == 1 and kpe.stride(1) == 1,
+          "kv_c [n, 512] / k_pe [n, 64] with contiguous rows")
+    _need(cache.dtype == torch.uint8 and cache.shape[-1] == rowb and cache.stride(-1) == 1, "cache rows of uint8")
+    _need(slots.dtype == torch.int64, "slots int64")
+    if cache.dim() == 3:
+        bs, bstride, R = cache.shape[1], cache.stride(0), cache.shape[0] * cache.shape[1]
+        _need(cache.stride(1) == rowb, "rows inside a block must be contiguous")
+    else:
+        R = cache.shape[0]
+        bs = block_size or max(1, R)
+        bstride = block_stride or bs * rowb
+    _lib.call("spmla_cache_write", kv_c.data_ptr(), kv_c.stride(0), kpe.data_ptr(), kpe.stride(0), slots.data_ptr(),
+              n, cache.data_ptr(), R, bs, bstride, int(fmt), float(kv_scale), _stream(kv_c))
+
+
+def index_key_write(k, slots, store, P=1, rank=0, ue8m0=False):
+    """k [n, 128] bf16 -> store [blocks, rows_per_block, 132] (or [R, 132]) uint8 rows of this rank."""
+    n = min(k.shape[0], slots.shape[0])
+    _need(k.dtype == torch.bfloat16 and k.shape[1] == 128 and k.stride(1) == 1, "k [n, 128] bf16")
+    _need(store.dtype == torch.uint8 and store.shape[-1] == KEYROW, "store rows of 132 bytes")
+    if store.dim() == 3:
+        rpb, bstride, R = store.shape[1], store.stride(0), store.shape[0] * store.shape[1]
+    else:
+        R = store.shape[0]
+        rpb, bstride = max(1, R), max(1, R) * KEYROW
+    _lib.call("spmla_index_key_write", k.data_ptr(), k.stride(0), slots.data_ptr(), n, store.data_ptr(), R, P, rank,
+              rpb, bstride, int(bool(ue8m0)), _stream(k))
+
+
+# ---------------------------------------------------------------------------------------------- indexer
+def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P=1, rank=0, noinf=False):
+    """q [rows, 64, 128] bf16, w [rows, 64] fp32, store [blocks, rpb, 132] uint8, block_table [nreq, cols] int32,
+    req / ctx [rows] int32 -> logits [rows, Lc] fp32 (column j = position j * P + rank)."""
+    rows, H, D = q.shape
+    _need(q.dtype == torch.bfloat16 and q.stride(2) == 1, "q bf16 with contiguous head dim")
+    _need(w.dtype == torch.float32 and w.stride(1) == 1, "w fp32")
+    _need(req.dtype == torch.int32 and ctx.dtype == torch.int32 and block_table.dtype == torch.int32, "int32 tables")
+    if store.dim() == 3:
+        rpb, bstride, R = store.shape[1], store.stride(0), store.shape[0] * store.shape[1]
+    else:
+        R = store.shape[0]
+        rpb, bstride = max(1, R), max(1, R) * KEYROW
+    if out is None:
+        out = torch.empty(rows, max(Lc, 1), dtype=torch.float32, device=q.device)
+    _lib.call("spmla_index_logits", q.data_ptr(), q.stride(0), q.stride(1), w.data_ptr(), w.stride(0),
+              store.data_ptr(), R, rpb, bstride, block_table.data_ptr(), block_table.stride(0), block_size,
+              req.data_ptr(), ctx.data_ptr(), rows, H, D, Lc, P, rank, int(bool(noinf)), out.data_ptr(),
+              out.stride(0), _stream(q))
+    return out
+
+
+def topk(logits, ctx, K, out=None):
+    """logits [rows, Lc] fp32, ctx [rows] int32 -> [rows, K] int32 positions (value desc, position asc; -1 pad)."""
+    rows, Lc = logits.shape
+    _need(logits.dtype == torch.float32 and logits.stride(1) == 1, "fp32 logits with contiguous rows")
+    _need(ctx.dtype == torch.int32 and ctx.is_contiguous(), "ctx int32")
+    if out is None:
+        out = torch.empty(rows, K, dtype=torch.int32, device=logits.device)
+    _need(out.dtype == torch.int32 and out.stride(1) == 1, "out int32")
+    _lib.call("spmla_topk", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
+              out.stride(0), _stream(logits))
+    return out
+
+
+def rows_from_topk(topk_pos, req, block_table, block_size, stride_rows=None, rows=None, counts=None):
+    """Request-local positions [T, K] -> global rows [T, K] int32 (vLLM triton_convert_req_index_to_global_index)."""
+    T, K = topk_pos.shape
+    if rows is None:
+        rows = torch.empty(T, K, dtype=torch.int32, device=topk_pos.device)
+    _lib.call("spmla_rows_from_topk", topk_pos.data_ptr(), topk_pos.stride(0), req.data_ptr(),
+              block_table.data_ptr(), block_table.stride(0), block_table.shape[1], block_size,
+              stride_rows if stride_rows is not None else block_size, T, K, rows.data_ptr(), rows.stride(0),
+              _ptr(counts), _stream(topk_pos))
+    return rows
+
+
+# ---------------------------------------------------------------------------------------------- rows
+def gather(src, rows, out, R=None):
+    """out[i] = src[rows[i]] (zero row when rows[i] is outside [0, R)); src [R, row] uint8 (device or mapped host)."""
+    n = rows.shape[0]
+    rowb = out.shape[-1]
+    _need(rows.dtype == torch.int64, "rows int64")
+    _lib.call("spmla_gather", src.data_ptr() if torch.is_tensor(src) else int(src),
+              int(R if R is not None else src.shape[0]), rowb, rows.data_ptr(), n, out.data_ptr(), out.stride(0),
+              _stream(out))
+    return out
+
+
+def copy_rows(src, src_rows, dst, dst_rows, R_src=None):
+    n = src_rows.shape[0]
+    _lib.call("spmla_copy_rows", src.data_ptr() if torch.is_tensor(src) else int(src),
+              int(R_src if R_src is not None else src.shape[0]), src_rows.data_ptr(), dst.data_ptr(), dst.shape[0],
+              dst_rows.data_ptr(), dst.shape[-1], n, _stream(dst))
+
+
+def tier_split(idx, rowmap, R, hbm=None, hbm_cnt=None, host=None, host_cnt=None):
+    T, K = idx.shape
+    dev = idx.device
+    hbm = torch.empty(T, K, dtype=torch.int32, device=dev) if hbm is None else hbm
+    host = torch.empty(T, K, dtype=torch.int32, device=dev) if host is None else host
+    hbm_cnt = torch.empty(T, dtype=torch.int32, device=dev) if hbm_cnt is None else hbm_cnt
+    host_cnt = torch.empty(T, dtype=torch.int32, device=dev) if host_cnt is None else host_cnt
+    _lib.call("spmla_tier_split", idx.data_ptr(), idx.stride(0), T, K, rowmap.data_ptr(), int(R), hbm.data_ptr(),
+              hbm.stride(0), hbm_cnt.data_ptr(), host.data_ptr(), host.stride(0), host_cnt.data_ptr(), _stream(idx))
+    return hbm, hbm_cnt, host, host_cnt
+
+
+def compact_stage(rows, sidx, workspace=None):
+    """rows [tot] int64, sidx [M, K] int32 -> (sel [tot] int64 (first U valid), U [1] int32 on device, sidx2)."""
+    tot = rows.shape[0]
+    M, K = sidx.shape
+    W = (tot + 31) // 32
+    if workspace is None:
+        workspace = torch.empty(max(1, 2 * W), dtype=torch.int32, device=rows.device)
+    sel = torch.empty(max(1, tot), dtype=torch.int64, device=rows.device)
+    U = torch.empty(1, dtype=torch.int32, device=rows.device)
+    sidx2 = torch.empty_like(sidx)
+    _lib.call("spmla_compact_stage", rows.data_ptr(), tot, sidx.data_ptr(), sidx.stride(0), M, K,
+              workspace.data_ptr(), sel.data_ptr(), U.data_ptr(), sidx2.data_ptr(), sidx2.stride(0), _stream(rows))
+    return sel, U, sidx2
+
+
+# ---------------------------------------------------------------------------------------------- attention
+def attention_ok(q, idx):
+    """Preconditions of spmla_attn_splitk (the reference's offload_cuda2.ok analogue)."""
+    return (q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[2] == D_QK and q.stride(2) == 1
+            and q.data_ptr() % 16 == 0 and q.stride(0) % 8 == 0 and q.stride(1) % 8 == 0
+            and idx.dtype == torch.int32 and idx.stride(1) == 1)
+
+
+def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=1, kcount=None, ws=None, R=None):
+    """q [T, H, 576] bf16, pool [R, 656] uint8 Row656 rows (or a mapped host address with R given), idx [T, K]
+    int32 rows -> (out [T, H, 512] bf16, lse [T, H] fp32). split > 1 cuts K into partials merged by lse_merge."""
+    T, H, _ = q.shape
+    K = idx.shape[1]
+    _need(attention_ok(q, idx), "attend: q must be bf16 [T, H, 576] with 16-byte aligned rows, idx int32")
+    if out is None:
+        out = torch.empty(T, H, D_LAT, dtype=torch.bfloat16, device=q.device)
+    if lse is None:
+        lse = torch.empty(T, H, dtype=torch.float32, device=q.device)
+    Rv = int(R if R is not None else pool.shape[0])
+    pptr = pool.data_ptr() if torch.is_tensor(pool) else int(pool)
+    st = _stream(q)
+    if split == 1:
+        _lib.call("spmla_attn_splitk", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(),
+                  idx.stride(0), K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), 1, out.data_ptr(),
+                  out.stride(0), out.stride(1), lse.data_ptr(), lse.stride(0), None, None, st)
+        return out, lse
+    if ws is None:
+        ws = (torch.empty(split, T, H, D_LAT, dtype=torch.float32, device=q.device),
+              torch.empty(split, T, H, dtype=torch.float32, device=q.device))
+    opart, lpart = ws
+    _lib.call("spmla_attn_splitk", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(), idx.stride(0),
+              K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), split, None, 0, 0, None, 0,
+              opart.data_ptr(), lpart.data_ptr(), st)
+    lse_merge(opart, lpart, out=out, lse=lse)
+    return out, lse
+
+
+def lse_merge(parts, lses, out=None, out_f32=None, lse=None):
+    """parts [n, T, H, 512] fp32 or bf16 (any strides with contiguous rows), lses [n, T, H] -> merged (out, lse)."""
+    n, T, H, _ = parts.shape
+    if out is None and out_f32 is None:
+        out = torch.empty(T, H, D_LAT, dtype=torch.bfloat16, device=parts.device)
+    if lse is None:
+        lse = torch.empty(T, H, dtype=torch.float32, device=parts.device)
+    ref = out if out is not None else out_f32
+    if out is not None and out_f32 is not None:
+        _need(out.stride() == out_f32.stride(), "out and out_f32 need the same strides")
+    _lib.call("spmla_lse_merge", parts.data_ptr(), int(parts.dtype == torch.bfloat16), parts.stride(0),
+              parts.stride(1), parts.stride(2), lses.data_ptr(), lses.stride(0), lses.stride(1), n, T, H,
+              _ptr(out), ref.stride(0), ref.stride(1), _ptr(out_f32), lse.data_ptr(), lse.stride(0),
+              _stream(parts))
+    return (out if out is not None else out_f32), lse

@@ -1,0 +1,135 @@
+/* libspmla_gfx950.so: MI355X (gfx950) kernels for the dotsnote FP8 sparse-MLA attention path.
+ *
+ * Calling convention (the reference's, dotsnote/engine/arcstats_pkg/arcstats/offload_cuda2.py:21-90 and
+ * csrc/offload_attn2.cu:2021-2104): raw device pointers into caller-owned buffers, element strides, a hipStream_t
+ * passed as void*, an int return code (0 ok, a hipError_t value, or SPMLA_EARG -2 / SPMLA_EALIGN -3 /
+ * SPMLA_ELIMIT -5 for rejected arguments). The library allocates nothing, never synchronizes the host and launches
+ * only kernels on the caller's stream, so every entry point can be captured in a HIP graph. Strides are in elements
+ * of the pointed-to type unless stated otherwise. bf16 tensors are passed as void* (uint16 bit patterns).
+ *
+ * Row formats: Row656 = [512 B e4m3fn latent | 4 x fp32 scale, one per 128 latent values | 64 x bf16 rope];
+ *              Row576 = [512 B e4m3fn latent | 64 B e4m3fn rope], one per-tensor kv_scale.
+ */
+#ifndef SPMLA_H
+#define SPMLA_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPMLA_EARG (-2)
+#define SPMLA_EALIGN (-3)
+#define SPMLA_ELIMIT (-5)
+
+/* KV-cache write: quantize and pack n tokens into rows at slots[i] (slot < 0 or >= R: skipped).
+ * Row of a slot: cache + (slot / block_size) * block_stride + (slot % block_size) * row_bytes (block_stride in bytes).
+ * fmt 0 = Row656 (per-128 absmax scales, kv_scale unused), fmt 1 = Row576 (clamp(x / kv_scale, +-448) -> e4m3).
+ * kv_c: [n][512] bf16 (row stride kv_st), k_pe: [n][64] bf16 (row stride pe_st).
+ * Replaces LayerOffload.store (dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:1131-1155, kernels :252-290)
+ * and PortableSparseImpl.do_kv_cache_update (dsa_sm89.py:281-290); Row656 closed form
+ * dotsnote/training/finetune/student.py:80-87, layout dotsnote/engine/vllm_patch/vllm/v1/hisparse/runtime.py:35-36. */
+int spmla_cache_write(const void* kv_c, long long kv_st, const void* k_pe, long long pe_st, const long long* slots,
+                      int n, void* cache, long long R, int block_size, long long block_stride, int fmt,
+                      float kv_scale, void* stream);
+
+/* Indexer key write: k [n][128] bf16 -> 132-byte rows [128 e4m3 codes | fp32 scale], scale = max(amax, 1e-4) / 448
+ * (ue8m0 != 0: rounded up to a power of two). Rank-sharded store: slot s is owned by rank s % P as local row s / P
+ * at store + (r / rows_per_block) * block_stride + (r % rows_per_block) * 132 (block_stride in bytes); P = 1 on one GPU.
+ * Replaces ShardStore.write / _shard_write_kernel (dotsnote/engine/arcstats_pkg/arcstats/shard_indexer.py:42-60, :112-116). */
+int spmla_index_key_write(const void* k, long long k_st, const long long* slots, int n, void* store,
+                          long long R_local, int P, int rank, int rows_per_block, long long block_stride, int ue8m0,
+                          void* stream);
+
+/* Indexer logits: out[row][j] = min(sum_h w[row][h] * relu(q[row][h] . kcode) * kscale, 60000) for the key at
+ * position pos = j * P + rank < ctx[row] (located through block_table[req[row]][pos / block_size]), -inf for
+ * pos >= ctx (columns j < Lc; noinf != 0 leaves tiles wholly beyond ctx unwritten). q [rows][H][D] bf16 with H = 64,
+ * D = 128; w [rows][H] fp32; out [rows][Lc] fp32. ctx[row] <= block_size * (columns of the block table).
+ * Replaces ShardStore.logits / _shard_logits_kernel and shard_logits_v2 'grp' / 'row8'
+ * (dotsnote/engine/arcstats_pkg/arcstats/shard_indexer.py:63-91, :118-143; shard_logits_v2.py:15-138). */
+int spmla_index_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
+                       const void* store, long long R_local, int rows_per_block, long long block_stride,
+                       const int* block_table, long long bt_st, int block_size, const int* req, const int* ctx,
+                       int rows, int H, int D, int Lc, int P, int rank, int noinf, float* out, long long out_st,
+                       void* stream);
+
+/* Exact top-K per row over columns j < min(ctx[row], Lc) of logits [rows][Lc] fp32: torch's order-preserving key
+ * (-0 < +0, NaN largest), equal values -> lower column; out[row][0..K) = columns sorted by (value desc, column asc),
+ * -1 where the value is +-inf and for slots beyond the valid columns. K <= 2048.
+ * Replaces fast_topk.local + fast_topk.merge at P = 1 (dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:52-78;
+ * csrc/topk_select.cu:251-286) and the torch.topk path of sharded_topk (shard_indexer.py:194-221). */
+int spmla_topk(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+               long long out_st, void* stream);
+
+/* Request-local top-k positions -> global cache rows: rows[t][k] = block_table[req[t]][p / block_size] * stride_rows
+ * + p % block_size for p = topk[t][k] >= 0 inside the table, else -1; counts[t] (optional) = valid entries.
+ * Replaces vLLM's triton_convert_req_index_to_global_index (call sites dotsnote/engine/arcstats_pkg/arcstats/
+ * dsa_sm89.py:314-315, :460-462, :467-469). T <= 65535. */
+int spmla_rows_from_topk(const int* topk, long long tk_st, const int* req, const int* block_table, long long bt_st,
+                         int bt_cols, int block_size, long long stride_rows, int T, int K, int* rows, long long r_st,
+                         int* counts, void* stream);
+
+/* Gather: dst row i (row stride dst_stride bytes) = src row rows[i] for 0 <= rows[i] < R, zero row otherwise.
+ * src may be HBM or pinned host memory mapped into the device address space. row_bytes % 16 == 0.
+ * Replaces LayerOffload.gather / _gather_rows_kernel (dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:
+ * 293-306, :1157-1163). */
+int spmla_gather(const void* src, long long R, int row_bytes, const long long* rows, int n, void* dst,
+                 long long dst_stride, void* stream);
+
+/* Row copy: dst row dst_rows[i] = src row src_rows[i] (pairs with an out-of-range side skipped); fills the HBM hot-row
+ * cache from the host pool. Replaces the row-cache fill copies (offload_fill.py:311-333, csrc/offload_attn.cu:522-584). */
+int spmla_copy_rows(const void* src, long long R_src, const long long* src_rows, void* dst, long long R_dst,
+                    const long long* dst_rows, int row_bytes, int n, void* stream);
+
+/* Tier split of the selected rows: for each token t, valid host rows h = idx[t][k] (0 <= h < R) with rowmap[h] >= 0
+ * go to hbm_idx[t] as cache line rowmap[h], the others to host_idx[t] as h; both compacted in order, padded with -1
+ * to K; hbm_cnt[t] / host_cnt[t] = lengths. Replaces the hit / miss resolution of the row cache
+ * (dotsnote/engine/arcstats_pkg/arcstats/offload_fill.py:204-248, sparse_offload.py:454-456, :756-778). */
+int spmla_tier_split(const int* idx, long long idx_st, int T, int K, const int* rowmap, long long R, int* hbm_idx,
+                     long long hbm_st, int* hbm_cnt, int* host_idx, long long host_st, int* host_cnt, void* stream);
+
+/* Prefill compact stage: sidx [M][K] positions into rows[0..tot) (-1 = none) -> sel[0..U) = rows of the distinct
+ * selected positions in ascending order, sidx2 = positions into sel (-1 kept), *U on the device.
+ * workspace: 2 * ceil(tot / 32) uint32, caller-owned. Replaces compact_stage (dsa_sm89.py:27-35). */
+int spmla_compact_stage(const long long* rows, int tot, const int* sidx, long long s_st, int M, int K, void* workspace,
+                        long long* sel, int* U, int* sidx2, long long s2_st, void* stream);
+
+/* Sparse-MLA attention over Row656 rows. q [T][H][576] bf16 (16-byte aligned rows), pool [R] Row656 rows,
+ * idx [T][K] int32 rows of the pool (invalid = outside [0, R)), kcount (optional) [T]: only the first kcount[t]
+ * entries are read. s = sm_scale * kv_scale * q . row; o = kv_scale * softmax(s) V_latent; lse = ln sum exp(s)
+ * (-inf and o = 0 for a token with no valid entry).
+ * S == 1: out [T][H][512] bf16 (strides o_st, o_sh), lse [T][H] fp32 (stride lse_st).
+ * S > 1: the K entries are cut into S splits; opart [S][T][H][512] fp32 (normalized) and lsepart [S][T][H] receive
+ * per-split partials for spmla_lse_merge. ceil(ceil(K / S) / 32) * 32 <= 2048.
+ * Replaces LayerOffload.attend's decode kernels (oa2_v2_launch dotsnote/engine/arcstats_pkg/arcstats/csrc/
+ * offload_attn2.cu:2021-2104, offload_split_launch csrc/offload_attn.cu:1155-1200, _sparse_mla_offload_split_kernel
+ * sparse_offload.py:419-516) and triton_bf16_mla_sparse_interface (vllm_patch/.../ops/xpu_mla_sparse.py:182-278),
+ * extended by the LSE output. */
+int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void* pool, long long R,
+                      const int* idx, long long idx_st, int K, const int* kcount, int T, int H, float sm_scale,
+                      float kv_scale, int S, void* out, long long o_st, long long o_sh, float* lse,
+                      long long lse_st, float* opart, float* lsepart, void* stream);
+
+/* LSE merge of n partial results (splits or tiers): part i of (t, h) at parts + i*o_ps + t*o_st + h*o_sh (512 values,
+ * fp32 or bf16), lse[i*l_ps + t*l_st + h]. o = sum_i exp(lse_i - L) o_i, L = ln sum_i exp(lse_i); all parts -inf ->
+ * o = 0, L = -inf. out bf16 and/or out_f32 (same strides), lse_out optional.
+ * Replaces _combine_kernel (dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:519-538) and the
+ * merge_attn_states call (vllm_patch/vllm/model_executor/layers/attention/sparse_mla_attention.py:1091-1097). */
+int spmla_lse_merge(const void* parts, int parts_bf16, long long o_ps, long long o_st, long long o_sh,
+                    const float* lse, long long l_ps, long long l_st, int n, int T, int H, void* out,
+                    long long out_st, long long out_sh, float* out_f32, float* lse_out, long long lo_st,
+                    void* stream);
+
+/* Build identification string (static storage). */
+const char* spmla_version(void);
+
+/* Workgroup shape used by spmla_attn_splitk: 1 or 2 teams of 4 waves (env SPMLA_ATTN_TEAMS, default 2). */
+int spmla_attn_teams(void);
+
+/* Host-side self-test hook: the e4m3fn encoder the kernels use, run on the CPU (no GPU call). */
+void spmla_host_e4m3_encode(const float* x, unsigned char* out, long long n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPMLA_H */

@@ -1,0 +1,347 @@
+"""CPU oracle for the dotsnote FP8 sparse-MLA path. TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the checker
+(or as the timed CPU baseline); the product path (arcagi2_flashnext_dots3_amd) never calls it.
+
+Every function restates the reference algorithm (numpy, float64 accumulation unless stated) and cites the reference
+file:line it follows (paths relative to the reference repository root). How each function is pinned independently
+of its own formula (library routines, invariants, brute force) is listed in `PINS` and exercised by
+tests/test_oracle.py.
+"""
+import numpy as np
+
+D_LAT, D_ROPE, D_QK = 512, 64, 576
+ROW656, ROW576, KEYROW = 656, 576, 132
+SC_OFF, ROPE_OFF = 512, 528
+LOG2E = 1.4426950408889634
+LN2 = 0.6931471805599453
+
+PINS = {
+    "e4m3_encode": "torch.Tensor.to(float8_e4m3fn) over every fp32 with |x| in [2^-12, 512) and signed specials",
+    "e4m3_decode": "torch float8_e4m3fn -> float32 on all 256 codes",
+    "bf16": "torch bfloat16 conversions",
+    "cache_write_656": "dequantized row within half an e4m3 ulp of x / s; per-group max code == 448 (0x7e); "
+                       "zero groups; rope bit copy; slot skipping",
+    "cache_write_576": "e4m3 of the clamped value (library encoder) ; rope codes",
+    "index_key_write": "same closed-form checks as cache_write_656 with s = max(amax, 1e-4) / 448; UE8M0 power of 2",
+    "attention": "torch.nn.functional.scaled_dot_product_attention (float64) on dequantized rows + torch.logsumexp;"
+                 " brute-force python loops on tiny cases; invariance under permutation of the selected rows",
+    "lse_merge": "merge of disjoint splits == single-pass attention (exact math), single part == identity",
+    "index_logits": "python triple loop on tiny cases; linearity in w; block-table indirection vs a flat store",
+    "topk": "torch.topk value sets; python sorted() with the (value desc, index asc) key on tiny / tie-heavy rows",
+    "rows_from_topk": "python loop over the block table",
+    "compact_stage": "torch.unique(sorted=True, return_inverse=True) (library)",
+    "gather": "numpy fancy indexing",
+    "tier_split": "python loop with stable order",
+}
+
+
+# ------------------------------------------------------------------------------------------------ scalars
+def bf16_bits_to_f32(b):
+    """uint16 bf16 bit patterns -> float32 (exact)."""
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x):
+    """float32 -> bf16 bits, round to nearest even (NaN kept quiet)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def e4m3_encode(x):
+    """float32 -> OCP e4m3fn codes, round to nearest even; |x| rounding past 448 and inf/NaN -> 0x7f | sign.
+    Integer restatement of the format (bias 7, 3 mantissa bits, subnormals m * 2^-9). The reference converts with
+    torch's / Triton's RNE float8e4nv casts: sparse_offload.py:263-266, shard_indexer.py:59,
+    dotsnote/training/finetune/student.py:87."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.int64)
+    sign = (u >> 24) & 0x80
+    a = u & 0x7FFFFFFF
+    e = (a >> 23) - 127
+    out = np.zeros(a.shape, dtype=np.int64)
+    # normal range
+    q = a >> 20
+    r = a & 0xFFFFF
+    q = q + ((r > 0x80000) | ((r == 0x80000) & ((q & 1) == 1))).astype(np.int64)
+    code_n = q - ((127 - 7) << 3)
+    code_n = np.where(code_n > 0x7E, 0x7F, code_n)
+    # subnormal range: value * 2^9 rounded to an integer 0..8
+    M = (a & 0x7FFFFF) | 0x800000
+    s = np.clip(14 - e, 0, 63)
+    s_ok = (e < -6) & (e >= -126) & (s <= 25)
+    sm = np.where(s_ok, s, 25)
+    qs = M >> sm
+    rs = M & ((np.int64(1) << sm) - 1)
+    half = np.int64(1) << (sm - 1)
+    qs = qs + ((rs > half) | ((rs == half) & ((qs & 1) == 1))).astype(np.int64)
+    code_s = np.where(s_ok, qs, 0)
+    out = np.where(e >= -6, code_n, code_s)
+    out = np.where(a >= 0x7F800000, 0x7F, out)
+    return (out | sign).astype(np.uint8)
+
+
+_E4M3_TABLE = None
+
+
+def e4m3_decode(c):
+    """e4m3fn codes -> float32 (exact): (-1)^s 2^(e-7)(1 + m/8), subnormal m 2^-9, 0x7f/0xff NaN."""
+    global _E4M3_TABLE
+    if _E4M3_TABLE is None:
+        t = np.zeros(256, dtype=np.float32)
+        for code in range(256):
+            s = -1.0 if code & 0x80 else 1.0
+            e, m = (code >> 3) & 15, code & 7
+            if e == 15 and m == 7:
+                t[code] = np.nan
+            elif e == 0:
+                t[code] = s * m * 2.0 ** -9
+            else:
+                t[code] = s * 2.0 ** (e - 7) * (1 + m / 8)
+        _E4M3_TABLE = t
+    return _E4M3_TABLE[np.asarray(c, dtype=np.uint8)]
+
+
+# ------------------------------------------------------------------------------------------------ KV write
+def _row_index(slot, block_size, R):
+    return slot
+
+
+def cache_write_656(kv_bits, pe_bits, slots, cache):
+    """Row656 quantize-and-pack into cache [R, 656] uint8 (in place); slots < 0 or >= R skipped.
+    Per 128 latent values: s = max(amax / 448, 1e-12) in fp32 (dotsnote/training/finetune/student.py:85-87:
+    clamp_min(amax / 448, 1e-12), (x / s).to(float8_e4m3fn)); layout [512 codes | 4 fp32 s | 64 bf16 rope]
+    (dotsnote/engine/vllm_patch/vllm/v1/hisparse/runtime.py:35-36)."""
+    R = cache.shape[0]
+    x = bf16_bits_to_f32(kv_bits).reshape(-1, 4, 128)
+    amax = np.abs(x).max(-1)
+    s = np.maximum((amax / np.float32(448.0)).astype(np.float32), np.float32(1e-12)).astype(np.float32)
+    codes = e4m3_encode((x / s[..., None]).astype(np.float32)).reshape(-1, 512)
+    for i, slot in enumerate(np.asarray(slots).tolist()[: x.shape[0]]):
+        if slot < 0 or slot >= R:
+            continue
+        row = cache[slot]
+        row[:512] = codes[i]
+        row[512:528] = s[i].astype(np.float32).view(np.uint8)
+        row[528:656] = np.asarray(pe_bits[i], dtype=np.uint16).view(np.uint8)
+    return cache
+
+
+def cache_write_576(kv_bits, pe_bits, slots, cache, kv_scale=1.0):
+    """Row576 (the reference's deployed row, dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:252-270):
+    e4m3_rne(clamp(x * (1 / kv_scale), -448, 448)) for latent and rope."""
+    R = cache.shape[0]
+    inv = np.float32(1.0 / kv_scale)
+    x = bf16_bits_to_f32(kv_bits) * inv
+    y = bf16_bits_to_f32(pe_bits).reshape(x.shape[0], -1) * inv
+    cx = e4m3_encode(np.clip(x, -448, 448).astype(np.float32))
+    cy = e4m3_encode(np.clip(y, -448, 448).astype(np.float32))
+    for i, slot in enumerate(np.asarray(slots).tolist()[: x.shape[0]]):
+        if 0 <= slot < R:
+            cache[slot, :512] = cx[i]
+            cache[slot, 512:576] = cy[i]
+    return cache
+
+
+def index_key_write(k_bits, slots, store, P=1, rank=0, ue8m0=False):
+    """Indexer key rows [128 codes | fp32 s], s = max(amax, 1e-4) / 448 (UE8M0: 2^ceil(log2 s)), owner slot % P,
+    local row slot // P (dotsnote/engine/arcstats_pkg/arcstats/shard_indexer.py:42-60)."""
+    x = bf16_bits_to_f32(k_bits).reshape(-1, 128)
+    s = (np.maximum(np.abs(x).max(-1), np.float32(1e-4)) / np.float32(448.0)).astype(np.float32)
+    if ue8m0:
+        u = s.view(np.uint32).astype(np.int64)
+        up = (u & 0x7FFFFF) != 0
+        u = np.where(up, (u & 0xFF800000) + 0x800000, u)
+        s = u.astype(np.uint32).view(np.float32)
+    codes = e4m3_encode((x / s[:, None]).astype(np.float32))
+    Rl = store.shape[0]
+    for i, slot in enumerate(np.asarray(slots).tolist()[: x.shape[0]]):
+        if slot < 0 or slot % P != rank or slot // P >= Rl:
+            continue
+        r = slot // P
+        store[r, :128] = codes[i]
+        store[r, 128:132] = s[i:i + 1].view(np.uint8)
+    return store
+
+
+# ------------------------------------------------------------------------------------------------ dequant
+def dequant_656(rows):
+    """Row656 bytes [n, 656] -> (latent [n, 512] float64, rope [n, 64] float64)."""
+    rows = np.asarray(rows, dtype=np.uint8)
+    codes = e4m3_decode(rows[:, :512]).astype(np.float64).reshape(-1, 4, 128)
+    sc = rows[:, 512:528].copy().view(np.float32).astype(np.float64)
+    lat = (codes * sc[:, :, None]).reshape(-1, 512)
+    rope = bf16_bits_to_f32(rows[:, 528:656].copy().view(np.uint16)).astype(np.float64)
+    return lat, rope
+
+
+def dequant_576(rows, kv_scale=1.0):
+    rows = np.asarray(rows, dtype=np.uint8)
+    v = e4m3_decode(rows[:, :576]).astype(np.float64)
+    return v[:, :512], v[:, 512:]
+
+
+# ------------------------------------------------------------------------------------------------ attention
+def attention(q, pool, idx, sm_scale, kv_scale=1.0, kcount=None, fmt=656):
+    """Sparse MLA over gathered rows (dotsnote/kaggle/runtime_dataset/bench_offload_attn2.py:77-93: gather rows,
+    s = q . row * scale, masked softmax in base 2, o = p V / sum p, x kv_scale; LSE of the same scores as in
+    dotsnote/engine/vllm_patch/vllm/v1/attention/ops/xpu_mla_sparse.py:155-161). float64.
+    q [T, H, 576] float (values of the bf16 query), pool [R, 656|576] uint8, idx [T, K] (valid iff 0 <= idx < R;
+    with kcount only the first kcount[t] entries). Returns out [T, H, 512], lse [T, H] (natural log).
+    No valid entry: out = 0, lse = -inf (the reference's split kernel gives o = 0, csrc/offload_attn.cu:446)."""
+    q = np.asarray(q, dtype=np.float64)
+    T, H, _ = q.shape
+    R = pool.shape[0]
+    idx = np.asarray(idx)
+    K = idx.shape[1]
+    out = np.zeros((T, H, 512))
+    lse = np.full((T, H), -np.inf)
+    for t in range(T):
+        kk = K if kcount is None else min(K, int(kcount[t]))
+        sel = idx[t, :kk].astype(np.int64)
+        v = sel[(sel >= 0) & (sel < R)]
+        if v.size == 0:
+            continue
+        if fmt == 656:
+            lat, rope = dequant_656(pool[v])
+        else:
+            lat, rope = dequant_576(pool[v])
+        rows = np.concatenate([lat, rope], 1)
+        s = (q[t] @ rows.T) * (sm_scale * kv_scale)          # [H, n]
+        m = s.max(1, keepdims=True)
+        p = np.exp(s - m)
+        l = p.sum(1, keepdims=True)
+        out[t] = (p @ lat) / l * kv_scale
+        lse[t] = (m + np.log(l))[:, 0]
+    return out, lse
+
+
+def lse_merge(parts, lses):
+    """o = sum_i exp(lse_i - L) o_i, L = log sum_i exp(lse_i); all -inf -> o = 0, L = -inf
+    (dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:519-538 in natural-log form)."""
+    parts = np.asarray(parts, dtype=np.float64)
+    lses = np.asarray(lses, dtype=np.float64)
+    M = lses.max(0)
+    finite = np.isfinite(M)
+    Ms = np.where(finite, M, 0.0)
+    w = np.where(np.isfinite(lses), np.exp(lses - Ms[None]), 0.0)
+    L = w.sum(0)
+    o = (w[..., None] * np.nan_to_num(parts)).sum(0) / np.where(L > 0, L, 1.0)[..., None]
+    o = np.where((L > 0)[..., None], o, 0.0)
+    lse = np.where(L > 0, Ms + np.log(np.where(L > 0, L, 1.0)), -np.inf)
+    return o, lse
+
+
+# ------------------------------------------------------------------------------------------------ indexer
+def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, P=1, rank=0, clamp=60000.0):
+    """logit[row, j] = min(sum_h w[row, h] * relu(q[row, h] . kcode) * kscale, 60000) for pos = j * P + rank <
+    ctx[row], -inf otherwise (dotsnote/engine/arcstats_pkg/arcstats/shard_logits_v2.py:84-100,
+    shard_indexer.py:77-91; torch statement dotsnote/training/finetune/student.py:220-221). float64.
+    store [R_local, 132] uint8; key of pos: block = block_table[req, pos // bs], local row (block*bs + pos%bs) // P."""
+    q = np.asarray(q, dtype=np.float64)
+    w = np.asarray(w, dtype=np.float64)
+    rows = q.shape[0]
+    out = np.full((rows, Lc), -np.inf)
+    Rl = store.shape[0]
+    for r in range(rows):
+        j = np.arange(Lc)
+        pos = j * P + rank
+        ok = pos < ctx[r]
+        j, pos = j[ok], pos[ok]
+        if j.size == 0:
+            continue
+        blk = np.asarray(block_table)[req[r], pos // block_size].astype(np.int64)
+        lrow = (blk * block_size + pos % block_size) // P
+        ok2 = (blk >= 0) & (lrow < Rl)
+        j, lrow = j[ok2], lrow[ok2]
+        kc = e4m3_decode(store[lrow, :128]).astype(np.float64)
+        ks = store[lrow, 128:132].copy().view(np.float32)[:, 0].astype(np.float64)
+        s = np.maximum(q[r] @ kc.T, 0.0)                       # [H, n]
+        lg = (w[r] @ s) * ks
+        out[r, j] = np.minimum(lg, clamp)
+    return out
+
+
+def okey(x):
+    """torch's order-preserving uint32 key of fp32 (-0 < +0, NaN largest): csrc/topk_select.cu:21-30 semantics."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    k = np.where(u & 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+    return np.where(np.isnan(np.asarray(x, dtype=np.float32)), 0xFFFFFFFF, k).astype(np.uint64)
+
+
+def topk(logits, ctx, K):
+    """Per row: the K largest of columns j < min(ctx, Lc) (key okey, equal keys -> lower column), output sorted by
+    (value desc, column asc), -1 for +-inf values and for missing slots (fast_topk.py:10-14 tie rule; merge
+    semantics csrc/topk_select.cu:13-15, :305-321; shard_indexer.py:212-221 maps +-inf to -1)."""
+    logits = np.asarray(logits, dtype=np.float32)
+    rows, Lc = logits.shape
+    out = np.full((rows, K), -1, dtype=np.int32)
+    for r in range(rows):
+        n = max(0, min(int(ctx[r]), Lc))
+        if n == 0:
+            continue
+        kv = okey(logits[r, :n]).astype(np.int64)
+        order = np.lexsort((np.arange(n), -kv))[:K]            # primary: key desc, secondary: column asc
+        vals = logits[r, order]
+        sel = np.where(np.isinf(vals), -1, order).astype(np.int32)
+        out[r, :sel.size] = sel
+    return out
+
+
+def rows_from_topk(topk_pos, req, block_table, block_size, stride_rows=None):
+    """rows = block_table[req, p // bs] * stride_rows + p % bs for p >= 0 inside the table and a block id >= 0,
+    else -1 (vLLM triton_convert_req_index_to_global_index semantics at dsa_sm89.py:314-315, :467-469)."""
+    stride_rows = block_size if stride_rows is None else stride_rows
+    tp = np.asarray(topk_pos, dtype=np.int64)
+    bt = np.asarray(block_table, dtype=np.int64)
+    out = np.full(tp.shape, -1, dtype=np.int64)
+    for t in range(tp.shape[0]):
+        for k in range(tp.shape[1]):
+            p = tp[t, k]
+            if p < 0 or p // block_size >= bt.shape[1]:
+                continue
+            b = bt[req[t], p // block_size]
+            if b >= 0:
+                out[t, k] = b * stride_rows + p % block_size
+    return out.astype(np.int32)
+
+
+def compact_stage(rows, sidx):
+    """(rows [tot], sidx [M, K]) -> (sel = rows of the sorted distinct selected positions, sidx2 into sel)
+    (dotsnote/engine/arcstats_pkg/arcstats/dsa_sm89.py:27-35)."""
+    sidx = np.asarray(sidx, dtype=np.int64)
+    v = sidx >= 0
+    u, inv = np.unique(sidx[v], return_inverse=True)
+    sidx2 = np.full(sidx.shape, -1, dtype=np.int64)
+    sidx2[v] = inv
+    return np.asarray(rows)[u], sidx2.astype(np.int32)
+
+
+def gather(src, rows):
+    """dst[i] = src[rows[i]] for 0 <= rows[i] < R, zero row otherwise (sparse_offload.py:293-306)."""
+    src = np.asarray(src)
+    rows = np.asarray(rows, dtype=np.int64)
+    ok = (rows >= 0) & (rows < src.shape[0])
+    out = np.zeros((rows.shape[0], src.shape[1]), dtype=src.dtype)
+    out[ok] = src[rows[ok]]
+    return out
+
+
+def tier_split(idx, rowmap, R):
+    """Per token: valid host rows with a cache line -> HBM list (line), others -> host list (row), stable order,
+    -1 padded (hit / miss resolution of the row cache, offload_fill.py:204-248)."""
+    idx = np.asarray(idx, dtype=np.int64)
+    T, K = idx.shape
+    hbm = np.full((T, K), -1, dtype=np.int32)
+    host = np.full((T, K), -1, dtype=np.int32)
+    hc = np.zeros(T, dtype=np.int32)
+    sc = np.zeros(T, dtype=np.int32)
+    for t in range(T):
+        a, b = [], []
+        for h in idx[t]:
+            if 0 <= h < R:
+                (a.append(int(rowmap[h])) if rowmap[h] >= 0 else b.append(int(h)))
+        hbm[t, :len(a)] = a
+        host[t, :len(b)] = b
+        hc[t], sc[t] = len(a), len(b)
+    return hbm, hc, host, sc

@@ -1,0 +1,33 @@
+"""Seeded input generators shared by the tests and bench.py (synthetic data with the shapes of BASELINE.json's
+configs). Nothing here computes a result: oracle/ does that."""
+import numpy as np
+import torch
+
+D_LAT, D_ROPE, D_QK, ROW = 512, 64, 576, 656
+
+
+def bf16_bits(x):
+    """float tensor -> numpy uint16 bf16 bit patterns (round to nearest even, torch's conversion)."""
+    return torch.as_tensor(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def make_pool_656(R, seed=1, scale=1.0, device=None):
+    """R Row656 rows from N(0, scale^2) latent / rope (bf16), packed by the oracle's writer. Returns
+    (pool uint8 numpy [R, 656], kv bits [R, 512], pe bits [R, 64])."""
+    from oracle import spmla_ref as ref
+    g = torch.Generator().manual_seed(seed)
+    kv = bf16_bits(torch.randn(R, D_LAT, generator=g) * scale)
+    pe = bf16_bits(torch.randn(R, D_ROPE, generator=g) * scale)
+    pool = np.zeros((R, ROW), dtype=np.uint8)
+    ref.cache_write_656(kv, pe, np.arange(R), pool)
+    return pool, kv, pe
+
+
+def make_q(T, H, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(T, H, D_QK, generator=g) * scale).to(torch.bfloat16)
+
+
+def distinct_idx(T, K, R, seed=2):
+    g = torch.Generator().manual_seed(seed)
+    return torch.stack([torch.randperm(R, generator=g)[:K] for _ in range(T)]).to(torch.int32)

@@ -1,0 +1,64 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point include/spmla.h declares, and rejects bad
+arguments with the documented codes before touching the GPU (no compute calls here)."""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    txt = open(os.path.join(ROOT, "include", "spmla.h")).read()
+    return sorted(set(re.findall(r"\b(spmla_\w+)\s*\(", txt)))
+
+
+def test_exports_every_declared_symbol():
+    from arcagi2_flashnext_dots3_amd import _lib
+    L = _lib.lib()
+    declared = _declared()
+    assert len(declared) >= 12
+    missing = [n for n in declared if not hasattr(L, n)]
+    assert not missing, missing
+    assert set(declared) <= set(_lib.SIGNATURES), "ctypes signatures must cover every declared entry point"
+
+
+def test_version():
+    from arcagi2_flashnext_dots3_amd import _lib
+    assert _lib.lib().spmla_version().startswith(b"spmla-gfx950")
+
+
+@pytest.mark.parametrize("call,code", [
+    (("spmla_attn_splitk", None, 0, 0, None, 0, None, 0, 0, None, -1, 1, 1.0, 1.0, 1, None, 0, 0, None, 0, None,
+      None, None), -2),
+    (("spmla_attn_splitk", None, 0, 0, None, 0, None, 0, 4096, None, 1, 1, 1.0, 1.0, 1, None, 0, 0, None, 0, None,
+      None, None), -2),
+    (("spmla_topk", None, 0, None, 1, 10, 5000, None, 0, None), -5),
+    (("spmla_topk", None, 0, None, 1, 10, 0, None, 0, None), -2),
+    (("spmla_gather", None, 0, 650, None, 1, None, 0, None), -2),
+    (("spmla_cache_write", None, 0, None, 0, None, 1, None, 10, 64, 0, 7, 1.0, None), -2),
+    (("spmla_index_logits", None, 0, 0, None, 0, None, 0, 64, 0, None, 0, 64, None, None, 1, 32, 128, 10, 1, 0, 0,
+      None, 0, None), -5),
+    (("spmla_lse_merge", None, 0, 0, 0, 0, None, 0, 0, 0, 1, 1, None, 0, 0, None, None, 0, None), -2),
+])
+def test_argument_rejection(call, code):
+    from arcagi2_flashnext_dots3_amd import _lib
+    assert getattr(_lib.lib(), call[0])(*call[1:]) == code
+
+
+def test_zero_sized_calls_are_noops():
+    from arcagi2_flashnext_dots3_amd import _lib
+    L = _lib.lib()
+    assert L.spmla_attn_splitk(None, 0, 0, None, 0, None, 0, 0, None, 0, 1, 1.0, 1.0, 1, None, 0, 0, None, 0,
+                               None, None, None) == 0
+    assert L.spmla_topk(None, 0, None, 0, 10, 16, None, 0, None) == 0
+    assert L.spmla_gather(None, 0, 656 - 656 % 16, None, 0, None, 0, None) == 0
+
+
+def test_product_package_does_not_import_oracle():
+    pkg = os.path.join(ROOT, "arcagi2_flashnext_dots3_amd")
+    for dp, _, fs in os.walk(pkg):
+        for f in fs:
+            if f.endswith(".py"):
+                txt = open(os.path.join(dp, f)).read()
+                assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", txt, re.M), f

@@ -1,0 +1,129 @@
+"""GPU parity of the indexer logits (tolerance vs the fp64 oracle, identical -inf pattern) and of the exact top-k
+(bit-exact indices vs the oracle on the same fp32 logits, lower index wins ties)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import spmla_ref as ref
+from tests.helpers import bf16_bits
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _keys(nb, bs, seed):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(nb * bs, 128, generator=g).to(torch.bfloat16)
+    store = np.zeros((nb * bs, 132), dtype=np.uint8)
+    ref.index_key_write(bf16_bits(k), np.arange(nb * bs), store)
+    return store
+
+
+@pytest.mark.parametrize("rows,L,seed", [(4, 2048, 0), (8, 5000, 1)])
+def test_index_logits(dev, rows, L, seed):
+    from arcagi2_flashnext_dots3_amd import kernels
+    bs = 64
+    nbp = (L + bs - 1) // bs
+    nb = rows * nbp + 3
+    store = _keys(nb, bs, seed + 10)
+    g = torch.Generator().manual_seed(seed)
+    bt = torch.randperm(nb, generator=g)[: rows * nbp].reshape(rows, nbp).to(torch.int32)
+    q = torch.randn(rows, 64, 128, generator=g).to(torch.bfloat16)
+    w = torch.rand(rows, 64, generator=g)
+    req = torch.arange(rows, dtype=torch.int32)
+    ctx = torch.randint(L // 2, L + 1, (rows,), generator=g).to(torch.int32)
+    ctx[0] = L
+    print(f"[logits] rows={rows} L={L}", flush=True)
+    out = kernels.index_logits(q.to(dev), w.to(dev), torch.from_numpy(store).to(dev).view(nb, bs, 132),
+                               bt.to(dev), bs, req.to(dev), ctx.to(dev), L)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    exp = ref.index_logits(q.float().numpy(), w.numpy(), store, bt.numpy(), bs, req.numpy(), ctx.numpy(), L)
+    assert np.array_equal(np.isinf(got), np.isinf(exp))
+    fin = np.isfinite(exp)
+    # bound: fp32 accumulation of 128-term dot products and of the 64-head weighted sum (bf16 MFMA, exact products)
+    err = np.abs(got[fin] - exp[fin]) / np.maximum(1.0, np.abs(exp[fin]))
+    print(f"[logits] max rel err {err.max():.3e}", flush=True)
+    assert err.max() <= 2e-5
+
+
+def _topk_check(dev, lg, ctx, K):
+    from arcagi2_flashnext_dots3_amd import kernels
+    out = kernels.topk(torch.from_numpy(lg).to(dev), torch.from_numpy(ctx).to(dev), K)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    exp = ref.topk(lg, ctx, K)
+    bad = np.where((got != exp).any(1))[0]
+    assert bad.size == 0, f"rows {bad[:8]} differ"
+
+
+def test_topk_random_and_lengths(dev):
+    g = np.random.default_rng(0)
+    rows, L = 16, 32768
+    lg = g.standard_normal((rows, L)).astype(np.float32)
+    ctx = g.integers(1, L + 1, rows).astype(np.int32)
+    ctx[0], ctx[1], ctx[2], ctx[3], ctx[4] = L, 0, 1, 2048, 2049
+    print("[topk] random", flush=True)
+    _topk_check(dev, lg, ctx, 2048)
+
+
+def test_topk_ties_and_specials(dev):
+    g = np.random.default_rng(1)
+    rows, L = 12, 9000
+    base = g.standard_normal((rows, L)).astype(np.float32)
+    lg = base.copy()
+    lg[0] = np.round(base[0] * 8) / 8                                  # ties quantized to 1/8
+    lg[1] = np.floor(np.abs(base[1]) * 3).clip(max=4)                  # 5 levels
+    lg[2] = np.where(base[2] > 0, 0.0, -0.0).astype(np.float32)        # signed zeros only
+    lg[3] = 1.0                                                        # all equal
+    lg[4, 100:900] = -np.inf                                           # -inf holes
+    lg[5, :] = -np.inf
+    lg[5, :10] = 3.0                                                   # fewer finite values than K
+    lg[6, 7] = np.nan                                                  # NaN is the largest
+    lg[7] = np.round(base[7] * 2) / 2
+    lg[8, ::3] = 60000.0                                               # clamped maxima
+    ctx = np.full(rows, L, dtype=np.int32)
+    ctx[9] = 2047
+    ctx[10] = 4000
+    print("[topk] ties", flush=True)
+    _topk_check(dev, lg, ctx, 2048)
+
+
+def test_topk_ctx_lengths_fixture(dev):
+    # context lengths from the reference's own fixture (runtime_dataset/ctx_lengths.json), clipped to L
+    with open(os.path.join(HERE, "golden", "ctx_lengths.json")) as f:
+        cl = json.load(f)["ctx"]
+    g = np.random.default_rng(2)
+    rows, L = 32, 131072
+    ctx = np.array([min(c, L) for c in g.choice(cl, rows)], dtype=np.int32)
+    lg = g.standard_normal((rows, L)).astype(np.float32)
+    print("[topk] fixture ctx", flush=True)
+    _topk_check(dev, lg, ctx, 2048)
+
+
+def test_logits_then_topk_end_to_end(dev):
+    """Indices bit-exact against the oracle's top-k of the GPU's own logits; against the fp64 oracle logits, the
+    selected sets agree wherever the gap at the k-th value exceeds the logits tolerance."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    rows, L, bs = 4, 8192, 64
+    nbp = L // bs
+    store = _keys(rows * nbp, bs, 30)
+    g = torch.Generator().manual_seed(31)
+    bt = torch.arange(rows * nbp, dtype=torch.int32).reshape(rows, nbp)
+    q = torch.randn(rows, 64, 128, generator=g).to(torch.bfloat16)
+    w = torch.rand(rows, 64, generator=g)
+    req = torch.arange(rows, dtype=torch.int32)
+    ctx = torch.full((rows,), L, dtype=torch.int32)
+    lg = kernels.index_logits(q.to(dev), w.to(dev), torch.from_numpy(store).to(dev).view(-1, bs, 132), bt.to(dev),
+                              bs, req.to(dev), ctx.to(dev), L)
+    sel = kernels.topk(lg, ctx.to(dev), 2048).cpu().numpy()
+    assert np.array_equal(sel, ref.topk(lg.cpu().numpy(), ctx.numpy(), 2048))
+    exp = ref.index_logits(q.float().numpy(), w.numpy(), store, bt.numpy(), bs, req.numpy(), ctx.numpy(), L)
+    for r in range(rows):
+        srt = np.sort(exp[r])[::-1]
+        gap = srt[2047] - srt[2048]
+        if gap > 1e-5 * max(1.0, abs(srt[2047])) * 4:
+            assert set(sel[r].tolist()) == set(np.argsort(-exp[r], kind="stable")[:2048].tolist())
