@@ -21,6 +21,8 @@ SIGNATURES = {
     "spmla_index_key_write": [P, LL, P, I, P, LL, I, I, I, LL, I, P],
     "spmla_index_logits": [P, LL, LL, P, LL, P, LL, I, LL, P, LL, I, P, P, I, I, I, I, I, I, I, P, LL, P],
     "spmla_topk": [P, LL, P, I, I, I, P, LL, P],
+    "spmla_topk_local": [P, LL, P, I, I, I, I, I, P, P],
+    "spmla_topk_merge": [P, I, I, I, I, I, P, LL, P],
     "spmla_rows_from_topk": [P, LL, P, P, LL, I, I, LL, I, I, P, LL, P, P],
     "spmla_gather": [P, LL, I, P, I, P, LL, P],
     "spmla_copy_rows": [P, LL, P, P, LL, P, I, I, P],

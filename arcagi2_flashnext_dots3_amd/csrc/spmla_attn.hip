@@ -122,7 +122,7 @@ struct Params {
   float kv_scale;
   uint16_t* out; long long o_st, o_sh;            // S == 1: bf16 out[t][h][512]
   float* lse; long long lse_st;                   // S == 1: lse[t][h]
-  float* opart; float* lsepart;                   // S > 1: opart[s][t][h][512], lsepart[s][t][h]
+  float* opart; float* lsepart;                   // fp32 partials: opart[s][t][h][512], lsepart[s][t][h]
 };
 
 // Copy instructions of one tile are spread over all waves: wave v issues j = v, v + NWAVES, ...
@@ -451,7 +451,7 @@ __global__ void __launch_bounds__(256 * TEAMS, 1) attn_kernel(Params p) {
   const float inv = lh > 0.f ? p.kv_scale / lh : 0.f;
   if (!hval) return;
   const float lse_v = lh > 0.f ? (mh + log2f(lh)) * 0.69314718055994531f : -__builtin_inff();
-  if (p.S == 1) {
+  if (p.opart == nullptr) {
     uint16_t* orow = p.out + (long long)t * p.o_st + (long long)h * p.o_sh;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -565,8 +565,8 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
   if (T < 0 || H <= 0 || K < 0 || S <= 0 || R < 0) return SPMLA_EARG;
   if (T == 0) return SPMLA_OK;
   if (!q || !idx || (R > 0 && !pool)) return SPMLA_EARG;
-  if (S == 1 && (!out || !lse)) return SPMLA_EARG;
-  if (S > 1 && (!opart || !lsepart)) return SPMLA_EARG;
+  const bool f32part = opart != nullptr;   // fp32 partials (any S) instead of the bf16 output (S == 1 only)
+  if (f32part ? !lsepart : (S != 1 || !out || !lse)) return SPMLA_EARG;
   if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7)) return SPMLA_EALIGN;
   if (out && (((uintptr_t)out & 7) || (o_st & 3) || (o_sh & 3))) return SPMLA_EALIGN;
   if (((K + S - 1) / S + attn::TR - 1) / attn::TR * attn::TR > attn::KMAX) return SPMLA_ELIMIT;
@@ -578,7 +578,7 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
   p.c = sm_scale * kv_scale * 1.4426950408889634f;
   p.kv_scale = kv_scale;
   p.out = (uint16_t*)out; p.o_st = o_st; p.o_sh = o_sh; p.lse = lse; p.lse_st = lse_st;
-  p.opart = opart; p.lsepart = lsepart;
+  p.opart = f32part ? opart : nullptr; p.lsepart = lsepart;
   const long long nwork = (long long)T * S * p.HGN;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);

@@ -143,12 +143,6 @@ __device__ inline uint32_t okey(float v) {
   return (x & 0x80000000u) ? ~x : (x | 0x80000000u);
 }
 
-struct TopkParams {
-  const float* lg; long long lg_st;
-  const int* ctx; int rows, Lc, K;
-  int* out; long long out_st;
-};
-
 // block-wide exclusive scan of a per-thread count (1024 threads = 16 waves)
 __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* wsum, uint32_t* total) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -194,140 +188,243 @@ __device__ inline void bitonic_desc(unsigned long long* a, int n) {
   }
 }
 
-__global__ void __launch_bounds__(TK_NT) topk_kernel(TopkParams p) {
-  __shared__ uint32_t hist[2048];
-  __shared__ unsigned long long sel[TK_KMAX];
-  __shared__ unsigned long long cand[TK_CAP];
-  __shared__ uint32_t wsum[17];
-  __shared__ uint32_t sh[8];
-  const int row = blockIdx.x, tid = threadIdx.x;
-  const float* x = p.lg + (long long)row * p.lg_st;
-  int n = p.ctx[row];
-  n = n < 0 ? 0 : (n > p.Lc ? p.Lc : n);
-  const int K = p.K;
-  int* o = p.out + (long long)row * p.out_st;
-  auto pack = [](uint32_t key, int j) { return ((unsigned long long)key << 32) | (uint32_t)(~(uint32_t)j); };
+// Candidate sources of one row. n = number of candidates; val(j) = the value of candidate j; id(j) = what the
+// output reports for it. Ties on the key go to the lower candidate number j.
+struct RowSrc {     // a logits row: candidate j = column j
+  const float* x; int n;
+  __device__ float val(int j) const { return x[j]; }
+  __device__ int id(int j) const { return j; }
+};
+struct MergeSrc {   // all-gathered payloads [P][nrows][2 * kl] = [values | positions]: candidate c = (c / kl, c % kl)
+  const float* allp; long long nrows; int row, kl, n;
+  __device__ const float* seg(int c, int& i) const {
+    const int r = c / kl;
+    i = c - r * kl;
+    return allp + ((long long)r * nrows + row) * 2 * kl;
+  }
+  __device__ float val(int c) const { int i; const float* b = seg(c, i); return b[i]; }
+  __device__ int id(int c) const { int i; const float* b = seg(c, i); return (int)f2u(b[kl + i]); }
+};
 
-  int nsel = 0;   // entries of sel filled (block-uniform)
+struct TopkLds {
+  uint32_t hist[2048];
+  unsigned long long sel[TK_KMAX];
+  unsigned long long cand[TK_CAP];
+  uint32_t wsum[17];
+  uint32_t sh[8];
+};
+
+__device__ inline unsigned long long tk_pack(uint32_t key, int j) {
+  return ((unsigned long long)key << 32) | (uint32_t)(~(uint32_t)j);
+}
+
+// Selects the K largest candidates (key desc, j asc) of src into L.sel (unordered); returns their number min(n, K).
+template <class Src>
+__device__ int tk_select(const Src& src, int K, TopkLds& L) {
+  const int tid = threadIdx.x, n = src.n;
+  uint32_t* hist = L.hist;
+  unsigned long long* sel = L.sel;
+  unsigned long long* cand = L.cand;
+  uint32_t* sh = L.sh;
   if (n <= K) {
-    for (int j = tid; j < n; j += TK_NT) sel[j] = pack(okey(x[j]), j);
-    nsel = n;
-  } else {
-    if (tid == 0) sh[0] = 0;   // sel fill counter
-    uint32_t prefix = 0, mask = 0;
-    uint32_t need = (uint32_t)K;
-    bool done = false;
-    for (int pass = 0; pass < 3 && !done; ++pass) {
-      const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-      const uint32_t dm = pass == 2 ? 0x3ffu : 0x7ffu;
-      for (int i = tid; i < 2048; i += TK_NT) hist[i] = 0;
+    for (int j = tid; j < n; j += TK_NT) sel[j] = tk_pack(okey(src.val(j)), j);
+    __syncthreads();
+    return n;
+  }
+  if (tid == 0) sh[0] = 0;   // sel fill counter
+  uint32_t prefix = 0, mask = 0;
+  uint32_t need = (uint32_t)K;
+  bool done = false;
+  for (int pass = 0; pass < 3 && !done; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t dm = pass == 2 ? 0x3ffu : 0x7ffu;
+    for (int i = tid; i < 2048; i += TK_NT) hist[i] = 0;
+    __syncthreads();
+    for (int j = tid; j < n; j += TK_NT) {
+      const uint32_t k = okey(src.val(j));
+      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & dm], 1u);
+    }
+    __syncthreads();
+    // thread t owns the two bins 2047 - 2t, 2046 - 2t (descending); suffix counts by a block scan
+    const int b0 = 2047 - 2 * tid, b1 = b0 - 1;
+    const uint32_t h0 = hist[b0], h1 = hist[b1];
+    uint32_t tot;
+    const uint32_t before = block_excl_scan(h0 + h1, L.wsum, &tot);
+    if (before < need && before + h0 >= need) { sh[1] = (uint32_t)b0; sh[2] = before; sh[3] = h0; }
+    if (before + h0 < need && before + h0 + h1 >= need) { sh[1] = (uint32_t)b1; sh[2] = before + h0; sh[3] = h1; }
+    __syncthreads();
+    const uint32_t b = sh[1], above = sh[2], binc = sh[3];
+    const uint32_t pmask = mask, pprefix = prefix;
+    const uint32_t np = prefix | (b << shift), nm = mask | (dm << shift);
+    // elements under the current prefix whose digit is above b are selected
+    const bool whole = above + binc == need;
+    const bool fits = binc <= TK_CAP;
+    const bool last = pass == 2;
+    if (whole || fits || last) {
+      if (tid == 0) sh[4] = 0;   // cand counter
       __syncthreads();
       for (int j = tid; j < n; j += TK_NT) {
-        const uint32_t k = okey(x[j]);
-        if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & dm], 1u);
+        const uint32_t k = okey(src.val(j));
+        if ((k & pmask) != pprefix) continue;
+        const uint32_t d = (k >> shift) & dm;
+        if (d > b || (whole && d == b)) {
+          const uint32_t s = atomicAdd(&sh[0], 1u);
+          sel[s] = tk_pack(k, j);
+        } else if (d == b && fits && !whole) {
+          const uint32_t s = atomicAdd(&sh[4], 1u);
+          cand[s] = tk_pack(k, j);
+        }
       }
       __syncthreads();
-      // thread t owns the two bins 2047 - 2t, 2046 - 2t (descending); suffix counts by a block scan
-      const int b0 = 2047 - 2 * tid, b1 = b0 - 1;
-      const uint32_t h0 = hist[b0], h1 = hist[b1];
-      uint32_t tot;
-      const uint32_t before = block_excl_scan(h0 + h1, wsum, &tot);
-      if (before < need && before + h0 >= need) { sh[1] = (uint32_t)b0; sh[2] = before; sh[3] = h0; }
-      if (before + h0 < need && before + h0 + h1 >= need) { sh[1] = (uint32_t)b1; sh[2] = before + h0; sh[3] = h1; }
-      __syncthreads();
-      const uint32_t b = sh[1], above = sh[2], binc = sh[3];
-      const uint32_t pmask = mask, pprefix = prefix;
-      const uint32_t np = prefix | (b << shift), nm = mask | (dm << shift);
-      // elements under the current prefix whose digit is above b are selected
-      const bool whole = above + binc == need;
-      const bool fits = binc <= TK_CAP;
-      const bool last = pass == 2;
-      if (whole || fits || last) {
-        if (tid == 0) sh[4] = 0;   // cand counter
+      if (whole) {
+        done = true;
+      } else if (fits) {
+        // resolve inside the boundary bin: sort candidates, keep the first need - above
+        const int nc = (int)sh[4];
+        int np2 = 1;
+        while (np2 < nc) np2 <<= 1;
+        for (int i = nc + tid; i < np2; i += TK_NT) cand[i] = 0ull;
         __syncthreads();
-        for (int j = tid; j < n; j += TK_NT) {
-          const uint32_t k = okey(x[j]);
-          if ((k & pmask) != pprefix) continue;
-          const uint32_t d = (k >> shift) & dm;
-          if (d > b || (whole && d == b)) {
-            const uint32_t s = atomicAdd(&sh[0], 1u);
-            sel[s] = pack(k, j);
-          } else if (d == b && fits && !whole) {
-            const uint32_t s = atomicAdd(&sh[4], 1u);
-            cand[s] = pack(k, j);
-          }
-        }
+        bitonic_desc(cand, np2);
+        const uint32_t take = need - above;
+        const uint32_t base = sh[0];
+        for (uint32_t i = tid; i < take; i += TK_NT) sel[base + i] = cand[i];
         __syncthreads();
-        if (whole) {
-          done = true;
-        } else if (fits) {
-          // resolve inside the boundary bin: sort candidates, keep the first need - above
-          int nc = (int)sh[4];
-          int np2 = 1;
-          while (np2 < nc) np2 <<= 1;
-          for (int i = nc + tid; i < np2; i += TK_NT) cand[i] = 0ull;
-          __syncthreads();
-          bitonic_desc(cand, np2);
-          const uint32_t take = need - above;
-          const uint32_t base = sh[0];
-          for (uint32_t i = tid; i < take; i += TK_NT) sel[base + i] = cand[i];
-          __syncthreads();
-          if (tid == 0) sh[0] = base + take;
-          done = true;
-        } else {
-          // last pass, boundary key fully known: take the lowest columns equal to it (ordered scan)
-          const uint32_t T = np;
-          const uint32_t take = need - above;
-          uint32_t got = 0;
-          const uint32_t base = sh[0];
-          __syncthreads();
-          for (int j0 = 0; j0 < n && got < take; j0 += TK_NT) {
-            const int j = j0 + tid;
-            const bool eq = j < n && okey(x[j]) == T;
-            uint32_t tot2;
-            const uint32_t r = block_excl_scan(eq ? 1u : 0u, wsum, &tot2);
-            if (eq && got + r < take) sel[base + got + r] = pack(T, j);
-            got += tot2;
-          }
-          __syncthreads();
-          if (tid == 0) sh[0] = base + take;
-          done = true;
-        }
+        if (tid == 0) sh[0] = base + take;
+        done = true;
       } else {
-        // narrow: everything above the bin is selected now, continue inside the bin
-        for (int j = tid; j < n; j += TK_NT) {
-          const uint32_t k = okey(x[j]);
-          if ((k & pmask) != pprefix) continue;
-          if (((k >> shift) & dm) > b) {
-            const uint32_t s = atomicAdd(&sh[0], 1u);
-            sel[s] = pack(k, j);
-          }
+        // last pass, boundary key fully known: take the lowest candidates equal to it (ordered scan)
+        const uint32_t T = np;
+        const uint32_t take = need - above;
+        uint32_t got = 0;
+        const uint32_t base = sh[0];
+        __syncthreads();
+        for (int j0 = 0; j0 < n && got < take; j0 += TK_NT) {
+          const int j = j0 + tid;
+          const bool eq = j < n && okey(src.val(j)) == T;
+          uint32_t tot2;
+          const uint32_t r = block_excl_scan(eq ? 1u : 0u, L.wsum, &tot2);
+          if (eq && got + r < take) sel[base + got + r] = tk_pack(T, j);
+          got += tot2;
         }
-        prefix = np;
-        mask = nm;
-        need -= above;
+        __syncthreads();
+        if (tid == 0) sh[0] = base + take;
+        done = true;
       }
-      __syncthreads();
+    } else {
+      // narrow: everything above the bin is selected now, continue inside the bin
+      for (int j = tid; j < n; j += TK_NT) {
+        const uint32_t k = okey(src.val(j));
+        if ((k & pmask) != pprefix) continue;
+        if (((k >> shift) & dm) > b) {
+          const uint32_t s = atomicAdd(&sh[0], 1u);
+          sel[s] = tk_pack(k, j);
+        }
+      }
+      prefix = np;
+      mask = nm;
+      need -= above;
     }
-    nsel = K;
+    __syncthreads();
   }
-  // sort the selection (descending key, ascending column), pad to a power of two with the smallest entry
+  return K;
+}
+
+// Sorts the nsel selected entries by (key desc, j asc) and writes src.id of the first kout slots to o
+// (-1 where the value is +-inf and for slots >= nsel).
+template <class Src>
+__device__ void tk_emit_sorted(const Src& src, int nsel, int kout, int* o, TopkLds& L) {
+  const int tid = threadIdx.x;
   int np2 = 1;
   while (np2 < nsel) np2 <<= 1;
-  for (int i = nsel + tid; i < np2; i += TK_NT) sel[i] = 0ull;
+  for (int i = nsel + tid; i < np2; i += TK_NT) L.sel[i] = 0ull;
   __syncthreads();
-  if (np2 > 1) bitonic_desc(sel, np2);
-  for (int s = tid; s < K; s += TK_NT) {
+  if (np2 > 1) bitonic_desc(L.sel, np2);
+  for (int s = tid; s < kout; s += TK_NT) {
     int r = -1;
     if (s < nsel) {
-      const unsigned long long e = sel[s];
+      const unsigned long long e = L.sel[s];
       const uint32_t key = (uint32_t)(e >> 32);
       const int j = (int)(~(uint32_t)e);
       const bool isinf = key == 0xff800000u || key == 0x007fffffu;   // +inf / -inf keys
-      if (!isinf) r = j;
+      if (!isinf) r = src.id(j);
     }
     o[s] = r;
   }
+}
+
+struct TopkParams {
+  const float* lg; long long lg_st;
+  const int* ctx; int rows, Lc, K;
+  int* out; long long out_st;
+};
+
+__global__ void __launch_bounds__(TK_NT) topk_kernel(TopkParams p) {
+  __shared__ TopkLds L;
+  const int row = blockIdx.x;
+  int n = p.ctx[row];
+  n = n < 0 ? 0 : (n > p.Lc ? p.Lc : n);
+  const RowSrc src{p.lg + (long long)row * p.lg_st, n};
+  const int nsel = tk_select(src, p.K, L);
+  tk_emit_sorted(src, nsel, p.K, p.out + (long long)row * p.out_st, L);
+}
+
+// fast_topk.local (dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:52-66, csrc/topk_select.cu:1-13, :75-201):
+// the row's valid columns are j < ceil((ctx - rank) / P) (clipped to Lc); the top kl of them go to the payload
+// pk[row] = [values fp32 | positions j * P + rank as int32 bits] in ascending column order; fewer than kl valid
+// columns: the rest is padded with -inf values and positions s * P + rank.
+struct LocalParams {
+  const float* lg; long long lg_st;
+  const int* ctx; int rows, rank, P, Lc, kl;
+  float* pk;
+};
+
+__global__ void __launch_bounds__(TK_NT) topk_local_kernel(LocalParams p) {
+  __shared__ TopkLds L;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const int c = p.ctx[row];
+  int n = c > p.rank ? (int)(((long long)c - p.rank + p.P - 1) / p.P) : 0;
+  if (n > p.Lc) n = p.Lc;
+  const RowSrc src{p.lg + (long long)row * p.lg_st, n};
+  const int nsel = tk_select(src, p.kl, L);
+  // ascending column order: sort descending on ~j
+  int np2 = 1;
+  while (np2 < nsel) np2 <<= 1;
+  for (int i = tid; i < np2; i += TK_NT) {
+    unsigned long long e = 0ull;
+    if (i < nsel) e = (unsigned long long)(uint32_t)L.sel[i] << 32;   // low word of a selected entry is ~j
+    L.sel[i] = e;
+  }
+  __syncthreads();
+  if (np2 > 1) bitonic_desc(L.sel, np2);
+  float* pv = p.pk + (long long)row * 2 * p.kl;
+  int* pp = reinterpret_cast<int*>(pv + p.kl);
+  for (int s = tid; s < p.kl; s += TK_NT) {
+    if (s < nsel) {
+      const int j = (int)(~(uint32_t)(L.sel[s] >> 32));
+      pv[s] = src.val(j);
+      pp[s] = j * p.P + p.rank;
+    } else {
+      pv[s] = u2f(0xff800000u);
+      pp[s] = s * p.P + p.rank;
+    }
+  }
+}
+
+// fast_topk.merge (dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:69-78, csrc/topk_select.cu:203-244): per row,
+// the top kk of the P * kl all-gathered candidates by (value key desc, concatenation index asc) -> their positions,
+// -1 where the value is +-inf, slots [kk, topk_tokens) = -1.
+struct MergeParams {
+  const float* allp; int n, P, kl, kk, topk_tokens;
+  int* out; long long out_st;
+};
+
+__global__ void __launch_bounds__(TK_NT) topk_merge_kernel(MergeParams p) {
+  __shared__ TopkLds L;
+  const int row = blockIdx.x;
+  const MergeSrc src{p.allp, p.n, row, p.kl, p.P * p.kl};
+  const int nsel = tk_select(src, p.kk, L);
+  tk_emit_sorted(src, nsel, p.topk_tokens, p.out + (long long)row * p.out_st, L);
 }
 
 // ------------------------------------------------------------------------------------------------ rows
@@ -396,6 +493,30 @@ int spmla_topk(const float* logits, long long lg_st, const int* ctx, int rows, i
   idx::TopkParams p;
   p.lg = logits; p.lg_st = lg_st; p.ctx = ctx; p.rows = rows; p.Lc = Lc; p.K = K; p.out = out; p.out_st = out_st;
   hipLaunchKernelGGL(idx::topk_kernel, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}
+
+int spmla_topk_local(const float* logits, long long lg_st, const int* ctx, int rows, int rank, int P, int Lc, int kl,
+                     float* pk, void* stream) {
+  if (rows < 0 || Lc < 0 || kl <= 0 || P <= 0 || rank < 0 || rank >= P) return SPMLA_EARG;
+  if (kl > idx::TK_KMAX) return SPMLA_ELIMIT;
+  if (rows == 0) return SPMLA_OK;
+  if (!logits || !ctx || !pk) return SPMLA_EARG;
+  idx::LocalParams p;
+  p.lg = logits; p.lg_st = lg_st; p.ctx = ctx; p.rows = rows; p.rank = rank; p.P = P; p.Lc = Lc; p.kl = kl; p.pk = pk;
+  hipLaunchKernelGGL(idx::topk_local_kernel, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}
+
+int spmla_topk_merge(const float* allp, int n, int P, int kl, int kk, int topk_tokens, int* out, long long out_st,
+                     void* stream) {
+  if (n < 0 || P <= 0 || kl <= 0 || kk < 0 || kk > P * kl || topk_tokens < kk) return SPMLA_EARG;
+  if (kk > idx::TK_KMAX) return SPMLA_ELIMIT;
+  if (n == 0 || topk_tokens == 0) return SPMLA_OK;
+  if (!allp || !out) return SPMLA_EARG;
+  idx::MergeParams p;
+  p.allp = allp; p.n = n; p.P = P; p.kl = kl; p.kk = kk; p.topk_tokens = topk_tokens; p.out = out; p.out_st = out_st;
+  hipLaunchKernelGGL(idx::topk_merge_kernel, dim3(n), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 

@@ -98,6 +98,29 @@ def topk(logits, ctx, K, out=None):
     return out
 
 
+def topk_local(lg, ctx, rank, P, kl, pk=None):
+    """fast_topk.local: lg [rows, Lc] fp32 (column j = position j * P + rank), ctx [rows] int32 positions ->
+    pk [rows, 2 * kl] fp32 = [top-kl values | their positions as int32 bits], ascending column order, -inf padded."""
+    rows, Lc = lg.shape
+    _need(lg.dtype == torch.float32 and lg.stride(1) == 1, "fp32 logits with contiguous rows")
+    _need(ctx.dtype == torch.int32 and ctx.is_contiguous(), "ctx int32")
+    if pk is None:
+        pk = torch.empty(rows, 2 * kl, dtype=torch.float32, device=lg.device)
+    _need(pk.dtype == torch.float32 and pk.is_contiguous() and pk.shape[-1] == 2 * kl, "pk [rows, 2 * kl] fp32")
+    _lib.call("spmla_topk_local", lg.data_ptr(), lg.stride(0), ctx.data_ptr(), rows, rank, P, Lc, kl, pk.data_ptr(),
+              _stream(lg))
+    return pk
+
+
+def topk_merge(allp, n, P, kl, kk, out):
+    """fast_topk.merge: allp [P * n, 2 * kl] rank-major payloads -> out [n, topk_tokens] int32 positions."""
+    _need(allp.dtype == torch.float32 and allp.is_contiguous(), "allp fp32 contiguous")
+    _need(out.dtype == torch.int32 and out.stride(1) == 1, "out int32 with contiguous rows")
+    _lib.call("spmla_topk_merge", allp.data_ptr(), n, P, kl, kk, out.shape[1], out.data_ptr(), out.stride(0),
+              _stream(allp))
+    return out
+
+
 def rows_from_topk(topk_pos, req, block_table, block_size, stride_rows=None, rows=None, counts=None):
     """Request-local positions [T, K] -> global rows [T, K] int32 (vLLM triton_convert_req_index_to_global_index)."""
     T, K = topk_pos.shape
@@ -191,6 +214,25 @@ def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=1, kc
               opart.data_ptr(), lpart.data_ptr(), st)
     lse_merge(opart, lpart, out=out, lse=lse)
     return out, lse
+
+
+def attend_partial(q, pool, idx, sm_scale, kv_scale=1.0, opart=None, lpart=None, split=1, kcount=None, R=None):
+    """Like attend, but the result stays as `split` normalized fp32 partials (opart [split, T, H, 512], lpart
+    [split, T, H]) for a later lse_merge (tier partials use split = 1)."""
+    T, H, _ = q.shape
+    K = idx.shape[1]
+    _need(attention_ok(q, idx), "attend_partial: q must be bf16 [T, H, 576] with 16-byte aligned rows, idx int32")
+    if opart is None:
+        opart = torch.empty(split, T, H, D_LAT, dtype=torch.float32, device=q.device)
+    if lpart is None:
+        lpart = torch.empty(split, T, H, dtype=torch.float32, device=q.device)
+    _need(opart.is_contiguous() and lpart.is_contiguous() and opart.shape[:3] == (split, T, H), "partials layout")
+    Rv = int(R if R is not None else pool.shape[0])
+    pptr = pool.data_ptr() if torch.is_tensor(pool) else int(pool)
+    _lib.call("spmla_attn_splitk", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(), idx.stride(0),
+              K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), split, None, 0, 0, None, 0,
+              opart.data_ptr(), lpart.data_ptr(), _stream(q))
+    return opart, lpart
 
 
 def lse_merge(parts, lses, out=None, out_f32=None, lse=None):

@@ -1,0 +1,150 @@
+"""Host-offloaded sparse-MLA KV rows for one DSA layer: the LayerOffload interface of the reference
+(dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:1051-1648) on libspmla_gfx950.so.
+
+Tiers
+  host pool   [R, 656] uint8 Row656 rows in pinned host memory (torch's pinned allocator = hipHostMalloc; the kernels
+              read and write it through its device-visible address, 16-byte accesses over PCIe). This replaces the
+              reference's cudaHostRegister'ed buffer (_HostReg, sparse_offload.py:917-980).
+  HBM cache   [C, 656] uint8 hot rows with tag[line] = host row and rowmap[row] = line (-1 = host only). The hot set
+              is chosen by the caller (set_hot_rows, e.g. hot_rows_by_frequency over recent selections); the
+              reference's dynamic W-way cache (offload_fill.py) is not part of this build.
+
+Decode (attend): the selected host rows of each token are split by tier (spmla_tier_split: cache hits -> lines,
+misses -> host rows, both compacted in order); the HBM tier is attended in place; the host tier's rows are first
+copied over PCIe into an HBM staging area (spmla_gather, the reference's miss fill) and attended there; the two fp32
+partials (o, lse) are merged exactly by spmla_lse_merge. Without a cache (C = 0) every row takes the host tier.
+"""
+import torch
+
+from . import kernels
+
+ROW = kernels.ROW656
+
+
+def hot_rows_by_frequency(counts, C):
+    """Rows to keep in an HBM cache of C lines: the C most frequently selected rows (counts [R] int64 selection
+    counts), equal counts -> lower row id first; rows never selected are not taken."""
+    C = min(int(C), counts.shape[0])
+    order = torch.sort(-counts.to(torch.int64), stable=True).indices[:C]
+    return order[counts[order] > 0]
+
+
+class LayerOffload:
+    """One DSA layer's offloaded KV rows (reference LayerOffload, sparse_offload.py:1051).
+
+    num_host_rows: R, the number of cache slots (every slot id written by store() is a host row id);
+    device: the GPU; key: the layer's cache prefix (identification only); cache_rows: C lines of HBM hot-row cache.
+    """
+
+    def __init__(self, num_host_rows, device, key=None, cache_rows=0):
+        self.R = int(num_host_rows)
+        self.device = torch.device(device)
+        self.key = key
+        self.host = torch.zeros((self.R, ROW), dtype=torch.uint8, pin_memory=True)
+        self.C = min(int(cache_rows), self.R)
+        self.cache = torch.zeros((max(self.C, 1), ROW), dtype=torch.uint8, device=self.device)
+        self.tag = torch.full((max(self.C, 1),), -1, dtype=torch.int64, device=self.device)
+        self.rowmap = torch.full((max(self.R, 1),), -1, dtype=torch.int32, device=self.device)
+        self._ws = {}
+
+    # ------------------------------------------------------------------------------------------------ rows in
+    def store(self, kv_c_normed, k_pe, slots, kv_scale=1.0):
+        """Quantize-and-pack n tokens (kv_c_normed [n, 512] bf16, k_pe [n, 64] / [n, 1, 64] bf16) into host rows
+        `slots` [n] int64 (reference LayerOffload.store, sparse_offload.py:1131-1155). Rows are Row656 (per-128
+        scales of their own); kv_scale is accepted for the reference's signature and must be 1. Cached copies of the
+        written rows are rewritten in HBM too (write-through), so both tiers hold identical bytes."""
+        n = min(kv_c_normed.shape[0], slots.shape[0])
+        if n == 0:
+            return
+        if float(kv_scale) != 1.0:
+            raise ValueError("LayerOffload.store: Row656 rows carry their own scales; kv_scale must be 1")
+        kpe = k_pe.reshape(k_pe.shape[0], -1)
+        slots = slots[:n].to(torch.int64)
+        kernels.cache_write(kv_c_normed[:n], kpe[:n], slots, self.host)
+        if self.C:
+            ok = (slots >= 0) & (slots < self.R)
+            lines = torch.where(ok, self.rowmap[slots.clamp(0, self.R - 1)].to(torch.int64), -1)
+            kernels.cache_write(kv_c_normed[:n], kpe[:n], lines, self.cache[:self.C])
+
+    def gather(self, rows, out):
+        """out[i] = host row rows[i] (int64; zero row when outside [0, R)); out [N, 656] uint8 in HBM
+        (reference LayerOffload.gather, sparse_offload.py:1157-1163)."""
+        if rows.shape[0]:
+            kernels.gather(self.host, rows.to(torch.int64), out)
+        return out
+
+    def set_hot_rows(self, rows):
+        """Make `rows` (distinct host rows, at most C) the HBM-resident set: line i holds rows[i]."""
+        rows = rows.to(device=self.device, dtype=torch.int64).reshape(-1)
+        if rows.numel() > self.C:
+            raise ValueError(f"set_hot_rows: {rows.numel()} rows > {self.C} cache lines")
+        old = self.tag[self.tag >= 0]
+        if old.numel():
+            self.rowmap[old] = -1
+        self.tag.fill_(-1)
+        m = rows.numel()
+        if m:
+            lines = torch.arange(m, dtype=torch.int64, device=self.device)
+            kernels.copy_rows(self.host, rows, self.cache[:self.C], lines)
+            self.tag[:m] = rows
+            self.rowmap[rows] = lines.to(torch.int32)
+
+    # ------------------------------------------------------------------------------------------------ attention
+    def _buf(self, name, shape, dtype):
+        b = self._ws.get(name)
+        n = 1
+        for s in shape:
+            n *= s
+        if b is None or b.numel() < n or b.dtype != dtype:
+            b = torch.empty(max(n, 1), dtype=dtype, device=self.device)
+            self._ws[name] = b
+        return b[:n].view(shape)
+
+    def attend(self, q, idx, sm_scale, kv_scale=1.0, num_heads=None, ql=1, mkey=None, slots=None, out=None,
+               lse=None, return_lse=False):
+        """q [T, H, 576] bf16, idx [T, K] int32 host rows (-1 / out of range = none) -> out [T, H, 512] bf16
+        (reference LayerOffload.attend, sparse_offload.py:1350). return_lse: also the fp32 LSE [T, H]
+        (ln sum exp of the scaled scores; -inf for a token without rows). ql / mkey / slots are accepted for the
+        reference's signature (request packing and prefetch hints) and do not change the result."""
+        T, H, _ = q.shape
+        K = idx.shape[1]
+        num_heads = H if num_heads is None else num_heads
+        if out is None or out.shape != (T, H, kernels.D_LAT) or out.dtype != torch.bfloat16:
+            out = torch.empty((T, H, kernels.D_LAT), dtype=torch.bfloat16, device=q.device)
+        if lse is None:
+            lse = torch.empty((T, H), dtype=torch.float32, device=q.device)
+        if T == 0:
+            return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+        idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
+        hbm = self._buf("hbm", (T, K), torch.int32)
+        host = self._buf("host", (T, K), torch.int32)
+        hcnt = self._buf("hcnt", (T,), torch.int32)
+        mcnt = self._buf("mcnt", (T,), torch.int32)
+        if self.C:
+            kernels.tier_split(idx, self.rowmap, self.R, hbm, hcnt, host, mcnt)
+        else:
+            host = idx
+            mcnt = None
+        # host tier: copy the missed rows over PCIe into HBM staging, then attend there
+        staged = self._buf("staged", (T * K, ROW), torch.uint8)
+        kernels.gather(self.host, host.reshape(-1).to(torch.int64), staged)
+        sidx = self._buf("sidx", (T, K), torch.int32)
+        ar = torch.arange(T * K, dtype=torch.int32, device=q.device).view(T, K)
+        torch.where((host >= 0) & (host < self.R), ar, torch.full_like(ar, -1), out=sidx)
+        if not self.C:
+            kernels.attend(q, staged, sidx, sm_scale, kv_scale, out=out, lse=lse)
+            return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+        op = self._buf("opart", (2, T, H, kernels.D_LAT), torch.float32)
+        lp = self._buf("lpart", (2, T, H), torch.float32)
+        kernels.attend_partial(q, self.cache[:self.C], hbm, sm_scale, kv_scale, op[0:1], lp[0:1], kcount=hcnt)
+        kernels.attend_partial(q, staged, sidx, sm_scale, kv_scale, op[1:2], lp[1:2], kcount=mcnt)
+        kernels.lse_merge(op, lp, out=out, lse=lse)
+        return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+
+    def hit_rate(self, idx):
+        """Fraction of the valid selected rows of idx [T, K] that the HBM cache holds."""
+        v = (idx >= 0) & (idx < self.R)
+        if not self.C or not bool(v.any()):
+            return 0.0
+        hit = self.rowmap[idx.clamp(0, self.R - 1).long()] >= 0
+        return float((hit & v).sum()) / float(v.sum())

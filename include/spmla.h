@@ -60,6 +60,23 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
 int spmla_topk(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
                long long out_st, void* stream);
 
+/* fast_topk.local at rank `rank` of P: the row's valid columns are j < ceil((ctx[row] - rank) / P) (clipped to Lc);
+ * the top kl of them by the same key and tie rule as spmla_topk go to pk[row] = [kl values fp32 | kl positions
+ * j * P + rank as int32 bits] (pk row stride 2 * kl floats) in ascending column order; rows with fewer than kl valid
+ * columns are padded with -inf values at positions s * P + rank. kl <= 2048.
+ * Replaces topk_local_launch (dotsnote/engine/arcstats_pkg/arcstats/csrc/topk_select.cu:251-270, binding
+ * fast_topk.py:52-66). */
+int spmla_topk_local(const float* logits, long long lg_st, const int* ctx, int rows, int rank, int P, int Lc, int kl,
+                     float* pk, void* stream);
+
+/* fast_topk.merge: allp [P][n][2 * kl] all-gathered local payloads (rank-major) -> out[row][0..kk) = positions of the
+ * top kk of the P * kl candidates, ordered by (value desc, concatenation index asc), -1 where the value is +-inf;
+ * out[row][kk..topk_tokens) = -1. kk <= min(P * kl, 2048).
+ * Replaces topk_merge_launch (dotsnote/engine/arcstats_pkg/arcstats/csrc/topk_select.cu:272-286, binding
+ * fast_topk.py:69-78). */
+int spmla_topk_merge(const float* allp, int n, int P, int kl, int kk, int topk_tokens, int* out, long long out_st,
+                     void* stream);
+
 /* Request-local top-k positions -> global cache rows: rows[t][k] = block_table[req[t]][p / block_size] * stride_rows
  * + p % block_size for p = topk[t][k] >= 0 inside the table, else -1; counts[t] (optional) = valid entries.
  * Replaces vLLM's triton_convert_req_index_to_global_index (call sites dotsnote/engine/arcstats_pkg/arcstats/
@@ -97,9 +114,10 @@ int spmla_compact_stage(const long long* rows, int tot, const int* sidx, long lo
  * idx [T][K] int32 rows of the pool (invalid = outside [0, R)), kcount (optional) [T]: only the first kcount[t]
  * entries are read. s = sm_scale * kv_scale * q . row; o = kv_scale * softmax(s) V_latent; lse = ln sum exp(s)
  * (-inf and o = 0 for a token with no valid entry).
- * S == 1: out [T][H][512] bf16 (strides o_st, o_sh), lse [T][H] fp32 (stride lse_st).
- * S > 1: the K entries are cut into S splits; opart [S][T][H][512] fp32 (normalized) and lsepart [S][T][H] receive
- * per-split partials for spmla_lse_merge. ceil(ceil(K / S) / 32) * 32 <= 2048.
+ * opart == NULL (S == 1): out [T][H][512] bf16 (strides o_st, o_sh), lse [T][H] fp32 (stride lse_st).
+ * opart != NULL (required for S > 1): the K entries are cut into S splits; opart [S][T][H][512] fp32 (normalized)
+ * and lsepart [S][T][H] receive per-split partials for spmla_lse_merge (S = 1: one fp32 partial, e.g. per tier);
+ * out / lse are not written then. ceil(ceil(K / S) / 32) * 32 <= 2048.
  * Replaces LayerOffload.attend's decode kernels (oa2_v2_launch dotsnote/engine/arcstats_pkg/arcstats/csrc/
  * offload_attn2.cu:2021-2104, offload_split_launch csrc/offload_attn.cu:1155-1200, _sparse_mla_offload_split_kernel
  * sparse_offload.py:419-516) and triton_bf16_mla_sparse_interface (vllm_patch/.../ops/xpu_mla_sparse.py:182-278),

@@ -29,6 +29,8 @@ PINS = {
     "lse_merge": "merge of disjoint splits == single-pass attention (exact math), single part == identity",
     "index_logits": "python triple loop on tiny cases; linearity in w; block-table indirection vs a flat store",
     "topk": "torch.topk value sets; python sorted() with the (value desc, index asc) key on tiny / tie-heavy rows",
+    "topk_local": "brute force python sort on tiny rows; at P = 1 the local + merge pair equals topk",
+    "topk_merge": "python sorted() over concatenated candidates; merge(local(x)) == topk(x) at P = 1",
     "rows_from_topk": "python loop over the block table",
     "compact_stage": "torch.unique(sorted=True, return_inverse=True) (library)",
     "gather": "numpy fancy indexing",
@@ -285,6 +287,42 @@ def topk(logits, ctx, K):
         vals = logits[r, order]
         sel = np.where(np.isinf(vals), -1, order).astype(np.int32)
         out[r, :sel.size] = sel
+    return out
+
+
+def topk_local(logits, ctx, rank, P, kl):
+    """fast_topk.local (dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:52-66; csrc/topk_select.cu:1-13, :75-201):
+    valid columns j < ceil((ctx - rank) / P) clipped to Lc; the top kl (key okey desc, lower column first) in
+    ascending column order -> pk [rows, 2 kl] float32 = [values | positions j * P + rank (int32 bits)]; short rows
+    padded with -inf at positions s * P + rank."""
+    logits = np.asarray(logits, dtype=np.float32)
+    rows, Lc = logits.shape
+    pk = np.zeros((rows, 2 * kl), dtype=np.float32)
+    pos = pk[:, kl:].view(np.int32)
+    for r in range(rows):
+        c = int(ctx[r])
+        n = min(Lc, (c - rank + P - 1) // P) if c > rank else 0
+        kv = okey(logits[r, :n]).astype(np.int64)
+        chosen = np.sort(np.lexsort((np.arange(n), -kv))[:kl])    # the selection, then ascending columns
+        m = chosen.size
+        pk[r, :m] = logits[r, chosen]
+        pos[r, :m] = chosen * P + rank
+        pk[r, m:kl] = -np.inf
+        pos[r, m:kl] = np.arange(m, kl) * P + rank
+    return pk
+
+
+def topk_merge(allp, n, P, kl, kk, topk_tokens):
+    """fast_topk.merge (fast_topk.py:69-78; csrc/topk_select.cu:203-244): per row the top kk of the P * kl gathered
+    candidates by (key desc, concatenation index asc) -> positions, -1 for +-inf values and slots >= kk."""
+    a = np.asarray(allp, dtype=np.float32).reshape(P, n, 2 * kl)
+    out = np.full((n, topk_tokens), -1, dtype=np.int32)
+    for r in range(n):
+        vals = a[:, r, :kl].reshape(-1)
+        poss = a[:, r, kl:].copy().view(np.int32).reshape(-1)
+        kv = okey(vals).astype(np.int64)
+        order = np.lexsort((np.arange(vals.size), -kv))[:kk]
+        out[r, :order.size] = np.where(np.isinf(vals[order]), -1, poss[order])
     return out
 
 

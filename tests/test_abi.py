@@ -35,6 +35,10 @@ def test_version():
       None, None), -2),
     (("spmla_topk", None, 0, None, 1, 10, 5000, None, 0, None), -5),
     (("spmla_topk", None, 0, None, 1, 10, 0, None, 0, None), -2),
+    (("spmla_topk_local", None, 0, None, 1, 0, 1, 100, 4096, None, None), -5),
+    (("spmla_topk_local", None, 0, None, 1, 2, 2, 100, 16, None, None), -2),
+    (("spmla_topk_merge", None, 4, 2, 16, 33, 33, None, 0, None), -2),
+    (("spmla_topk_merge", None, 4, 2, 2048, 4000, 4000, None, 0, None), -5),
     (("spmla_gather", None, 0, 650, None, 1, None, 0, None), -2),
     (("spmla_cache_write", None, 0, None, 0, None, 1, None, 10, 64, 0, 7, 1.0, None), -2),
     (("spmla_index_logits", None, 0, 0, None, 0, None, 0, 64, 0, None, 0, 64, None, None, 1, 32, 128, 10, 1, 0, 0,

@@ -1,0 +1,113 @@
+"""CPU checks of the host-side mirror: metadata building, backend descriptor, hot-set choice, argument validation,
+and the oracle's fast_topk.local / merge restatement (brute force on tiny rows, and local + merge == top-k)."""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import spmla_ref as ref
+
+
+def test_backend_descriptor():
+    from arcagi2_flashnext_dots3_amd import dsa
+    B = dsa.PortableSparseBackend
+    assert B.get_name() == "DOTS3_PORTABLE_MLA_SPARSE"
+    assert B.get_impl_cls() is dsa.PortableSparseImpl
+    assert B.get_builder_cls() is dsa.PortableXPUBuilder
+    assert B.get_metadata_cls() is dsa.SparseMetadata
+    assert B.get_supported_head_sizes() == []
+
+
+def test_builder_req_id_per_token():
+    from arcagi2_flashnext_dots3_amd.dsa import CommonAttentionMetadata, PortableXPUBuilder
+    qsl = torch.tensor([0, 3, 3, 7, 8], dtype=torch.int32)           # request 1 has no tokens
+    cam = CommonAttentionMetadata(query_start_loc=qsl, num_reqs=4, num_actual_tokens=8, max_query_len=4,
+                                  max_seq_len=100, slot_mapping=torch.arange(8),
+                                  block_table_tensor=torch.zeros(4, 2, dtype=torch.int32))
+    b = PortableXPUBuilder(64, 2048, 12, "cpu")
+    md = b.build(0, cam)
+    assert md.req_id_per_token.tolist() == [0, 0, 0, 2, 2, 2, 2, 3]
+    assert b.req_id_per_token_buffer[8:].tolist() == [3, 3, 3, 3]     # padding tokens clamp to the last request
+    assert md.num_decode_tokens == 8 and md.block_size == 64 and md.topk_tokens == 2048
+
+
+def test_impl_rejects_unsupported_shapes():
+    from arcagi2_flashnext_dots3_amd.dsa import PortableSparseImpl
+    with pytest.raises(ValueError):
+        PortableSparseImpl(128, 512, 0.1, 1, None, None, "fp8_ds_mla", None, "decoder", None)
+    with pytest.raises(NotImplementedError):
+        PortableSparseImpl(128, 576, 0.1, 1, None, 128, "fp8_ds_mla", None, "decoder", None)
+
+
+def test_hot_rows_by_frequency():
+    from arcagi2_flashnext_dots3_amd.sparse_offload import hot_rows_by_frequency
+    counts = torch.tensor([3, 0, 5, 3, 1, 5, 0, 3])
+    assert hot_rows_by_frequency(counts, 4).tolist() == [2, 5, 0, 3]   # ties -> lower row id
+    assert hot_rows_by_frequency(counts, 100).tolist() == [2, 5, 0, 3, 7, 4]
+
+
+def test_shard_store_validates_layout():
+    from arcagi2_flashnext_dots3_amd.shard_indexer import ShardStore
+    st = ShardStore(torch.zeros(10, 64, 132, dtype=torch.uint8), 1, 0)
+    assert (st.BS, st.RPB, st.STRIDE_BLK, st.R_local) == (64, 64, 64 * 132, 640)
+    st4 = ShardStore(torch.zeros(10, 64, 33, dtype=torch.uint8), 4, 1)     # [blocks, BS, 132 / P]
+    assert (st4.RPB, st4.R_local) == (16, 160)
+    with pytest.raises(ValueError):
+        ShardStore(torch.zeros(10, 64, 128, dtype=torch.uint8), 1, 0)
+
+
+def _brute_local(x, ctx, rank, P, kl):
+    rows, Lc = x.shape
+    pk = np.zeros((rows, 2 * kl), dtype=np.float32)
+    pos = pk[:, kl:].view(np.int32)
+    for r in range(rows):
+        n = min(Lc, -(-(int(ctx[r]) - rank) // P)) if ctx[r] > rank else 0
+        key = [int(ref.okey(np.float32(v))) for v in x[r, :n]]
+        order = sorted(range(n), key=lambda j: (-key[j], j))[:kl]
+        chosen = sorted(order)
+        for s, j in enumerate(chosen):
+            pk[r, s] = x[r, j]
+            pos[r, s] = j * P + rank
+        for s in range(len(chosen), kl):
+            pk[r, s] = -np.inf
+            pos[r, s] = s * P + rank
+    return pk
+
+
+def test_oracle_topk_local_brute_force():
+    g = np.random.RandomState(3)
+    for trial, (rank, P) in enumerate([(0, 1), (1, 2), (3, 4), (0, 3)]):
+        x = np.round(g.randn(5, 23).astype(np.float32) * 2) / 2          # ties
+        x[0, 3] = np.nan
+        x[1, 4] = np.inf
+        x[2, 5] = -0.0
+        x[2, 6] = 0.0
+        ctx = np.array([80, 23 * P, 7, 0, rank + 1], dtype=np.int32)
+        for kl in (1, 6, 23, 30):
+            a = ref.topk_local(x, ctx, rank, P, kl)
+            b = _brute_local(x, ctx, rank, P, kl)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (trial, kl)
+
+
+def test_oracle_topk_merge_brute_force_and_composition():
+    g = np.random.RandomState(4)
+    n, P, kl = 3, 3, 5
+    allp = np.zeros((P * n, 2 * kl), dtype=np.float32)
+    allp[:, :kl] = np.round(g.randn(P * n, kl) * 2) / 2
+    allp[0, 1] = -np.inf
+    allp[4, 2] = np.inf
+    allp[:, kl:] = g.randint(0, 1000, (P * n, kl)).astype(np.int32).view(np.float32)
+    for kk, tt in itertools.product((1, 7, 15), (15, 18)):
+        got = ref.topk_merge(allp, n, P, kl, kk, tt)
+        for r in range(n):
+            cand = [(allp[p * n + r, i], p * kl + i, allp[p * n + r, kl + i:kl + i + 1].view(np.int32)[0])
+                    for p in range(P) for i in range(kl)]
+            cand.sort(key=lambda c: (-int(ref.okey(np.float32(c[0]))), c[1]))
+            exp = [(-1 if np.isinf(v) else int(pos)) for v, _, pos in cand[:kk]] + [-1] * (tt - kk)
+            assert got[r].tolist() == exp
+    # local + merge at P = 1 is the exact top-k
+    x = np.round(g.randn(4, 200).astype(np.float32) * 3) / 3
+    ctx = np.array([200, 150, 20, 0], dtype=np.int32)
+    pk = ref.topk_local(x, ctx, 0, 1, 64)
+    assert np.array_equal(ref.topk_merge(pk, 4, 1, 64, 64, 64), ref.topk(x, ctx, 64))
