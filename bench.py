@@ -1,17 +1,20 @@
-"""Benchmark of the MI355X sparse-MLA decode step (BASELINE.json metric: "sparse-MLA decode step us + effective GB/s
+"""Benchmark of the MI355X sparse-MLA decode path (BASELINE.json metric: "sparse-MLA decode step us + effective GB/s
 (% of 8 TB/s), B=64 ctx32K top2048").
 
-Default workload = BASELINE config 2 (all-HBM decode): B = 64 sequences, 128 query heads, 32768-token context per
-sequence held as Row656 KV rows in HBM (latent / rope N(0,1), written by the library's own cache-write kernel),
-q bf16 N(0,1), top-2048 row indices per sequence drawn uniformly without replacement, softmax scale 1/sqrt(192),
-bf16 out + fp32 LSE. One step = one spmla_attn_splitk launch over the whole batch (inputs resident in HBM).
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 1|2|3|4|5] [--no-variant]
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Default (--config 2) = BASELINE config 2, all-HBM decode: B = 64 sequences, 128 query heads, 32768-token context per
+sequence held as Row656 KV rows in HBM (latent / rope N(0,1), written by the library's own cache-write kernel), q bf16
+N(0,1), top-2048 row indices per sequence drawn uniformly without replacement, softmax scale 1/sqrt(192), bf16 out +
+fp32 LSE. One step = one spmla_attn_splitk launch over the whole batch (inputs resident in HBM). `value` = effective
+GB/s = algorithmic bytes / step time, algorithmic bytes = 131072 rows x 656 B + q + idx + out + lse = 104,366,080 B.
+`roofline` is timed live with HIP events on the stream the kernel is launched on; `cpu_baseline` times the float32
+torch-CPU restatement (oracle/cpu_port.py) of the same step on this host's cores. Unless --no-variant, the line also
+carries `host_tier_variant`: BASELINE config 3 (same shapes, 2M-row pool in pinned host memory, 25% HBM hot set,
+Zipf(1.1) selections) measured in the same run.
 
-Prints ONE JSON line. `value` = effective GB/s = algorithmic bytes of the step / measured step time, where the
-algorithmic bytes are 131072 rows x 656 B + q + idx + out + lse = 104,366,080 B. `roofline` is measured live with
-HIP events on the stream the kernel is launched on; `cpu_baseline` times the float32 torch-CPU restatement
-(oracle/cpu_port.py) of the same full step on this host's cores.
+Other configs print their own JSON line (same keys): 1 = B=1 / 16 heads / K=256 check + timing, 3 = offload split-K,
+4 = indexer logits + top-2048 at L = 32768 and 131072, 5 = chunked prefill (8192 queries) + cache write.
 """
 import argparse
 import json
@@ -29,21 +32,58 @@ ALG_BYTES = B * K * ROWB + B * H * D * 2 + B * K * 4 + B * H * 512 * 2 + B * H *
 ALG_FLOPS = B * H * K * (2 * 576 + 2 * 512)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+METRIC = "sparse-MLA decode step us + effective GB/s (% of 8 TB/s), B=64 ctx32K top2048"
 
 
-def build_inputs(dev, nsets=1):
+# ------------------------------------------------------------------------------------------------ helpers
+def _timed(fn, steps, warmup):
+    """Average ms of fn() over `steps` calls (after `warmup`), HIP events on the current stream (the stream every
+    library entry point launches on)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _line(metric, value, unit, a, ms, dtype, config, roofline, cpu=None, hib=True, **extra):
+    res = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": a.steps,
+           "warmup": a.warmup, "ms_per_step": round(ms, 5), "higher_is_better": hib, "scaling": "weak",
+           "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded)", "config": config,
+           "roofline": roofline, "cpu_baseline": cpu}
+    res.update(extra)
+    return res
+
+
+def _cache_fill(pool_u8, nrows, seed, dev):
+    """Rows 0..nrows of pool_u8 (device or pinned host) written from seeded N(0,1) bf16 latents / ropes by the
+    library's cache-write kernel."""
     import torch
     from arcagi2_flashnext_dots3_amd import kernels
-    R = B * CTX
-    pool = torch.empty(R, ROWB, dtype=torch.uint8, device=dev)
-    g = torch.Generator(device=dev).manual_seed(1)
+    g = torch.Generator(device=dev).manual_seed(seed)
     chunk = 1 << 18
-    for r0 in range(0, R, chunk):
-        n = min(chunk, R - r0)
+    for r0 in range(0, nrows, chunk):
+        n = min(chunk, nrows - r0)
         kv = torch.randn(n, 512, generator=g, device=dev).to(torch.bfloat16)
         pe = torch.randn(n, 64, generator=g, device=dev).to(torch.bfloat16)
         slots = torch.arange(r0, r0 + n, dtype=torch.int64, device=dev)
-        kernels.cache_write(kv, pe, slots, pool)
+        kernels.cache_write(kv, pe, slots, pool_u8)
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------------------------------------ config 2
+def build_inputs(dev, nsets=1):
+    import torch
+    R = B * CTX
+    pool = torch.empty(R, ROWB, dtype=torch.uint8, device=dev)
+    _cache_fill(pool, R, 1, dev)
     gq = torch.Generator().manual_seed(0)
     q = torch.randn(B, H, D, generator=gq).to(torch.bfloat16).to(dev)
     idxs = []
@@ -73,9 +113,293 @@ def cpu_baseline(pool, q, idx):
         ts.append(time.perf_counter() - t0)
     ts.sort()
     t = ts[2]
-    return {"value": ALG_BYTES / t / 1e9, "unit": "GB/s", "cores": nt, "kind": "port",
+    return {"value": round(ALG_BYTES / t / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
             "sample": f"full config-2 step (B=64, H=128, K=2048) in fp32 torch on {nt} threads, median of 5: "
                       f"{t * 1e3:.1f} ms/step"}
+
+
+def run_config2(a, dev):
+    import torch
+    from arcagi2_flashnext_dots3_amd import kernels
+    pool, q, idxs = build_inputs(dev, a.idx_sets)
+    out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    cur = [0]
+
+    def step():
+        kernels.attend(q, pool, idxs[cur[0] % len(idxs)], SM_SCALE, out=out, lse=lse)
+        cur[0] += 1
+
+    ms = _timed(step, a.steps, a.warmup)
+    gbs = ALG_BYTES / (ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "spmla::attn::attn_kernel", "alg_bytes_per_launch": ALG_BYTES,
+            "mfma_tflops": round(ALG_FLOPS / (ms * 1e-3) / 1e12, 2),
+            "mfma_frac_bf16_peak": round(ALG_FLOPS / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+    tf = os.path.join(ROOT, "profiles", "attn_kernel_config2_traffic.json")
+    if os.path.exists(tf):   # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (calibrated)
+        roof["traffic"] = json.load(open(tf)).get("bytes_per_launch")
+    cfg = {"workload": "BASELINE config 2: all-HBM sparse-MLA decode, B=64, H=128, ctx=32768/seq, top-2048, Row656 "
+                       "rows, bf16 out + fp32 LSE", "global_batch": B, "heads": H, "ctx": CTX, "topk": K,
+           "row_bytes": ROWB, "idx_sets": a.idx_sets, "attn_teams": kernels._lib.lib().spmla_attn_teams()}
+    res = _line(METRIC, gbs, "GB/s", a, ms, "fp8e4m3 rows x bf16 q: bf16 MFMA (QK), f16 MFMA (PV), fp32 accumulate",
+                cfg, roof, step_us=round(ms * 1e3, 2))
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(pool, q, idxs[0])
+    del pool
+    torch.cuda.empty_cache()
+    return res
+
+
+# ------------------------------------------------------------------------------------------------ config 3
+R3 = 2097152
+
+
+def zipf_selections(nseq, K, R, seed, s=1.1, perm=None, device="cpu"):
+    """Per sequence K distinct rows: Zipf(s) ranks (P(r) ~ r^-s over R ranks) mapped through a seeded permutation of
+    the pool, repeated draws rejected (first appearances kept in draw order). Returns int64 [nseq, K] on `device`."""
+    import torch
+    if perm is None:
+        perm = torch.randperm(R, generator=torch.Generator().manual_seed(3))
+    perm = perm.to(device)
+    cdf = torch.cumsum(torch.arange(1, R + 1, dtype=torch.float64, device=device) ** (-s), 0)
+    cdf /= cdf[-1].clone()
+    g = torch.Generator(device=device).manual_seed(seed)
+    M = 6 * K
+    out = torch.empty((nseq, K), dtype=torch.int64, device=device)
+    for b0 in range(0, nseq, 256):
+        n = min(256, nseq - b0)
+        r = torch.searchsorted(cdf, torch.rand(n, M, generator=g, device=device, dtype=torch.float64))
+        r = r.clamp_(max=R - 1)
+        rs, order = torch.sort(r, dim=1, stable=True)                # equal ranks keep draw order
+        first = torch.ones_like(rs, dtype=torch.bool)
+        first[:, 1:] = rs[:, 1:] != rs[:, :-1]
+        pos = torch.sort(torch.where(first, order, torch.full_like(order, M)), dim=1).values[:, :K]
+        if bool((pos[:, -1] >= M).any()):
+            raise RuntimeError("zipf_selections: too few distinct draws; raise M")
+        out[b0:b0 + n] = perm[torch.gather(r, 1, pos)]
+    return out
+
+
+def run_config3(a, dev, steps=None):
+    import torch
+    from arcagi2_flashnext_dots3_amd import kernels
+    from arcagi2_flashnext_dots3_amd.sparse_offload import LayerOffload, hot_rows_by_frequency
+    steps = steps or a.steps
+    C = R3 // 4
+    lo = LayerOffload(R3, dev, cache_rows=C)
+    _cache_fill(lo.host, R3, 1, dev)
+    perm = torch.randperm(R3, generator=torch.Generator().manual_seed(3))
+    warm = zipf_selections(64 * B, K, R3, seed=4, perm=perm, device=dev)   # 64 warm-up steps of B sequences
+    counts = torch.bincount(warm.reshape(-1), minlength=R3)
+    del warm
+    lo.set_hot_rows(hot_rows_by_frequency(counts, C))
+    idx = zipf_selections(B, K, R3, seed=5, perm=perm, device=dev).to(torch.int32)
+    gq = torch.Generator().manual_seed(0)
+    q = torch.randn(B, H, D, generator=gq).to(torch.bfloat16).to(dev)
+    hit = lo.hit_rate(idx)
+    out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    ms = _timed(lambda: lo.attend(q, idx, SM_SCALE, 1.0, H, out=out, lse=lse), steps, max(2, a.warmup // 4))
+    o_t, l_t = lo.attend(q, idx, SM_SCALE, 1.0, H, return_lse=True)
+    # single-tier check: the same rows gathered into HBM and attended in one pass
+    staged = torch.empty(B * K, ROWB, dtype=torch.uint8, device=dev)
+    kernels.gather(lo.host, idx.reshape(-1).to(torch.int64), staged)
+    sidx = torch.arange(B * K, dtype=torch.int32, device=dev).view(B, K)
+    o_1, l_1 = kernels.attend(q, staged, sidx, SM_SCALE)
+    torch.cuda.synchronize()
+    d_o = float((o_t.float() - o_1.float()).abs().max())
+    d_l = float((l_t - l_1).abs().max())
+    # host-tier roofline: pinned host -> HBM copy bandwidth
+    hb = torch.empty(1 << 28, dtype=torch.uint8, pin_memory=True)
+    db = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+    h2d_ms = _timed(lambda: db.copy_(hb, non_blocking=True), 5, 2)
+    h2d = (1 << 28) / (h2d_ms * 1e-3) / 1e9
+    miss_bytes = (1.0 - hit) * B * K * ROWB
+    gbs = ALG_BYTES / (ms * 1e-3) / 1e9
+    res = {"value": round(gbs, 3), "unit": "GB/s (algorithmic bytes of the config-2 step / step time)",
+           "ms_per_step": round(ms, 4), "hit_rate": round(hit, 4), "host_rows_per_step": int(round((1 - hit) * B * K)),
+           "pcie_bytes_per_step": int(miss_bytes), "pcie_gbs_achieved": round(miss_bytes / (ms * 1e-3) / 1e9, 2),
+           "h2d_copy_gbs": round(h2d, 2), "max_abs_diff_vs_single_tier": {"out": d_o, "lse": d_l},
+           "workload": "BASELINE config 3: B=64, H=128, top-2048 Zipf(1.1) rows of a 2,097,152-row Row656 pool in "
+                       "pinned host memory, HBM hot set = 524,288 most frequent rows over 64 warm-up steps; tier split "
+                       "-> HBM-tier attention + host rows gathered over PCIe -> host-tier attention -> LSE merge"}
+    del lo, hb, db, staged
+    torch.cuda.empty_cache()
+    return res
+
+
+# ------------------------------------------------------------------------------------------------ config 4
+def run_config4(a, dev):
+    import numpy as np
+    import torch
+    from arcagi2_flashnext_dots3_amd import kernels
+    from arcagi2_flashnext_dots3_amd.shard_indexer import ShardStore
+    bs = 64
+    results = {}
+    for L in (32768, 131072):
+        nbp = L // bs
+        kc = torch.empty(B * nbp, bs, 132, dtype=torch.uint8, device=dev)
+        st = ShardStore(kc, 1, 0)
+        g = torch.Generator(device=dev).manual_seed(5)
+        chunk = 1 << 20
+        for r0 in range(0, B * L, chunk):
+            n = min(chunk, B * L - r0)
+            k = torch.randn(n, 128, generator=g, device=dev).to(torch.bfloat16)
+            st.write(k, torch.arange(r0, r0 + n, dtype=torch.int64, device=dev), False)
+        bt = torch.arange(B * nbp, dtype=torch.int32, device=dev).view(B, nbp)
+        q = torch.randn(B, 64, 128, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(dev)
+        w = torch.rand(B, 64, generator=torch.Generator().manual_seed(7)).to(dev)
+        req = torch.arange(B, dtype=torch.int32, device=dev)
+        ctx = torch.full((B,), L, dtype=torch.int32, device=dev)
+        lg = torch.empty(B, L, dtype=torch.float32, device=dev)
+        out = torch.empty(B, K, dtype=torch.int32, device=dev)
+
+        def logits():
+            kernels._lib.call("spmla_index_logits", q.data_ptr(), q.stride(0), q.stride(1), w.data_ptr(),
+                              w.stride(0), kc.data_ptr(), st.R_local, st.RPB, st.STRIDE_BLK, bt.data_ptr(),
+                              bt.stride(0), bs, req.data_ptr(), ctx.data_ptr(), B, 64, 128, L, 1, 0, 1,
+                              lg.data_ptr(), lg.stride(0), kernels._stream(q))
+
+        ms_l = _timed(logits, a.steps, a.warmup)
+        ms_t = _timed(lambda: kernels.topk(lg, ctx, K, out=out), a.steps, a.warmup)
+        key_bytes = B * L * 132
+        alg = key_bytes + B * 64 * 128 * 2 + B * 64 * 4 + B * L * 4
+        flops = B * L * 64 * 128 * 2
+        cpu = None
+        if not a.no_cpu and L == 32768:
+            cpu = _cpu_indexer(q, w, kc, B, L, bt, bs)
+        results[str(L)] = {"step_us": round((ms_l + ms_t) * 1e3, 2), "logits_us": round(ms_l * 1e3, 2),
+                           "topk_us": round(ms_t * 1e3, 2),
+                           "logits_gbs": round(alg / (ms_l * 1e-3) / 1e9, 1),
+                           "logits_hbm_frac": round(alg / (ms_l * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                           "logits_tflops": round(flops / (ms_l * 1e-3) / 1e12, 1),
+                           "topk_read_gbs": round(B * L * 4 / (ms_t * 1e-3) / 1e9, 1),
+                           "alg_bytes": alg, "cpu_baseline": cpu}
+        del kc, lg
+        torch.cuda.empty_cache()
+    r = results["32768"]
+    roof = {"bound": "hbm", "achieved": r["logits_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": r["logits_hbm_frac"], "traffic": None, "kernel": "spmla::idx::logits_kernel"}
+    return _line("indexer logits + top-2048 step us, B=64, 64 heads x 128, L=32768", r["step_us"], "us", a,
+                 r["step_us"] / 1e3, "e4m3 keys x bf16 q: bf16 MFMA, fp32 accumulate",
+                 {"workload": "BASELINE config 4: indexer top-2048 of L = 32768 and 131072, B=64"}, roof,
+                 r["cpu_baseline"], hib=False, by_ctx=results)
+
+
+def _cpu_indexer(q, w, kc, Bn, L, bt, bs):
+    """torch-CPU restatement (fp32) of the indexer step: dequantized keys, sum_h w relu(q k) * s, topk; one
+    sequence timed (median of 3), scaled to B sequences."""
+    import torch
+    from oracle import cpu_port
+    nt = cpu_port.threads()
+    torch.set_num_threads(nt)
+    rows = kc.view(-1, 132)[bt[0].long().repeat_interleave(bs) * bs + torch.arange(L, device=kc.device) % bs].cpu()
+    tab = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float()
+    kk = tab[rows[:, :128].long()] * rows[:, 128:132].contiguous().view(torch.float32)
+    qh, wh = q[0].float().cpu(), w[0].cpu()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        s = (torch.relu(qh @ kk.T) * wh[:, None]).sum(0)
+        torch.topk(s, K)
+        ts.append(time.perf_counter() - t0)
+    t = sorted(ts)[1] * Bn
+    return {"value": round(t * 1e6, 1), "unit": "us per step (B=64 scaled from one sequence)", "cores": nt,
+            "kind": "port", "sample": f"one sequence of L={L} keys in fp32 torch, median of 3, x{Bn}"}
+
+
+# ------------------------------------------------------------------------------------------------ config 5
+def run_config5(a, dev):
+    import torch
+    from arcagi2_flashnext_dots3_amd import kernels
+    NQ, CTXMAX, bs = 8192, 65536, 64
+    nblk = CTXMAX // bs + 64
+    cache = torch.zeros(nblk, bs, ROWB, dtype=torch.uint8, device=dev)
+    gb = torch.Generator().manual_seed(10)
+    bt = torch.randperm(nblk, generator=gb)[: CTXMAX // bs].to(torch.int32).view(1, -1).to(dev)
+    pos0 = CTXMAX - NQ
+    posp = torch.arange(pos0, device=dev)
+    prior = (bt[0, posp // bs].long() * bs + posp % bs)
+    g = torch.Generator(device=dev).manual_seed(1)
+    for r0 in range(0, pos0, 1 << 16):
+        n = min(1 << 16, pos0 - r0)
+        kernels.cache_write(torch.randn(n, 512, generator=g, device=dev).to(torch.bfloat16),
+                            torch.randn(n, 64, generator=g, device=dev).to(torch.bfloat16), prior[r0:r0 + n], cache)
+    g9 = torch.Generator(device=dev).manual_seed(9)
+    kv = torch.randn(NQ, 512, generator=g9, device=dev).to(torch.bfloat16)
+    pe = torch.randn(NQ, 64, generator=g9, device=dev).to(torch.bfloat16)
+    posn = torch.arange(pos0, CTXMAX, device=dev)
+    slots = bt[0, posn // bs].long() * bs + posn % bs
+    ms_w = _timed(lambda: kernels.cache_write(kv, pe, slots, cache), a.steps, a.warmup)
+    g8 = torch.Generator().manual_seed(8)
+    tk = torch.stack([torch.randperm(min(p + 1, CTXMAX), generator=g8)[:K] for p in range(pos0, CTXMAX)])
+    tk = tk.to(torch.int32).to(dev)
+    rows = kernels.rows_from_topk(tk, torch.zeros(NQ, dtype=torch.int32, device=dev), bt, bs)
+    q = torch.randn(NQ, H, D, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
+    out = torch.empty(NQ, H, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(NQ, H, dtype=torch.float32, device=dev)
+    flat = cache.view(-1, ROWB)
+    ms_a = _timed(lambda: kernels.attend(q, flat, rows, SM_SCALE, out=out, lse=lse), max(3, a.steps // 20),
+                  max(1, a.warmup // 10))
+    flops = NQ * H * K * (2 * 576 + 2 * 512)
+    tf = flops / (ms_a * 1e-3) / 1e12
+    wb = NQ * (1024 + 128 + 8) + NQ * ROWB
+    cpu = None
+    if not a.no_cpu:
+        from oracle import cpu_port
+        nt = cpu_port.threads()
+        torch.set_num_threads(nt)
+        ns = 256
+        rh = flat[rows[:ns].clamp(min=0).reshape(-1).long()].cpu()
+        li = torch.arange(ns * K, dtype=torch.int32).view(ns, K)
+        qh = q[:ns].cpu()
+        t0 = time.perf_counter()
+        cpu_port.attention_f32(qh, rh, li, SM_SCALE)
+        t = (time.perf_counter() - t0) * NQ / ns
+        cpu = {"value": round(t * 1e3, 1), "unit": "ms per prefill chunk (attention only)", "cores": nt,
+               "kind": "port", "sample": f"{ns} of {NQ} queries in fp32 torch, scaled linearly"}
+    roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None, "kernel": "spmla::attn::attn_kernel"}
+    res = _line("chunked prefill attention ms (8192 queries x 128 heads x top-2048) + cache write us", ms_a, "ms", a,
+                ms_a + ms_w, "bf16 MFMA (QK), f16 MFMA (PV), fp32 accumulate",
+                {"workload": "BASELINE config 5: 8192 queries, 128 heads, top-2048 of <= 65536 prior rows; write "
+                             "8192 rows at random slots of a paged cache (block 64)"}, roof, cpu, hib=False,
+                cache_write_us=round(ms_w * 1e3, 2),
+                cache_write_gbs=round(wb / (ms_w * 1e-3) / 1e9, 1))
+    return res
+
+
+# ------------------------------------------------------------------------------------------------ config 1
+def run_config1(a, dev):
+    import numpy as np
+    import torch
+    from arcagi2_flashnext_dots3_amd import kernels
+    from oracle import cpu_port
+    T1, H1, R1, K1 = 1, 16, 4096, 256
+    pool = torch.empty(R1, ROWB, dtype=torch.uint8, device=dev)
+    _cache_fill(pool, R1, 1, dev)
+    q = torch.randn(T1, H1, D, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
+    idx = torch.randperm(R1, generator=torch.Generator().manual_seed(2))[:K1].to(torch.int32).view(1, K1).to(dev)
+    ms = _timed(lambda: kernels.attend(q, pool, idx, SM_SCALE), a.steps, a.warmup)
+    o, l = kernels.attend(q, pool, idx, SM_SCALE)
+    ph, qh, ih = pool.cpu(), q.cpu(), idx.cpu()
+    eo, el = cpu_port.attention_f32(qh, ph, ih, SM_SCALE)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        cpu_port.attention_f32(qh, ph, ih, SM_SCALE)
+    tc = (time.perf_counter() - t0) / 20
+    alg = K1 * ROWB + H1 * D * 2 + H1 * 512 * 2 + H1 * 4 + K1 * 4
+    return _line("sparse-MLA decode us, B=1, 16 heads, top-256 of 4096", ms * 1e3, "us", a, ms,
+                 "bf16 / f16 MFMA, fp32 accumulate", {"workload": "BASELINE config 1"},
+                 {"bound": "hbm", "achieved": round(alg / (ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS,
+                  "unit": "GB/s", "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5), "traffic": None},
+                 {"value": round(tc * 1e6, 1), "unit": "us", "cores": cpu_port.threads(), "kind": "port",
+                  "sample": "the full config-1 step, mean of 20"}, hib=False,
+                 max_abs_diff_vs_fp32_cpu={"out": float((o.float().cpu() - eo).abs().max()),
+                                           "lse": float((l.cpu() - el).abs().max())})
 
 
 def main():
@@ -84,6 +408,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-variant", action="store_true", help="config 2 only: skip the host-tier (config 3) variant")
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
+                    help="only run 5 plain device-to-device copies of BYTES bytes (the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     ap.add_argument("--idx-sets", type=int, default=4,
                     help="steps rotate over this many independent top-k draws; 4 sets select 344 MB of rows, more "
                          "than the 256 MB Infinity Cache, so rows come from HBM rather than from the previous step")
@@ -93,51 +422,35 @@ def main():
               f"supported", file=sys.stderr)
         sys.exit(2)
     import torch
-    from arcagi2_flashnext_dots3_amd import kernels
     dev = torch.device("cuda:0")
-    pool, q, idxs = build_inputs(dev, a.idx_sets)
-    out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
-    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
-
-    cur = [0]
-
-    def step():
-        kernels.attend(q, pool, idxs[cur[0] % len(idxs)], SM_SCALE, out=out, lse=lse)
-        cur[0] += 1
-
-    for _ in range(a.warmup):
-        step()
-    torch.cuda.synchronize()
-    st = torch.cuda.current_stream(dev)            # the stream spmla_attn_splitk is launched on
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for _ in range(a.steps):
-        step()
-    e1.record(st)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / a.steps
-    gbs = ALG_BYTES / (ms * 1e-3) / 1e9
-    res = {
-        "metric": "sparse-MLA decode step us + effective GB/s (% of 8 TB/s), B=64 ctx32K top2048",
-        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": round(ms, 5), "step_us": round(ms * 1e3, 2), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp8e4m3 x bf16 MFMA, fp32 accumulate", "data": "synthetic (seeded N(0,1))",
-        "config": {"workload": "BASELINE config 2: all-HBM sparse-MLA decode, B=64, H=128, ctx=32768/seq, "
-                               "top-2048, Row656 rows, bf16 out + fp32 LSE",
-                   "global_batch": B, "heads": H, "ctx": CTX, "topk": K, "row_bytes": ROWB,
-                   "idx_sets": a.idx_sets, "attn_teams": int(os.environ.get("SPMLA_ATTN_TEAMS", "2"))},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "spmla::attn::attn_kernel", "alg_bytes_per_launch": ALG_BYTES,
-                     "mfma_tflops": round(ALG_FLOPS / (ms * 1e-3) / 1e12, 2),
-                     "mfma_frac_bf16_peak": round(ALG_FLOPS / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
-        "cpu_baseline": None,
-    }
-    tf = os.environ.get("SPMLA_TRAFFIC_JSON")   # optional: HBM bytes per launch measured by rocprofv3 --pmc
-    if tf and os.path.exists(tf):
-        res["roofline"]["traffic"] = json.load(open(tf)).get("attn_kernel_bytes")
-    if not a.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(pool, q, idxs[0])
+    if a.copy_calib:
+        src = torch.ones(a.copy_calib, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes": a.copy_calib}), flush=True)
+        return
+    if a.config == 2:
+        res = run_config2(a, dev)
+        if not a.no_variant:
+            try:
+                res["host_tier_variant"] = run_config3(a, dev, steps=min(a.steps, 20))
+            except Exception as e:   # the primary line must still print
+                res["host_tier_variant"] = {"error": repr(e)[:300]}
+    elif a.config == 3:
+        r = run_config3(a, dev)
+        res = _line("offload split-K decode step us (host tier + HBM hot rows), B=64 top2048", r["ms_per_step"] * 1e3,
+                    "us", a, r["ms_per_step"], "bf16 / f16 MFMA, fp32 accumulate", {"workload": r["workload"]},
+                    {"bound": "pcie", "achieved": r["pcie_gbs_achieved"], "peak": r["h2d_copy_gbs"], "unit": "GB/s",
+                     "frac": round(r["pcie_gbs_achieved"] / max(r["h2d_copy_gbs"], 1e-9), 4), "traffic": None},
+                    hib=False, detail=r)
+    elif a.config == 4:
+        res = run_config4(a, dev)
+    elif a.config == 5:
+        res = run_config5(a, dev)
+    else:
+        res = run_config1(a, dev)
     print(json.dumps(res), flush=True)
 
 
