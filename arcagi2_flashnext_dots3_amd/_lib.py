@@ -31,7 +31,6 @@ SIGNATURES = {
     "spmla_attn_splitk": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, I, P, LL, LL, P, LL, P, P, P],
     "spmla_lse_merge": [P, I, LL, LL, LL, P, LL, LL, I, I, I, P, LL, LL, P, P, LL, P],
     "spmla_version": [],
-    "spmla_attn_teams": [],
     "spmla_host_e4m3_encode": [P, P, LL],
 }
 _RESTYPE = {"spmla_version": ctypes.c_char_p, "spmla_host_e4m3_encode": None}

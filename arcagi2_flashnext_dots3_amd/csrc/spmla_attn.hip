@@ -7,20 +7,24 @@
 //   p = exp2(s * log2e - m), o[h] = kv_scale * sum_k p latent / sum_k p,  lse = ln sum_k exp(s)
 //   invalid entries contribute nothing; a token with no valid entry gives o = 0 and lse = -inf.
 //
-// gfx950 mapping. One workgroup = (token t, group of 32 heads, split s); TEAMS x 4 waves.
-//   * Rows are staged through a ring of NBUF 32-row tiles in LDS with direct global->LDS copies
-//     (global_load_lds_dwordx4), chunk-major layout [chunk][row][16 B]: each MFMA operand read is a conflict-free
-//     ds_read_b128 and the V^T operand is one ds_read_b64_tr_b8 (8 rows x 16 columns per 16-lane group).
-//   * In a team, wave w owns latent scale group w (columns 128w..128w+127) and rope quarter w for QK, and the same
-//     128 output columns for PV. QK on bf16 MFMA (32x32x16): e4m3 codes convert exactly to bf16, two per
-//     v_cvt_scalef32_pk_bf16_fp8; the per-row group scale multiplies the fp32 partial. (fp8 MFMA is not used for
-//     QK: its internal accumulation keeps only ~2^-12 of the largest product, measured on gfx950.)
-//     Partial S^T tiles (32 rows x 32 heads) meet in LDS; wave w runs the online softmax of heads 8w..8w+7 and
-//     publishes P and the rescale factor; PV on fp16 MFMA with P' = P * scale (fp16, RNE) and the codes in fp16.
-//   * Lazy rescaling: the reference max m of a head moves only when a tile exceeds it by more than TAU (log2
-//     units), so p <= 2^TAU: an exact softmax either way, fewer rescales of O.
-//   * With TEAMS = 2 the two teams take alternate tiles (2 waves per SIMD hide each other's latencies); their
-//     states merge in LDS at the end.
+// gfx950 mapping. One workgroup = (token t, group of 32 heads, split s), 4 waves, one wave per SIMD (each wave
+// holds its 32 heads' query in VGPRs and their 32 x 512 fp32 output accumulator in AGPRs). The rows of the split
+// are cut into 32-row tiles; wave w streams tiles w, w + 4, w + 8, ... on its own, so the main loop has no
+// workgroup barrier and no exchange between waves:
+//   * a tile (codes + scales) is copied into the wave's private double buffer in LDS with direct global->LDS
+//     copies (global_load_lds_dwordx4), chunk-major [chunk][row][16 B], while the rope of its rows goes straight
+//     into VGPRs (the rope is an MFMA A operand as stored); the copy of tile j + 1 runs during the math of tile j;
+//   * S^T (32 rows x 32 heads) on bf16 MFMA (32x32x16): e4m3 codes convert exactly to bf16, two per
+//     v_cvt_scalef32_pk_bf16_fp8; each scale group's partial is multiplied by the row's fp32 scale (the fp8 MFMA
+//     is not used: its internal accumulation keeps only ~2^-12 of the largest product, measured on gfx950);
+//   * the C layout puts one head in each lane (16 rows; the other 16 in lane + 32), so the online softmax is
+//     in-lane plus one cross-half exchange, and P feeds the PV B operand without data movement (the row order of
+//     the V^T operand, read with ds_read_b64_tr_b8, follows the lane's rows);
+//   * PV on f16 MFMA with P' = P * scale (fp16, RNE) and the codes in fp16; p <= 2^TAU keeps P' finite for
+//     scales up to 65504 / 2^TAU (rows whose largest latent magnitude is below 458,000);
+//   * lazy rescaling: a head's reference max moves only when a tile exceeds it by more than TAU (log2 units),
+//     so p <= 2^TAU: exact either way, and O is rescaled rarely;
+//   * at the end the 4 waves' (m, l, O) merge through LDS (the tile buffers are free by then).
 #include "spmla_common.h"
 #include <stdlib.h>
 
@@ -28,38 +32,33 @@ namespace spmla {
 namespace attn {
 
 constexpr int HG = 32;                // heads per workgroup
+constexpr int NW = 4;                 // waves per workgroup
 constexpr int TR = 32;                // rows per tile
 constexpr int KMAX = 2048;            // selected rows per (token, split) staged in LDS
-constexpr float TAU = 4.0f;
-constexpr float F16_MAX = 65504.0f;
+constexpr float TAU = 6.0f;
 
-// tile layout (bytes)
-constexpr int T_LAT = 0;                       // 32 latent chunks: [c][r][16]
-constexpr int T_ROPE = 32 * TR * 16;           // 8 rope chunks:    [e][r][16]   (16384)
-constexpr int T_SC = T_ROPE + 8 * TR * 16;     // scales:           [g][r] f32   (20480)
-constexpr int TILE = T_SC + 4 * TR * 4;        // 20992
-constexpr int NCOPY = 22;                      // copy instructions per tile
-
-// exchange layouts, in 16-byte units (4 rows of one head), padded to 33 heads per row block
-constexpr int XS_UNITS = 4 * 8 * 33;           // S partials [w][rb][h]
-constexpr int XP_UNITS = 8 * 33;               // P [rb][h]
-
-template <int TEAMS, int NBUF>
-struct Lds {
-  static constexpr int TILES = 0;
-  static constexpr int S = TILES + NBUF * TILE;
-  static constexpr int P = S + TEAMS * XS_UNITS * 16;
-  static constexpr int IDX = P + TEAMS * XP_UNITS * 16;
-  static constexpr int MISC = IDX + KMAX * 4;              // per team: alpha[32], m[32], l[32]
-  static constexpr int TOTAL = MISC + TEAMS * 3 * 32 * 4;
-  static_assert(TOTAL <= 160 * 1024, "LDS budget");
-};
+// tile layout (bytes): 32 code chunks [c][r][16] (chunk-major: each MFMA operand read is one conflict-free
+// ds_read_b128, each V^T operand one ds_read_b64_tr_b8), then the row scales transposed to [g][r] fp32 (the copy
+// writes them in that order: one 4-byte copy per (row, group))
+constexpr int T_SCT = 32 * TR * 16;            // 16384
+constexpr int TILE = T_SCT + 4 * TR * 4;       // 16896
+constexpr int NBUF = 2;
+// Query in LDS (shared by the 4 waves): the rope (64 dims) and latent groups 2, 3 (dims 256..511) of each head;
+// latent groups 0, 1 stay in VGPRs. Row stride padded so 16-byte reads of 32 consecutive heads hit distinct banks.
+constexpr int QRS = (64 + 256) * 2 + 16;       // 656
+constexpr int QPIECES = (64 + 256) / 8;        // 16-byte pieces per head in LDS
+constexpr int L_TILES = 0;
+constexpr int L_QROPE = NW * NBUF * TILE;      // 135168
+constexpr int L_ML = L_QROPE + HG * QRS;       // 156160: per wave m[32], l[32]
+constexpr int L_TOTAL = L_ML + NW * 64 * 4;    // 157184
+static_assert(L_TOTAL <= 160 * 1024, "LDS budget");
+static_assert(NW * 8 * 4 * 64 * 16 <= L_QROPE, "merge staging (8 output tiles per wave) fits the tile buffers");
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"   // m0 is reserved; nothing else in these kernels uses it
-// Direct global->LDS copies (lane l's bytes land at lds + size * l). Issued through inline asm so that the
-// compiler does not track them: it would otherwise drain every outstanding copy (vmcnt(0)) at each
-// workgroup barrier. Completion is tracked by hand with wait_vm<>() below. The LDS destination is
+// Direct global->LDS copy (lane l's 16 bytes land at lds + 16 * l). Issued through inline asm so that the
+// compiler does not track it: it would otherwise drain every outstanding copy (vmcnt(0)) at the first
+// s_waitcnt it places for its own loads. Completion is tracked by hand with wait_vm<>(). The LDS destination is
 // wave-uniform; readfirstlane pins it to an SGPR for m0; one wait state separates the m0 write from the
 // LDS-DMA instruction that reads it (an SALU m0 write -> LDS DMA hazard the assembler does not resolve).
 __device__ inline void dma16(const void* g, SPMLA_LDS void* l) {
@@ -72,8 +71,7 @@ __device__ inline void dma4(const void* g, SPMLA_LDS void* l) {
 }
 #pragma clang diagnostic pop
 
-// Workgroup barrier for data exchanged through LDS only. __syncthreads() adds workgroup-scope fences whose
-// lowering waits for every outstanding vector-memory operation (vmcnt(0)), which would drain the copy ring.
+// Workgroup barrier for data exchanged through LDS only (no vector-memory drain).
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // vmcnt-only wait (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
@@ -112,6 +110,41 @@ __device__ inline uint32_t pk_bf16(float a, float b) {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
+// QK MFMAs with the accumulator in VGPRs. The compiler builtin puts every MFMA result in AGPRs when the function
+// uses AGPRs, which here would evict part of the PV accumulator around each QK phase; inline asm pins the QK
+// accumulator (read by the scale FMAs) to VGPRs. Hazards the compiler cannot see inside asm are covered here:
+// "s_nop 1" before the MFMA for VALU-written operands (2 wait states), and after the last MFMA of a chain
+// 16 wait states before any VALU reads the result (8-pass XDL write -> VALU read). Back-to-back MFMAs of one
+// chain have srcC == vdst exactly, which the hardware forwards.
+__device__ inline f32x16 qk_first(bf16x8 a, bf16x8 b) {
+  f32x16 d;
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  return d;
+}
+__device__ inline f32x16 qk_next(bf16x8 a, bf16x8 b, f32x16 c) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+  return c;
+}
+__device__ inline f32x16 qk_last(bf16x8 a, bf16x8 b, f32x16 c) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7" : "+v"(c) : "v"(a), "v"(b));
+  return c;
+}
+
+// O *= a for the 256 AGPR accumulator values of a lane, one register at a time through one VGPR. Written as
+// inline asm on the AGPRs: a plain C++ multiply makes the register allocator move the whole accumulator into
+// VGPRs (and spill), although the rescale is a rare path.
+__device__ inline void scale_acc(f32x16 (&O)[16], float a) {
+#pragma unroll
+  for (int b = 0; b < 16; ++b)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float tmp;
+      asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+                   : "+a"(O[b][e]), "=&v"(tmp)
+                   : "v"(a));
+    }
+}
+
 struct Params {
   const uint16_t* q; long long q_st, q_sh;        // q[t][h][576] bf16 (last dim contiguous)
   const uint8_t* pool; long long R;               // Row656 rows
@@ -120,67 +153,30 @@ struct Params {
   int T, H, S, HGN;                               // tokens, heads, splits, head groups
   float c;                                        // sm_scale * kv_scale * log2(e)
   float kv_scale;
-  uint16_t* out; long long o_st, o_sh;            // S == 1: bf16 out[t][h][512]
-  float* lse; long long lse_st;                   // S == 1: lse[t][h]
+  uint16_t* out; long long o_st, o_sh;            // bf16 out[t][h][512] (when opart is null)
+  float* lse; long long lse_st;                   // lse[t][h]
   float* opart; float* lsepart;                   // fp32 partials: opart[s][t][h][512], lsepart[s][t][h]
 };
 
-// Copy instructions of one tile are spread over all waves: wave v issues j = v, v + NWAVES, ...
-template <int NWAVES>
-__device__ constexpr int copies_of(int v) { return (NCOPY - v + NWAVES - 1) / NWAVES; }
-
-template <int NWAVES>
-__device__ inline void issue_tile(const uint8_t* __restrict__ pool, long long R, const SPMLA_LDS int* rid,
-                                  SPMLA_LDS uint8_t* tile, int wave, int lane) {
-  const int row_id = rid[lane & 31];
-  const bool valid = row_id >= 0 && (long long)row_id < R;
-  // an invalid row copies row 0 (present: the tile loop only runs when R > 0) and is zeroed by zero_tile()
-  const uint8_t* src = pool + (valid ? (long long)row_id : 0ll) * ROW656;
-  const int half = lane >> 5;
+// Copy one tile (32 rows: codes + scales) into the wave's buffer and load the rows' rope into VGPRs.
+// rid: the tile's 32 row ids (-1 = none: such a row copies row 0, which exists whenever a tile is read, and is
+// masked out of the softmax). 18 vector-memory instructions of the copy + 4 rope loads.
+constexpr int VM_PER_TILE = 22;
+__device__ inline void issue_tile(const uint8_t* __restrict__ pool, const SPMLA_LDS int* rid,
+                                  SPMLA_LDS uint8_t* tb, int lane, u32x4 (&rp)[4]) {
+  const int x = rid[lane & 31];
+  const uint8_t* src = pool + (long long)(x >= 0 ? x : 0) * ROW656;
+  const int h = lane >> 5;
 #pragma unroll
-  for (int j = wave; j < NCOPY; j += NWAVES) {
-    if (j < 16) dma16(src + (2 * j + half) * 16, tile + T_LAT + j * 1024);
-    else if (j < 20) dma16(src + ROPE_OFF + (2 * (j - 16) + half) * 16, tile + T_ROPE + (j - 16) * 1024);
-    else dma4(src + SC_OFF + (2 * (j - 20) + half) * 4, tile + T_SC + (j - 20) * 256);
-  }
-}
-
-template <int NWAVES>
-__device__ inline void zero_tile(long long R, const SPMLA_LDS int* rid, SPMLA_LDS uint8_t* tile, int wave, int lane) {
-  const int row_id = rid[lane & 31];
-  if (row_id >= 0 && (long long)row_id < R) return;
+  for (int i = 0; i < 16; ++i) dma16(src + (2 * i + h) * 16, tb + i * 1024);
+  // scales: copy e, lane l -> group 2e + h of row l % 32 at float (2e + h) * 32 + l % 32
+  dma4(src + SC_OFF + h * 4, tb + T_SCT);
+  dma4(src + SC_OFF + (2 + h) * 4, tb + T_SCT + 256);
 #pragma unroll
-  for (int j = wave; j < NCOPY; j += NWAVES) {
-    if (j < 16) *(SPMLA_LDS u32x4*)(tile + T_LAT + j * 1024 + lane * 16) = u32x4{0, 0, 0, 0};
-    else if (j < 20) *(SPMLA_LDS u32x4*)(tile + T_ROPE + (j - 16) * 1024 + lane * 16) = u32x4{0, 0, 0, 0};
-    else *(SPMLA_LDS uint32_t*)(tile + T_SC + (j - 20) * 256 + lane * 4) = 0u;
-  }
+  for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(src + ROPE_OFF + ks * 32 + h * 16);
 }
 
-// Wait until this wave's copies of every tile <= `upto` have landed, given that tiles up to `issued` were issued.
-// In the steady state exactly LATER tiles are issued after `upto` (LATER = NBUF - 2 * TEAMS: the ring holds the
-// tiles of the current and the next step plus LATER in flight), so the wait is a compile-time vmcnt; any other
-// situation (ramp-up / tail) drains all copies, which is always safe.
-template <int NWAVES, int LATER>
-__device__ inline void wait_tiles(int upto, int issued, int wave) {
-  const int later = issued - upto;
-  const int n = copies_of<NWAVES>(wave);
-  if (LATER > 0 && later == LATER) {
-    if (n == 6) wait_vm<6 * LATER>();
-    else if (n == 5) wait_vm<5 * LATER>();
-    else if (n == 3) wait_vm<3 * LATER>();
-    else if (n == 2) wait_vm<2 * LATER>();
-    else wait_vm<0>();
-  } else {
-    wait_vm<0>();
-  }
-}
-
-template <int TEAMS, int NBUF>
-__global__ void __launch_bounds__(256 * TEAMS, 1) attn_kernel(Params p) {
-  using L = Lds<TEAMS, NBUF>;
-  constexpr int NWAVES = 4 * TEAMS;
-  static_assert(NBUF >= 2 * TEAMS + 1, "ring must hold the tiles in use plus one in flight");
+__global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_generic[];
   SPMLA_LDS uint8_t* lds = (SPMLA_LDS uint8_t*)smem_generic;
 
@@ -193,8 +189,7 @@ __global__ void __launch_bounds__(256 * TEAMS, 1) attn_kernel(Params p) {
   const int t = ts / p.S;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control flow
-  const int team = wave >> 2, w = wave & 3;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control flow
   const int half = lane >> 5, l32 = lane & 31;
 
   // ---- row range of this split
@@ -205,277 +200,317 @@ __global__ void __launch_bounds__(256 * TEAMS, 1) attn_kernel(Params p) {
   const int nrow = ke > kb ? ke - kb : 0;
   const int ntile = p.R > 0 ? (nrow + TR - 1) / TR : 0;     // no rows to read: o = 0, lse = -inf
 
-  SPMLA_LDS int* sidx = (SPMLA_LDS int*)(lds + L::IDX);
-  SPMLA_LDS float* s_alpha = (SPMLA_LDS float*)(lds + L::MISC) + team * 96;
-  SPMLA_LDS float* s_m = s_alpha + 32;
-  SPMLA_LDS float* s_l = s_alpha + 64;
-  SPMLA_LDS f32x4* xS = (SPMLA_LDS f32x4*)(lds + L::S) + team * XS_UNITS;
-  SPMLA_LDS f32x4* xP = (SPMLA_LDS f32x4*)(lds + L::P) + team * XP_UNITS;
-  SPMLA_LDS uint8_t* tiles = lds + L::TILES;
+  SPMLA_LDS uint8_t* qrope = lds + L_QROPE;
 
-  // ---- stage the row ids of this range (out-of-range slots read as -1)
+  // ---- prologue, two memory round trips: (1) the row ids of this wave's first two tiles and the query parts
+  // that go to LDS; (2) the first tile's copy, its rope and the latent query fragments (in flight while the query
+  // staging is written). Row ids of later tiles are loaded one tile ahead, into registers.
   const int* idxrow = p.idx + (long long)t * p.idx_st + kb;
-  for (int i = tid; i < ntile * TR; i += 256 * TEAMS) sidx[i] = i < nrow ? idxrow[i] : -1;
-
-  // ---- query fragments (bf16 B operands) for latent group w and rope quarter w.
-  // k-pair kp (32 dims): lane half h holds dims 128w + 32kp + 16h + 0..15; MFMA 2kp uses the first 8, 2kp+1 the
-  // next 8 (the same permutation as the K operand read below).
   const int h = hg * HG + l32;
   const bool hval = h < p.H;
-  const uint16_t* qh = p.q + (long long)t * p.q_st + (long long)(hval ? h : 0) * p.q_sh;
-  bf16x8 qf[8];
+  auto row_id = [&](int tile) -> int {        // row id of this lane's row in `tile` (-1: none / invalid)
+    const int i = tile * TR + l32;
+    int x = -1;
+    if (i < nrow) x = idxrow[i];
+    return (x >= 0 && (long long)x < p.R) ? x : -1;
+  };
+  int rcur = row_id(w), rnxt = row_id(w + NW);
+  {
+    u32x4 qv[HG * QPIECES / 256];
 #pragma unroll
-  for (int kp = 0; kp < 4; ++kp) {
-    const uint16_t* src = qh + w * QGROUP + kp * 32 + half * 16;
-    const u32x4 a = hval ? *(const u32x4*)src : u32x4{0, 0, 0, 0};
-    const u32x4 b = hval ? *(const u32x4*)(src + 8) : u32x4{0, 0, 0, 0};
+    for (int k = 0; k < HG * QPIECES / 256; ++k) {          // 32 heads x 40 pieces (rope, latent groups 2, 3)
+      const int i = tid + 256 * k, qh = i / QPIECES, part = i % QPIECES;
+      const bool ok = hg * HG + qh < p.H;
+      const uint16_t* qsrc = p.q + (long long)t * p.q_st + (long long)(ok ? hg * HG + qh : 0) * p.q_sh;
+      const uint16_t* src = part < 8 ? qsrc + D_LAT + part * 8 : qsrc + 2 * QGROUP + (part - 8) * 8;
+      qv[k] = *(const u32x4*)src & (ok ? 0xffffffffu : 0u);
+    }
+    wait_vm<0>();
+#pragma unroll
+    for (int k = 0; k < HG * QPIECES / 256; ++k) {
+      const int i = tid + 256 * k;
+      *(SPMLA_LDS u32x4*)(qrope + (i / QPIECES) * QRS + (i % QPIECES) * 16) = qv[k];
+    }
+  }
+  const int ntw = ntile > w ? (ntile - w + NW - 1) / NW : 0;   // tiles w, w + 4, ...
+  SPMLA_LDS uint8_t* mybuf = lds + L_TILES + w * NBUF * TILE;
+  u32x4 rp[4];
+  if (ntw > 0) {
+    const uint8_t* src = p.pool + (long long)(rcur >= 0 ? rcur : 0) * ROW656;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dma16(src + (2 * i + half) * 16, mybuf + i * 1024);
+    dma4(src + SC_OFF + half * 4, mybuf + T_SCT);
+    dma4(src + SC_OFF + (2 + half) * 4, mybuf + T_SCT + 256);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(src + ROPE_OFF + ks * 32 + half * 16);
+  }
+  // latent query fragments of groups 0, 1 (bf16 B operands), k-pair kp (32 dims = chunks 2kp, 2kp + 1): lane half
+  // h holds the dims of chunk 2kp + h; MFMA 2kp + e uses its bytes 8e .. 8e + 7 (the K operand is read the same
+  // way). They are waited for with the first tile.
+  const uint16_t* qrow = p.q + (long long)t * p.q_st + (long long)(hval ? h : 0) * p.q_sh;
+  bf16x8 qf[16];
+  const uint32_t qmask = hval ? 0xffffffffu : 0u;       // heads past H: zero query (row 0 is read instead)
+#pragma unroll
+  for (int kp = 0; kp < 8; ++kp) {
+    const uint16_t* src = qrow + (2 * kp + half) * 16;
+    const u32x4 a = *(const u32x4*)src & qmask;
+    const u32x4 b = *(const u32x4*)(src + 8) & qmask;
     qf[2 * kp] = __builtin_bit_cast(bf16x8, a);
     qf[2 * kp + 1] = __builtin_bit_cast(bf16x8, b);
   }
-  bf16x8 qrope;
-  {
-    const u32x4 v = hval ? *(const u32x4*)(qh + D_LAT + w * 16 + half * 8) : u32x4{0, 0, 0, 0};
-    qrope = __builtin_bit_cast(bf16x8, v);
-  }
+  lds_barrier();                                // query staging visible to all waves (copies stay in flight)
+  wait_vm<0>();                                 // query fragments (and the first tile) landed
 
-  // Complete the query loads now, before any tile copy is in flight: an explicit s_waitcnt the compiler sees, so
-  // that it does not place its own vmcnt(0) for them inside the tile loop (which would drain the copy ring).
-  wait_vm<0>();
+  const float c = p.c;
+  float m_run = -__builtin_inff();     // reference max of this lane's head (log2 units)
+  float l_run = 0.f;                   // sum of p over this lane's 16 rows of every tile
+  bool started = false;                // wave-uniform: O holds contributions
 
-  // softmax ownership: wave w of a team owns heads 8w..8w+7; lane -> head 8w + lane/8, rows 4*(lane%8) .. +3
-  const int sm_h = w * 8 + (lane >> 3);
-  const int sm_rb = lane & 7;
-  float m_ref = -__builtin_inff();
-  float l_part = 0.f;
-
-  f32x16 O[4];
+  f32x16 O[16];
 #pragma unroll
-  for (int b = 0; b < 4; ++b) O[b] = f32x16{};
+  for (int b = 0; b < 16; ++b) O[b] = f32x16{};
 
-  __syncthreads();                              // sidx staged (plain global loads: a fence is fine here)
+  // per-lane V^T transpose-read address (16-lane group G reads 8 rows x 16 columns: lane 2i + c supplies row i,
+  // bytes 8c .. 8c + 7; the rows follow the C-layout rows of the lane's P values)
+  const int G = lane >> 4, gi = (lane & 15) >> 1, gc = lane & 1;
+  const int tr_off = ((G & 1) * 32 + 8 * (gi >> 2) + 4 * (G >> 1) + (gi & 3)) * 16 + gc * 8;
 
-  // ---- prologue: NBUF - TEAMS tiles in flight (the ring keeps TEAMS slots for the tiles being computed)
-  constexpr int AHEAD = NBUF - TEAMS;
-  int issued = -1;
 #pragma unroll 1
-  for (int j = 0; j < AHEAD && j < ntile; ++j) {
-    issue_tile<NWAVES>(p.pool, p.R, sidx + j * TR, tiles + j * TILE, wave, lane);
-    issued = j;
-  }
-  // first step's tiles
-  if (ntile > 0) {
-    const int upto = ntile - 1 < TEAMS - 1 ? ntile - 1 : TEAMS - 1;
-    wait_tiles<NWAVES, NBUF - 2 * TEAMS>(upto, issued, wave);
-    for (int j = 0; j <= upto; ++j) zero_tile<NWAVES>(p.R, sidx + j * TR, tiles + j * TILE, wave, lane);
-  }
-  lds_barrier();
+  for (int j = 0; j < ntw; ++j) {
+    wait_vm<0>();                               // tile j copied, its rope loaded
+    SPMLA_LDS uint8_t* tb = mybuf + (j & 1) * TILE;
+    const int tix = w + NW * j;
 
-  const int nstep = (ntile + TEAMS - 1) / TEAMS;
-  float sc[16];      // scale of group w for this lane's 16 C-layout rows (8q + 4half + j)
-#pragma unroll 1
-  for (int st = 0; st < nstep; ++st) {
-    const int it = st * TEAMS + team;            // this team's tile
-    const bool act = it < ntile;
-    SPMLA_LDS uint8_t* tile = tiles + (it % NBUF) * TILE;
-
-    // ---- QK partial for latent group w and rope quarter w
-    if (act) {
-      f32x16 acc = f32x16{};
+    // ---- first LDS reads of the tile: query rope, K group 0, the row ids of this and of the next tile
+    u32x4 qr[4], kr[4];
 #pragma unroll
-      for (int kp = 0; kp < 4; ++kp) {
-        const int c = 8 * w + 2 * kp + half;                   // 16-byte chunk of 16 latent codes
-        const u32x4 raw = *(SPMLA_LDS u32x4*)(tile + T_LAT + c * 512 + l32 * 16);
+    for (int ks = 0; ks < 4; ++ks) qr[ks] = *(SPMLA_LDS u32x4*)(qrope + l32 * QRS + (16 * ks + 8 * half) * 2);
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) kr[kq] = *(SPMLA_LDS u32x4*)(tb + (2 * kq + half) * 512 + l32 * 16);
+    const bool more = j + 1 < ntw;
+    const int rnn = j + 2 < ntw ? row_id(tix + 2 * NW) : -1;   // row ids two tiles ahead (used next iteration)
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- rope part of S^T (operands in VGPRs / LDS)
+    f32x16 S;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 a = __builtin_bit_cast(bf16x8, rp[ks]), b = __builtin_bit_cast(bf16x8, qr[ks]);
+      S = ks == 0 ? qk_first(a, b) : (ks == 3 ? qk_last(a, b, S) : qk_next(a, b, S));
+    }
+    const unsigned vmask = (unsigned)__ballot(rcur >= 0);  // rows of the tile that exist
+    // the next tile's copy is issued in four parts, one per latent group, between that group's MFMAs
+    const uint8_t* nsrc = p.pool + (long long)(rnxt >= 0 ? rnxt : 0) * ROW656;
+    SPMLA_LDS uint8_t* nbuf = mybuf + ((j + 1) & 1) * TILE;
+
+    // ---- latent part of S^T: group g = chunks 8g .. 8g + 7; group g + 1's K is read while group g's MFMAs run
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32x4 kn[4];
+      if (g < 3) {
+#pragma unroll
+        for (int kq = 0; kq < 4; ++kq) kn[kq] = *(SPMLA_LDS u32x4*)(tb + (2 * (4 * g + 4 + kq) + half) * 512 + l32 * 16);
+      }
+      if (more) {                                  // part g of the next tile's copy
+#pragma unroll
+        for (int i = 4 * g; i < 4 * g + 4; ++i) dma16(nsrc + (2 * i + half) * 16, nbuf + i * 1024);
+        if (g == 3) {
+          dma4(nsrc + SC_OFF + half * 4, nbuf + T_SCT);
+          dma4(nsrc + SC_OFF + (2 + half) * 4, nbuf + T_SCT + 256);
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(nsrc + ROPE_OFF + ks * 32 + half * 16);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      f32x16 acc;
+#pragma unroll
+      for (int kq = 0; kq < 4; ++kq) {
+        const int kp = 4 * g + kq;
+        const u32x4 raw = kr[kq];
         i32x4 a0, a1;
         a0[0] = (int)fp8lo_bf16x2(raw[0]); a0[1] = (int)fp8hi_bf16x2(raw[0]);
         a0[2] = (int)fp8lo_bf16x2(raw[1]); a0[3] = (int)fp8hi_bf16x2(raw[1]);
         a1[0] = (int)fp8lo_bf16x2(raw[2]); a1[1] = (int)fp8hi_bf16x2(raw[2]);
         a1[2] = (int)fp8lo_bf16x2(raw[3]); a1[3] = (int)fp8hi_bf16x2(raw[3]);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a0), qf[2 * kp], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1), qf[2 * kp + 1], acc, 0, 0, 0);
+        bf16x8 b0, b1;
+        if (g < 2) {
+          b0 = qf[2 * kp];
+          b1 = qf[2 * kp + 1];
+        } else {                                   // dims 16 (2kp + half) + 8e of latent groups 2, 3, from LDS
+          const SPMLA_LDS uint8_t* qp = qrope + l32 * QRS + 128 + ((2 * kp + half) * 16 - 2 * QGROUP) * 2;
+          b0 = __builtin_bit_cast(bf16x8, *(const SPMLA_LDS u32x4*)qp);
+          b1 = __builtin_bit_cast(bf16x8, *(const SPMLA_LDS u32x4*)(qp + 16));
+        }
+        acc = kq == 0 ? qk_first(__builtin_bit_cast(bf16x8, a0), b0) : qk_next(__builtin_bit_cast(bf16x8, a0), b0, acc);
+        acc = kq == 3 ? qk_last(__builtin_bit_cast(bf16x8, a1), b1, acc) : qk_next(__builtin_bit_cast(bf16x8, a1), b1, acc);
       }
-      const u32x4 ar = *(SPMLA_LDS u32x4*)(tile + T_ROPE + (2 * w + half) * 512 + l32 * 16);
-      const f32x16 accr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ar), qrope, f32x16{}, 0, 0, 0);
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const f32x4 v = *(SPMLA_LDS f32x4*)(tile + T_SC + w * 128 + (8 * qd + 4 * half) * 4);
-        sc[4 * qd + 0] = v[0]; sc[4 * qd + 1] = v[1]; sc[4 * qd + 2] = v[2]; sc[4 * qd + 3] = v[3];
-      }
-      // S partial -> xS[w][rb][h], rb = 2qd + half (rows 8qd + 4half .. +3)
+        const f32x4 sg = *(SPMLA_LDS f32x4*)(tb + T_SCT + (g * 32 + 8 * qd + 4 * half) * 4);
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        f32x4 v;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = __builtin_fmaf(sc[4 * qd + j], acc[4 * qd + j], accr[4 * qd + j]);
-        xS[(w * 8 + 2 * qd + half) * 33 + l32] = v;
+        for (int e = 0; e < 4; ++e) S[4 * qd + e] = __builtin_fmaf(acc[4 * qd + e], sg[e], S[4 * qd + e]);
       }
-    }
-    lds_barrier();   // B2: partials ready; every wave is past PV of its previous tile
-
-    // ---- refill the ring with the tiles whose slots the previous step freed
-#pragma unroll 1
-    for (int jt = issued + 1; jt < ntile && jt <= st * TEAMS + NBUF - 1; ++jt) {
-      issue_tile<NWAVES>(p.pool, p.R, sidx + jt * TR, tiles + (jt % NBUF) * TILE, wave, lane);
-      issued = jt;
+      if (g < 3) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) kr[q4] = kn[q4];
+      }
     }
 
-    // ---- online softmax for heads 8w .. 8w+7 of this team's tile
-    if (act) {
-      f32x4 sum = xS[(0 * 8 + sm_rb) * 33 + sm_h];
+    // ---- PV operands of group 0 (scales, V^T codes) read while the softmax runs
+    f32x4 ps[4];
+    i32x2 tv[8];
 #pragma unroll
-      for (int w2 = 1; w2 < 4; ++w2) {
-        const f32x4 v = xS[(w2 * 8 + sm_rb) * 33 + sm_h];
-        sum[0] += v[0]; sum[1] += v[1]; sum[2] += v[2]; sum[3] += v[3];
-      }
-      const i32x4 rid = *(SPMLA_LDS i32x4*)(sidx + it * TR + 4 * sm_rb);
-      const float c = p.c;
-      float x[4];
-      float tmax = -__builtin_inff();
+    for (int qd = 0; qd < 4; ++qd) ps[qd] = *(SPMLA_LDS f32x4*)(tb + T_SCT + (8 * qd + 4 * half) * 4);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool ok = rid[j] >= 0 && (long long)rid[j] < p.R;
-        x[j] = ok ? c * sum[j] : -__builtin_inff();
-        tmax = fmaxf(tmax, x[j]);
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 4, 64));
-      float alpha = 1.f;
-      if (tmax > m_ref + TAU) {                 // also true for the first finite tile (m_ref = -inf)
-        alpha = __builtin_amdgcn_exp2f(m_ref - tmax);   // exp2(-inf) = 0
-        m_ref = tmax;
-      }
-      f32x4 pv;
-      float ps = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pv[j] = x[j] > -__builtin_inff() ? __builtin_amdgcn_exp2f(x[j] - m_ref) : 0.f;
-        ps += pv[j];
-      }
-      l_part = l_part * alpha + ps;
-      xP[sm_rb * 33 + sm_h] = pv;
-      if ((lane & 7) == 0) s_alpha[sm_h] = alpha;
-    }
-    // the next step's tiles must have landed before the barrier that precedes their QK
-    {
-      const int nxt = (st + 2) * TEAMS - 1 < ntile - 1 ? (st + 2) * TEAMS - 1 : ntile - 1;
-      if ((st + 1) * TEAMS < ntile) {
-        wait_tiles<NWAVES, NBUF - 2 * TEAMS>(nxt, issued, wave);
-        for (int j = (st + 1) * TEAMS; j <= nxt; ++j)
-          zero_tile<NWAVES>(p.R, sidx + j * TR, tiles + (j % NBUF) * TILE, wave, lane);
-      }
-    }
-    lds_barrier();   // B3: P and alpha published; the next step's tiles complete
+    for (int f8 = 0; f8 < 8; ++f8)
+      tv[f8] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((SPMLA_LDS i32x2*)(tb + (f8 >> 1) * 1024 + (f8 & 1) * 256 + tr_off));
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- PV for output columns 128w .. 128w+127 (fp16 MFMA)
-    if (act) {
-      const float al = s_alpha[l32];
-      if (__ballot(al != 1.f)) {
+    // ---- rows that do not exist: -inf (C-layout row of value i: 8 (i / 4) + 4 half + i % 4)
+    if (vmask != 0xffffffffu) {
+      const unsigned lm = vmask >> (4 * half);
 #pragma unroll
-        for (int b = 0; b < 4; ++b) O[b] *= al;
+      for (int i = 0; i < 16; ++i)
+        if (!((lm >> (8 * (i >> 2) + (i & 3))) & 1u)) S[i] = -__builtin_inff();
+    }
+
+    // ---- online softmax of this lane's head
+    float mx = S[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, S[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;             // c > 0; -inf stays -inf
+    const bool need = mx > m_run + TAU;                      // also true for the first finite tile
+    if (__ballot(need)) {
+      const float mn = need ? mx : m_run;
+      const float alpha = need ? (m_run > -__builtin_inff() ? __builtin_amdgcn_exp2f(m_run - mn) : 0.f) : 1.f;
+      l_run *= alpha;
+      if (started) scale_acc(O, alpha);
+      m_run = mn;
+    }
+    const float mref = m_run > -__builtin_inff() ? m_run : 0.f;
+    float P[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      P[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[i], c, -mref));   // exp2(-inf) = 0
+      l_run += P[i];
+    }
+    started = true;
+
+    // ---- PV: output columns of group g use P' = P * scale(row, g) (fp16); group g + 1's operands read meanwhile
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f32x4 pn[4];
+      i32x2 vn[8];
+      if (g < 3) {
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) pn[qd] = *(SPMLA_LDS f32x4*)(tb + T_SCT + ((g + 1) * 32 + 8 * qd + 4 * half) * 4);
+#pragma unroll
+        for (int f8 = 0; f8 < 8; ++f8)
+          vn[f8] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (SPMLA_LDS i32x2*)(tb + (4 * (g + 1) + (f8 >> 1)) * 1024 + (f8 & 1) * 256 + tr_off));
       }
+      __builtin_amdgcn_sched_barrier(0);
       f16x8 pb[2];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const f32x4 v0 = xP[(4 * ks + half) * 33 + l32];        // rows 16ks + 4half + 0..3   (qd = 2ks)
-        const f32x4 v1 = xP[(4 * ks + 2 + half) * 33 + l32];    // rows 16ks + 8 + 4half + 0..3 (qd = 2ks+1)
-        const float* s0 = sc + 8 * ks;
+        const f32x4 s0 = ps[2 * ks], s1 = ps[2 * ks + 1];
+        const float* pp = P + 8 * ks;
         i32x4 o;
-        o[0] = (int)pk_f16(fminf(v0[0] * s0[0], F16_MAX), fminf(v0[1] * s0[1], F16_MAX));
-        o[1] = (int)pk_f16(fminf(v0[2] * s0[2], F16_MAX), fminf(v0[3] * s0[3], F16_MAX));
-        o[2] = (int)pk_f16(fminf(v1[0] * s0[4], F16_MAX), fminf(v1[1] * s0[5], F16_MAX));
-        o[3] = (int)pk_f16(fminf(v1[2] * s0[6], F16_MAX), fminf(v1[3] * s0[7], F16_MAX));
+        o[0] = (int)pk_f16(pp[0] * s0[0], pp[1] * s0[1]);
+        o[1] = (int)pk_f16(pp[2] * s0[2], pp[3] * s0[3]);
+        o[2] = (int)pk_f16(pp[4] * s1[0], pp[5] * s1[1]);
+        o[3] = (int)pk_f16(pp[6] * s1[2], pp[7] * s1[3]);
         pb[ks] = __builtin_bit_cast(f16x8, o);
       }
-      // V^T operand via LDS transpose reads: 16-lane group g reads 8 rows x 16 columns of one chunk.
-      const int g = lane >> 4, gi = (lane & 15) >> 1, gc = lane & 1;
-      const int hh = g >> 1;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int row = 16 * ks + 4 * hh + (gi & 3) + 8 * (gi >> 2);
+      for (int f8 = 0; f8 < 8; ++f8) {
+        const int mt = 4 * g + (f8 >> 1), ks = f8 & 1;     // output columns 32 mt .. 32 mt + 31, rows 16 ks ..
+        const i32x2 raw = tv[f8];
+        i32x4 a;
+        a[0] = (int)fp8lo_f16x2((uint32_t)raw[0]); a[1] = (int)fp8hi_f16x2((uint32_t)raw[0]);
+        a[2] = (int)fp8lo_f16x2((uint32_t)raw[1]); a[3] = (int)fp8hi_f16x2((uint32_t)raw[1]);
+        O[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), pb[ks], O[mt], 0, 0, 0);
+      }
+      if (g < 3) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int chunk = 8 * w + 2 * b + (g & 1);
-          SPMLA_LDS i32x2* addr = (SPMLA_LDS i32x2*)(tile + T_LAT + chunk * 512 + row * 16 + gc * 8);
-          const i32x2 raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(addr);
-          i32x4 a;
-          a[0] = (int)fp8lo_f16x2((uint32_t)raw[0]); a[1] = (int)fp8hi_f16x2((uint32_t)raw[0]);
-          a[2] = (int)fp8lo_f16x2((uint32_t)raw[1]); a[3] = (int)fp8hi_f16x2((uint32_t)raw[1]);
-          O[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), pb[ks], O[b], 0, 0, 0);
+        for (int q4 = 0; q4 < 4; ++q4) ps[q4] = pn[q4];
+#pragma unroll
+        for (int f8 = 0; f8 < 8; ++f8) tv[f8] = vn[f8];
+      }
+    }
+    rcur = rnxt;
+    rnxt = rnn;
+  }
+
+  // ---- merge the 4 waves: per head M = max m_w, L = sum l_w 2^(m_w - M), O = sum O_w 2^(m_w - M) / L
+  l_run += __shfl_xor(l_run, 32, 64);
+  SPMLA_LDS float* s_ml = (SPMLA_LDS float*)(lds + L_ML);
+  lds_barrier();                                 // every wave is done with its tiles (no copy in flight)
+  if (half == 0) { s_ml[w * 64 + l32] = m_run; s_ml[w * 64 + 32 + l32] = l_run; }
+  lds_barrier();
+  // weight of wave v's partial for this lane's head: 2^(m_v - M) kv_scale / L (applied by the reducing wave, so
+  // the partials go to LDS straight from the accumulator registers)
+  float M = -__builtin_inff();
+#pragma unroll
+  for (int v = 0; v < NW; ++v) M = fmaxf(M, s_ml[v * 64 + l32]);
+  float fv[NW];
+  float L = 0.f;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    const float mv = s_ml[v * 64 + l32];
+    fv[v] = mv > -__builtin_inff() ? __builtin_amdgcn_exp2f(mv - M) : 0.f;
+    L += s_ml[v * 64 + 32 + l32] * fv[v];
+  }
+  const float inv = L > 0.f ? p.kv_scale / L : 0.f;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) fv[v] *= inv;
+  const float lse_v = L > 0.f ? (M + log2f(L)) * 0.69314718055994531f : -__builtin_inff();
+
+  SPMLA_LDS f32x4* xo = (SPMLA_LDS f32x4*)(lds + L_TILES);   // [wave][tile 0..7][qd][lane]
+  // output head of this lane, recomputed from the lane id (cheaper than keeping it live across the loop)
+  const int ho = hg * HG + (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31);
+  const bool hoval = ho < p.H;
+#pragma unroll
+  for (int rnd = 0; rnd < 2; ++rnd) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x16& o = O[8 * rnd + b];
+        xo[((w * 8 + b) * 4 + qd) * 64 + lane] = f32x4{o[4 * qd], o[4 * qd + 1], o[4 * qd + 2], o[4 * qd + 3]};
+      }
+    lds_barrier();
+    // wave w reduces output tiles 2w, 2w + 1 of this round and writes them
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      const int b = 2 * w + bb;
+      const int mt = 8 * rnd + b;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int v = 0; v < NW; ++v) {
+          const f32x4 x = xo[((v * 8 + b) * 4 + qd) * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(x[e], fv[v], acc[e]);
+        }
+        if (hoval) {
+          const int col = 32 * mt + 8 * qd + 4 * half;      // C-layout rows of values 4qd .. 4qd + 3
+          if (p.opart == nullptr) {
+            uint16_t* orow = p.out + (long long)t * p.o_st + (long long)ho * p.o_sh;
+            *(uint2*)(orow + col) = make_uint2(pk_bf16(acc[0], acc[1]), pk_bf16(acc[2], acc[3]));
+          } else {
+            float* orow = p.opart + (((long long)s * p.T + t) * p.H + ho) * D_LAT;
+            *(f32x4*)(orow + col) = acc;
+          }
         }
       }
     }
-  }
-
-  // ---- finalize: per-head (m, l) from the owner waves; with two teams merge team 1 into team 0 through LDS
-  {
-    float lt = l_part;
-    lt += __shfl_xor(lt, 1, 64);
-    lt += __shfl_xor(lt, 2, 64);
-    lt += __shfl_xor(lt, 4, 64);
-    lds_barrier();
-    if ((lane & 7) == 0) { s_l[sm_h] = lt; s_m[sm_h] = m_ref; }
     lds_barrier();
   }
-  float mh = s_m[l32], lh = s_l[l32];
-  if (TEAMS == 2) {
-    // team 1 parks its O (x its own normalizer weight) in the ring's LDS; team 0 adds it
-    SPMLA_LDS float* s_m1 = (SPMLA_LDS float*)(lds + L::MISC) + 96 + 32;
-    SPMLA_LDS float* s_l1 = s_m1 + 32;
-    SPMLA_LDS float* s_m0 = (SPMLA_LDS float*)(lds + L::MISC) + 32;
-    const float m0 = s_m0[l32], m1 = s_m1[l32];
-    const float M = fmaxf(m0, m1);
-    const float w0 = m0 > -__builtin_inff() ? __builtin_amdgcn_exp2f(m0 - M) : 0.f;
-    const float w1 = m1 > -__builtin_inff() ? __builtin_amdgcn_exp2f(m1 - M) : 0.f;
-    SPMLA_LDS f32x4* park = (SPMLA_LDS f32x4*)(lds + L::TILES);     // 4 waves x 4 blocks x 16 floats x 64 lanes
-    if (team == 1) {
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd)
-          park[((w * 4 + b) * 4 + qd) * 64 + lane] =
-              f32x4{O[b][4 * qd] * w1, O[b][4 * qd + 1] * w1, O[b][4 * qd + 2] * w1, O[b][4 * qd + 3] * w1};
-    }
-    lds_barrier();
-    if (team == 1) return;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x4 v = park[((w * 4 + b) * 4 + qd) * 64 + lane];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) O[b][4 * qd + j] = O[b][4 * qd + j] * w0 + v[j];
-      }
-    lh = s_l1[l32] * w1 + s_l[l32] * w0;
-    mh = M;
-  }
-  const float inv = lh > 0.f ? p.kv_scale / lh : 0.f;
-  if (!hval) return;
-  const float lse_v = lh > 0.f ? (mh + log2f(lh)) * 0.69314718055994531f : -__builtin_inff();
-  if (p.opart == nullptr) {
-    uint16_t* orow = p.out + (long long)t * p.o_st + (long long)h * p.o_sh;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int v0 = w * 128 + 32 * b + 8 * qd + 4 * half;
-        const uint32_t w0 = pk_bf16(O[b][4 * qd] * inv, O[b][4 * qd + 1] * inv);
-        const uint32_t w1 = pk_bf16(O[b][4 * qd + 2] * inv, O[b][4 * qd + 3] * inv);
-        *(uint2*)(orow + v0) = make_uint2(w0, w1);
-      }
-    }
-    if (w == 0 && half == 0) p.lse[(long long)t * p.lse_st + h] = lse_v;
-  } else {
-    float* orow = p.opart + (((long long)s * p.T + t) * p.H + h) * D_LAT;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int v0 = w * 128 + 32 * b + 8 * qd + 4 * half;
-        *(f32x4*)(orow + v0) = f32x4{O[b][4 * qd] * inv, O[b][4 * qd + 1] * inv, O[b][4 * qd + 2] * inv,
-                                     O[b][4 * qd + 3] * inv};
-      }
-    }
-    if (w == 0 && half == 0) p.lsepart[((long long)s * p.T + t) * p.H + h] = lse_v;
+  if (w == 0 && half == 0 && hoval) {
+    if (p.opart == nullptr) p.lse[(long long)t * p.lse_st + ho] = lse_v;
+    else p.lsepart[((long long)s * p.T + t) * p.H + ho] = lse_v;
   }
 }
 
@@ -547,16 +582,6 @@ using namespace spmla;
 
 extern "C" {
 
-// Workgroup shape of spmla_attn_splitk: 1 or 2 teams of 4 waves (SPMLA_ATTN_TEAMS, default 2).
-int spmla_attn_teams(void) {
-  static int teams = 0;
-  if (!teams) {
-    const char* e = getenv("SPMLA_ATTN_TEAMS");
-    teams = (e && e[0] == '1') ? 1 : 2;
-  }
-  return teams;
-}
-
 // See include/spmla.h for the contract.
 int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void* pool, long long R,
                       const int* idx, long long idx_st, int K, const int* kcount, int T, int H, float sm_scale,
@@ -567,7 +592,7 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
   if (!q || !idx || (R > 0 && !pool)) return SPMLA_EARG;
   const bool f32part = opart != nullptr;   // fp32 partials (any S) instead of the bf16 output (S == 1 only)
   if (f32part ? !lsepart : (S != 1 || !out || !lse)) return SPMLA_EARG;
-  if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7)) return SPMLA_EALIGN;
+  if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)pool & 15)) return SPMLA_EALIGN;
   if (out && (((uintptr_t)out & 7) || (o_st & 3) || (o_sh & 3))) return SPMLA_EALIGN;
   if (((K + S - 1) / S + attn::TR - 1) / attn::TR * attn::TR > attn::KMAX) return SPMLA_ELIMIT;
   attn::Params p;
@@ -582,30 +607,14 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
   const long long nwork = (long long)T * S * p.HGN;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);
-  const int teams = spmla_attn_teams();
-  if (teams == 2) {
-    constexpr int NB = 5;
-    using Lt = attn::Lds<2, NB>;
-    static bool attr = false;
-    if (!attr) {
-      hipError_t e = hipFuncSetAttribute((const void*)attn::attn_kernel<2, NB>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, Lt::TOTAL);
-      if (e != hipSuccess) return (int)e;
-      attr = true;
-    }
-    hipLaunchKernelGGL((attn::attn_kernel<2, NB>), dim3(grid), dim3(512), Lt::TOTAL, (hipStream_t)stream, p);
-  } else {
-    constexpr int NB = 6;
-    using Lt = attn::Lds<1, NB>;
-    static bool attr = false;
-    if (!attr) {
-      hipError_t e = hipFuncSetAttribute((const void*)attn::attn_kernel<1, NB>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, Lt::TOTAL);
-      if (e != hipSuccess) return (int)e;
-      attr = true;
-    }
-    hipLaunchKernelGGL((attn::attn_kernel<1, NB>), dim3(grid), dim3(256), Lt::TOTAL, (hipStream_t)stream, p);
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)attn::attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       attn::L_TOTAL);
+    if (e != hipSuccess) return (int)e;
+    attr = true;
   }
+  hipLaunchKernelGGL(attn::attn_kernel, dim3(grid), dim3(256), attn::L_TOTAL, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 

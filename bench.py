@@ -142,7 +142,7 @@ def run_config2(a, dev):
         roof["traffic"] = json.load(open(tf)).get("bytes_per_launch")
     cfg = {"workload": "BASELINE config 2: all-HBM sparse-MLA decode, B=64, H=128, ctx=32768/seq, top-2048, Row656 "
                        "rows, bf16 out + fp32 LSE", "global_batch": B, "heads": H, "ctx": CTX, "topk": K,
-           "row_bytes": ROWB, "idx_sets": a.idx_sets, "attn_teams": kernels._lib.lib().spmla_attn_teams()}
+           "row_bytes": ROWB, "idx_sets": a.idx_sets}
     res = _line(METRIC, gbs, "GB/s", a, ms, "fp8e4m3 rows x bf16 q: bf16 MFMA (QK), f16 MFMA (PV), fp32 accumulate",
                 cfg, roof, step_us=round(ms * 1e3, 2))
     if not a.no_cpu:

@@ -140,9 +140,6 @@ int spmla_lse_merge(const void* parts, int parts_bf16, long long o_ps, long long
 /* Build identification string (static storage). */
 const char* spmla_version(void);
 
-/* Workgroup shape used by spmla_attn_splitk: 1 or 2 teams of 4 waves (env SPMLA_ATTN_TEAMS, default 2). */
-int spmla_attn_teams(void);
-
 /* Host-side self-test hook: the e4m3fn encoder the kernels use, run on the CPU (no GPU call). */
 void spmla_host_e4m3_encode(const float* x, unsigned char* out, long long n);
 
