@@ -367,7 +367,8 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- rows that do not exist: -inf (C-layout row of value i: 8 (i / 4) + 4 half + i % 4)
-    if (vmask != 0xffffffffu) {
+    if (__builtin_expect(vmask != 0xffffffffu, 0)) {     // rare: keep it a branch, not 48 selects per tile
+      asm volatile("" ::: "memory");
       const unsigned lm = vmask >> (4 * half);
 #pragma unroll
       for (int i = 0; i < 16; ++i)
