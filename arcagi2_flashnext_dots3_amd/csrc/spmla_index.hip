@@ -13,9 +13,11 @@
 //   per row, the K largest values among columns j < n = min(ctx, Lc) by torch's order-preserving key
 //   (-0 < +0, NaN largest); equal keys -> lower column first; output positions sorted by (value desc, column asc),
 //   -1 where the value is +-inf and in slots >= n.
-//   gfx950: one 1024-thread workgroup per row: 11/11/10-bit radix passes with an LDS histogram; once the boundary
-//   bin is small it is resolved exactly in LDS (candidate sort), else narrowed further; ties on the final key take
-//   the lowest columns through an ordered block scan. The K winners are bitonic-sorted in LDS.
+//   gfx950: one 1024-thread workgroup per row, the row's keys in VGPRs (32 per thread, all loads in flight):
+//   11/11/10-bit radix levels with an LDS histogram; keys above the boundary bin are appended with one LDS atomic
+//   per wave; once the boundary bin holds at most TK_CAP keys the remaining levels run on those candidates alone;
+//   ties on the final key take the lowest columns. The K winners are bitonic-sorted in LDS (only the stages whose
+//   pairs cross waves take a workgroup barrier).
 #include "spmla_common.h"
 
 namespace spmla {
@@ -172,7 +174,9 @@ __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* wsum, uint32_t*
   return r;
 }
 
-// bitonic sort of n (power of two) uint64 in LDS, descending
+// bitonic sort of n (power of two) uint64 in LDS, descending. Thread t handles pairs t, t + 1024, ...; for a
+// stride <= 64 both elements of its pairs lie in the 128-element block of its wave, so such a stage needs no
+// workgroup barrier (LDS operations of one wave complete in issue order), only a compiler fence.
 __device__ inline void bitonic_desc(unsigned long long* a, int n) {
   for (int size = 2; size <= n; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
@@ -183,13 +187,73 @@ __device__ inline void bitonic_desc(unsigned long long* a, int n) {
         const unsigned long long x = a[lo], y = a[hi];
         if ((x < y) == desc) { a[lo] = y; a[hi] = x; }
       }
-      __syncthreads();
+      const int next = stride > 1 ? stride >> 1 : size;   // stride of the next stage (size << 1 >> 1)
+      if (stride >= 128 || next >= 128) __syncthreads();
+      else __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
   }
+  __syncthreads();
 }
 
-// Candidate sources of one row. n = number of candidates; val(j) = the value of candidate j; id(j) = what the
-// output reports for it. Ties on the key go to the lower candidate number j.
+__device__ inline unsigned long long shfl_xor64(unsigned long long v, int m) {
+  const int lo = __shfl_xor((int)(uint32_t)v, m, 64), hi = __shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+  return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// Bitonic sort of a[0, 2048) descending with the data in VGPRs: thread t of wave w holds elements 128w + l and
+// 128w + 64 + l (l = lane). Stride 64 is an in-thread exchange, strides 1..32 are lane-xor shuffles, and only the
+// strides >= 128 (10 of the 66 stages) go through LDS with workgroup barriers.
+__device__ inline void sort2048_desc(unsigned long long* a) {
+  const int t = threadIdx.x, l = t & 63;
+  const int e0 = 128 * (t >> 6) + l;
+  unsigned long long x0 = a[e0], x1 = a[e0 + 64];
+  for (int size = 2; size <= 2048; size <<= 1) {
+    int stride = size >> 1;
+    if (stride >= 128) {
+      a[e0] = x0;
+      a[e0 + 64] = x1;
+      __syncthreads();
+      for (; stride >= 128; stride >>= 1) {
+        const int lo = 2 * t - (t & (stride - 1)), hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const unsigned long long x = a[lo], y = a[hi];
+        if ((x < y) == desc) { a[lo] = y; a[hi] = x; }
+        __syncthreads();
+      }
+      x0 = a[e0];
+      x1 = a[e0 + 64];
+    }
+    if (stride == 64) {
+      const bool desc = (e0 & size) == 0;
+      if ((x0 < x1) == desc) { const unsigned long long tmp = x0; x0 = x1; x1 = tmp; }
+      stride = 32;
+    }
+    const bool d0 = (e0 & size) == 0, d1 = ((e0 + 64) & size) == 0;
+    for (; stride > 0; stride >>= 1) {
+      const unsigned long long y0 = shfl_xor64(x0, stride), y1 = shfl_xor64(x1, stride);
+      const bool lower = (l & stride) == 0;
+      // the lower element of a pair keeps the max when descending, the upper one the min (and the reverse)
+      x0 = ((lower == d0) == (x0 > y0)) ? x0 : y0;
+      x1 = ((lower == d1) == (x1 > y1)) ? x1 : y1;
+    }
+  }
+  __syncthreads();                                   // every thread has read a: write the sorted data back
+  a[e0] = x0;
+  a[e0 + 64] = x1;
+  __syncthreads();
+}
+
+// Sorts a[0, n) descending (entries are nonzero); pads with zeros to the sorting network's size.
+__device__ inline void tk_sort_desc(unsigned long long* a, int n) {
+  int np2 = 1;
+  while (np2 < n) np2 <<= 1;
+  if (np2 > 256 && np2 <= 2048) np2 = 2048;
+  for (int i = n + (int)threadIdx.x; i < np2; i += TK_NT) a[i] = 0ull;
+  __syncthreads();
+  if (np2 == 2048) sort2048_desc(a);
+  else if (np2 > 1) bitonic_desc(a, np2);
+}
+
 struct RowSrc {     // a logits row: candidate j = column j
   const float* x; int n;
   __device__ float val(int j) const { return x[j]; }
@@ -206,8 +270,13 @@ struct MergeSrc {   // all-gathered payloads [P][nrows][2 * kl] = [values | posi
   __device__ int id(int c) const { int i; const float* b = seg(c, i); return (int)f2u(b[kl + i]); }
 };
 
+// Four copies of the 2048-bin histogram (lane & 3 picks one) split same-bin atomics of a wave four ways; a copy
+// stride of 2049 words keeps the copies of a bin in different banks.
+constexpr int TK_HCOPY = 4;
+constexpr int TK_HSTR = 2049;
+
 struct TopkLds {
-  uint32_t hist[2048];
+  uint32_t hist[TK_HCOPY * TK_HSTR];
   unsigned long long sel[TK_KMAX];
   unsigned long long cand[TK_CAP];
   uint32_t wsum[17];
@@ -218,128 +287,220 @@ __device__ inline unsigned long long tk_pack(uint32_t key, int j) {
   return ((unsigned long long)key << 32) | (uint32_t)(~(uint32_t)j);
 }
 
-// Selects the K largest candidates (key desc, j asc) of src into L.sel (unordered); returns their number min(n, K).
+__device__ inline void tk_hist_add(TopkLds& L, uint32_t bin) {
+  atomicAdd(&L.hist[(threadIdx.x & (TK_HCOPY - 1)) * TK_HSTR + bin], 1u);
+}
+
+// Radix level bookkeeping: digit d = (key >> shift) & dm of the keys under (prefix, mask).
+__device__ inline int tk_shift(int level) { return level == 0 ? 21 : (level == 1 ? 10 : 0); }
+__device__ inline uint32_t tk_dmask(int level) { return level == 2 ? 0x3ffu : 0x7ffu; }
+
+// From the level's histogram: the boundary bin b holding the need-th largest key, the count above it and in it.
+__device__ inline void tk_bin(TopkLds& L, uint32_t need, uint32_t& b, uint32_t& above, uint32_t& binc) {
+  const int tid = threadIdx.x;
+  const int b0 = 2047 - 2 * tid, b1 = b0 - 1;   // thread t owns bins 2047 - 2t, 2046 - 2t (descending)
+  uint32_t h0 = 0, h1 = 0;
+#pragma unroll
+  for (int c = 0; c < TK_HCOPY; ++c) { h0 += L.hist[c * TK_HSTR + b0]; h1 += L.hist[c * TK_HSTR + b1]; }
+  uint32_t tot;
+  const uint32_t before = block_excl_scan(h0 + h1, L.wsum, &tot);
+  if (before < need && before + h0 >= need) { L.sh[1] = (uint32_t)b0; L.sh[2] = before; L.sh[3] = h0; }
+  if (before + h0 < need && before + h0 + h1 >= need) { L.sh[1] = (uint32_t)b1; L.sh[2] = before + h0; L.sh[3] = h1; }
+  __syncthreads();
+  b = L.sh[1]; above = L.sh[2]; binc = L.sh[3];
+}
+
+__device__ inline void tk_clear_hist(TopkLds& L) {
+  for (int i = threadIdx.x; i < TK_HCOPY * TK_HSTR; i += TK_NT) L.hist[i] = 0;
+  __syncthreads();
+}
+
+// Block-wide placement of per-thread selections: each thread passes how many entries it appends to sel and to cand;
+// returns its first slot in each (after the bases *sb, *cb, which advance by the block totals on every thread).
+__device__ inline void tk_slots(uint32_t ns, uint32_t nc, TopkLds& L, uint32_t& sb, uint32_t& cb, uint32_t& so,
+                                uint32_t& co) {
+  uint32_t tot;
+  const uint32_t off = block_excl_scan(ns | (nc << 16), L.wsum, &tot);   // both totals < 65536
+  so = sb + (off & 0xffffu);
+  co = cb + (off >> 16);
+  sb += tot & 0xffffu;
+  cb += tot >> 16;
+}
+
+constexpr int TK_KPT = 32;                 // keys per thread per chunk (held in VGPRs)
+constexpr int TK_CH = TK_KPT * TK_NT;      // 32768 columns per chunk
+constexpr int TK_EPT = TK_CAP / TK_NT;     // boundary-bin candidates per thread
+
 template <class Src>
-__device__ int tk_select(const Src& src, int K, TopkLds& L) {
+__device__ inline void tk_load(const Src& src, int base, uint32_t (&k)[TK_KPT]) {
+#pragma unroll
+  for (int i = 0; i < TK_KPT; ++i) {
+    const int j = base + i * TK_NT + (int)threadIdx.x;
+    k[i] = j < src.n ? okey(src.val(j)) : 0u;
+  }
+}
+
+// Finishes a selection from the boundary-bin candidates L.cand[0, nc) (all under (prefix, mask) of level lvl - 1):
+// radix levels lvl..2 on the candidates held in registers; equal final keys go to the lowest columns. sb = entries
+// already in L.sel.
+__device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, uint32_t prefix, uint32_t mask,
+                                                 uint32_t need, uint32_t sb) {
+  const int tid = threadIdx.x;
+  unsigned long long e[TK_EPT];
+  uint32_t vm = 0;                                   // bit i: e[i] is a candidate
+  int t = tid;                                       // opaque copy: keeps the slot indices from being hoisted
+  asm volatile("" : "+v"(t));
+#pragma unroll
+  for (int i = 0; i < TK_EPT; ++i) {
+    const int c = t + i * TK_NT;
+    vm |= (uint32_t)(c < nc) << i;
+    e[i] = c < nc ? L.cand[c] : 0ull;
+  }
+  for (int level = lvl; level < 3; ++level) {
+    const int shift = tk_shift(level);
+    const uint32_t dm = tk_dmask(level);
+    tk_clear_hist(L);
+#pragma unroll
+    for (int i = 0; i < TK_EPT; ++i) {
+      const uint32_t k = (uint32_t)(e[i] >> 32);
+      if (((vm >> i) & 1u) && (k & mask) == prefix) tk_hist_add(L, (k >> shift) & dm);
+    }
+    __syncthreads();
+    uint32_t b, above, binc;
+    tk_bin(L, need, b, above, binc);
+    const bool whole = above + binc == need;
+    uint32_t selm = 0;
+#pragma unroll
+    for (int i = 0; i < TK_EPT; ++i) {
+      const uint32_t k = (uint32_t)(e[i] >> 32);
+      const uint32_t d = (k >> shift) & dm;
+      const bool in = ((vm >> i) & 1u) && (k & mask) == prefix;
+      selm |= (uint32_t)(in && (d > b || (whole && d == b))) << i;
+    }
+    uint32_t cb = 0, so, co;
+    tk_slots(__popc(selm), 0u, L, sb, cb, so, co);
+#pragma unroll
+    for (int i = 0; i < TK_EPT; ++i)
+      if ((selm >> i) & 1u) L.sel[so++] = e[i];
+    if (whole) { __syncthreads(); return; }
+    prefix |= b << shift;
+    mask |= dm << shift;
+    need -= above;
+    if (level == 2) {
+      // binc candidates carry the final key; the need lowest columns win: sort them by column ascending
+      uint32_t eqm = 0;
+#pragma unroll
+      for (int i = 0; i < TK_EPT; ++i)
+        eqm |= (uint32_t)(((vm >> i) & 1u) && (uint32_t)(e[i] >> 32) == prefix) << i;
+      __syncthreads();                             // every thread has read its candidates: L.cand is free
+      uint32_t cb2 = 0, sb2 = 0;
+      tk_slots(0u, __popc(eqm), L, sb2, cb2, so, co);
+#pragma unroll
+      for (int i = 0; i < TK_EPT; ++i)
+        if ((eqm >> i) & 1u) L.cand[co++] = (unsigned long long)(uint32_t)e[i] << 32;   // ~j high: desc = j asc
+      __syncthreads();
+      tk_sort_desc(L.cand, (int)binc);
+      for (uint32_t i = tid; i < need; i += TK_NT) L.sel[sb + i] = (((unsigned long long)prefix) << 32) | (L.cand[i] >> 32);
+      __syncthreads();
+      return;
+    }
+  }
+}
+
+// Selects the K largest candidates (key desc, j asc) of src into L.sel (unordered); returns their number min(n, K).
+// The row's keys sit in VGPRs (32 per thread; longer rows are re-read per 32768-column chunk with all loads of a
+// chunk in flight). Each radix level builds an LDS histogram; the keys above the boundary bin are written to slots
+// from one block scan of per-thread counts; a boundary bin of at most TK_CAP keys is finished on the candidates alone.
+template <class Src>
+__device__ __forceinline__ int tk_select(const Src& src, int K, TopkLds& L) {
   const int tid = threadIdx.x, n = src.n;
-  uint32_t* hist = L.hist;
-  unsigned long long* sel = L.sel;
-  unsigned long long* cand = L.cand;
-  uint32_t* sh = L.sh;
   if (n <= K) {
-    for (int j = tid; j < n; j += TK_NT) sel[j] = tk_pack(okey(src.val(j)), j);
+    for (int j = tid; j < n; j += TK_NT) L.sel[j] = tk_pack(okey(src.val(j)), j);
     __syncthreads();
     return n;
   }
-  if (tid == 0) sh[0] = 0;   // sel fill counter
-  uint32_t prefix = 0, mask = 0;
-  uint32_t need = (uint32_t)K;
-  bool done = false;
-  for (int pass = 0; pass < 3 && !done; ++pass) {
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const uint32_t dm = pass == 2 ? 0x3ffu : 0x7ffu;
-    for (int i = tid; i < 2048; i += TK_NT) hist[i] = 0;
-    __syncthreads();
-    for (int j = tid; j < n; j += TK_NT) {
-      const uint32_t k = okey(src.val(j));
-      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & dm], 1u);
+  const int nch = (n + TK_CH - 1) / TK_CH;
+  uint32_t key[TK_KPT];
+  if (nch == 1) tk_load(src, 0, key);
+  uint32_t prefix = 0, mask = 0, need = (uint32_t)K, sb = 0;
+  for (int level = 0; level < 3; ++level) {
+    const int shift = tk_shift(level);
+    const uint32_t dm = tk_dmask(level);
+    // the column of key[i] is recomputed per level from an opaque copy of tid: hoisting the 32 columns (and the
+    // packed entries built from them) out of the level loop would spill them
+    int t = tid;
+    asm volatile("" : "+v"(t));
+    tk_clear_hist(L);
+    for (int c = 0; c < nch; ++c) {
+      if (nch > 1) tk_load(src, c * TK_CH, key);
+#pragma unroll
+      for (int i = 0; i < TK_KPT; ++i) {
+        const int j = c * TK_CH + i * TK_NT + t;
+        if (j < n && (key[i] & mask) == prefix) tk_hist_add(L, (key[i] >> shift) & dm);
+      }
     }
     __syncthreads();
-    // thread t owns the two bins 2047 - 2t, 2046 - 2t (descending); suffix counts by a block scan
-    const int b0 = 2047 - 2 * tid, b1 = b0 - 1;
-    const uint32_t h0 = hist[b0], h1 = hist[b1];
-    uint32_t tot;
-    const uint32_t before = block_excl_scan(h0 + h1, L.wsum, &tot);
-    if (before < need && before + h0 >= need) { sh[1] = (uint32_t)b0; sh[2] = before; sh[3] = h0; }
-    if (before + h0 < need && before + h0 + h1 >= need) { sh[1] = (uint32_t)b1; sh[2] = before + h0; sh[3] = h1; }
-    __syncthreads();
-    const uint32_t b = sh[1], above = sh[2], binc = sh[3];
-    const uint32_t pmask = mask, pprefix = prefix;
-    const uint32_t np = prefix | (b << shift), nm = mask | (dm << shift);
-    // elements under the current prefix whose digit is above b are selected
+    uint32_t b, above, binc;
+    tk_bin(L, need, b, above, binc);
     const bool whole = above + binc == need;
-    const bool fits = binc <= TK_CAP;
-    const bool last = pass == 2;
-    if (whole || fits || last) {
-      if (tid == 0) sh[4] = 0;   // cand counter
-      __syncthreads();
-      for (int j = tid; j < n; j += TK_NT) {
-        const uint32_t k = okey(src.val(j));
-        if ((k & pmask) != pprefix) continue;
-        const uint32_t d = (k >> shift) & dm;
-        if (d > b || (whole && d == b)) {
-          const uint32_t s = atomicAdd(&sh[0], 1u);
-          sel[s] = tk_pack(k, j);
-        } else if (d == b && fits && !whole) {
-          const uint32_t s = atomicAdd(&sh[4], 1u);
-          cand[s] = tk_pack(k, j);
-        }
+    const bool fits = !whole && level < 2 && binc <= (uint32_t)TK_CAP;
+    uint32_t cb = 0;
+    for (int c = 0; c < nch; ++c) {
+      if (nch > 1) tk_load(src, c * TK_CH, key);
+      uint32_t selm = 0, candm = 0;
+#pragma unroll
+      for (int i = 0; i < TK_KPT; ++i) {
+        const int j = c * TK_CH + i * TK_NT + t;
+        const uint32_t d = (key[i] >> shift) & dm;
+        const bool in = j < n && (key[i] & mask) == prefix;
+        selm |= (uint32_t)(in && (d > b || (whole && d == b))) << i;
+        candm |= (uint32_t)(fits && in && d == b) << i;
       }
-      __syncthreads();
-      if (whole) {
-        done = true;
-      } else if (fits) {
-        // resolve inside the boundary bin: sort candidates, keep the first need - above
-        const int nc = (int)sh[4];
-        int np2 = 1;
-        while (np2 < nc) np2 <<= 1;
-        for (int i = nc + tid; i < np2; i += TK_NT) cand[i] = 0ull;
-        __syncthreads();
-        bitonic_desc(cand, np2);
-        const uint32_t take = need - above;
-        const uint32_t base = sh[0];
-        for (uint32_t i = tid; i < take; i += TK_NT) sel[base + i] = cand[i];
-        __syncthreads();
-        if (tid == 0) sh[0] = base + take;
-        done = true;
-      } else {
-        // last pass, boundary key fully known: take the lowest candidates equal to it (ordered scan)
-        const uint32_t T = np;
-        const uint32_t take = need - above;
-        uint32_t got = 0;
-        const uint32_t base = sh[0];
-        __syncthreads();
-        for (int j0 = 0; j0 < n && got < take; j0 += TK_NT) {
-          const int j = j0 + tid;
-          const bool eq = j < n && okey(src.val(j)) == T;
-          uint32_t tot2;
-          const uint32_t r = block_excl_scan(eq ? 1u : 0u, L.wsum, &tot2);
-          if (eq && got + r < take) sel[base + got + r] = tk_pack(T, j);
-          got += tot2;
-        }
-        __syncthreads();
-        if (tid == 0) sh[0] = base + take;
-        done = true;
+      uint32_t so, co;
+      tk_slots(__popc(selm), __popc(candm), L, sb, cb, so, co);
+#pragma unroll
+      for (int i = 0; i < TK_KPT; ++i) {
+        const int j = c * TK_CH + i * TK_NT + t;
+        if ((selm >> i) & 1u) L.sel[so++] = tk_pack(key[i], j);
+        if ((candm >> i) & 1u) L.cand[co++] = tk_pack(key[i], j);
       }
-    } else {
-      // narrow: everything above the bin is selected now, continue inside the bin
-      for (int j = tid; j < n; j += TK_NT) {
-        const uint32_t k = okey(src.val(j));
-        if ((k & pmask) != pprefix) continue;
-        if (((k >> shift) & dm) > b) {
-          const uint32_t s = atomicAdd(&sh[0], 1u);
-          sel[s] = tk_pack(k, j);
-        }
-      }
-      prefix = np;
-      mask = nm;
-      need -= above;
     }
     __syncthreads();
+    if (whole) return K;
+    if (fits) {
+      tk_resolve_cands(L, (int)binc, level + 1, prefix | (b << shift), mask | (dm << shift), need - above, sb);
+      return K;
+    }
+    prefix |= b << shift;
+    mask |= dm << shift;
+    need -= above;
   }
+  // the boundary key is fully known (prefix); the need lowest columns holding it win, in column order
+  uint32_t got = 0;
+  for (int c = 0; c < nch && got < need; ++c) {
+    if (nch > 1) tk_load(src, c * TK_CH, key);
+#pragma unroll
+    for (int i = 0; i < TK_KPT; ++i) {
+      if (got < need) {                          // uniform: got is a block-wide total
+        const int j = c * TK_CH + i * TK_NT + tid;
+        const bool eq = j < n && key[i] == prefix;
+        uint32_t tot;
+        const uint32_t r = block_excl_scan(eq ? 1u : 0u, L.wsum, &tot);
+        if (eq && got + r < need) L.sel[sb + got + r] = tk_pack(prefix, j);
+        got += tot;
+      }
+    }
+  }
+  __syncthreads();
   return K;
 }
 
 // Sorts the nsel selected entries by (key desc, j asc) and writes src.id of the first kout slots to o
 // (-1 where the value is +-inf and for slots >= nsel).
 template <class Src>
-__device__ void tk_emit_sorted(const Src& src, int nsel, int kout, int* o, TopkLds& L) {
+__device__ __forceinline__ void tk_emit_sorted(const Src& src, int nsel, int kout, int* o, TopkLds& L) {
   const int tid = threadIdx.x;
-  int np2 = 1;
-  while (np2 < nsel) np2 <<= 1;
-  for (int i = nsel + tid; i < np2; i += TK_NT) L.sel[i] = 0ull;
-  __syncthreads();
-  if (np2 > 1) bitonic_desc(L.sel, np2);
+  tk_sort_desc(L.sel, nsel);
   for (int s = tid; s < kout; s += TK_NT) {
     int r = -1;
     if (s < nsel) {
@@ -387,16 +548,9 @@ __global__ void __launch_bounds__(TK_NT) topk_local_kernel(LocalParams p) {
   if (n > p.Lc) n = p.Lc;
   const RowSrc src{p.lg + (long long)row * p.lg_st, n};
   const int nsel = tk_select(src, p.kl, L);
-  // ascending column order: sort descending on ~j
-  int np2 = 1;
-  while (np2 < nsel) np2 <<= 1;
-  for (int i = tid; i < np2; i += TK_NT) {
-    unsigned long long e = 0ull;
-    if (i < nsel) e = (unsigned long long)(uint32_t)L.sel[i] << 32;   // low word of a selected entry is ~j
-    L.sel[i] = e;
-  }
-  __syncthreads();
-  if (np2 > 1) bitonic_desc(L.sel, np2);
+  // ascending column order: sort descending on ~j (the low word of a selected entry)
+  for (int i = tid; i < nsel; i += TK_NT) L.sel[i] = (unsigned long long)(uint32_t)L.sel[i] << 32;
+  tk_sort_desc(L.sel, nsel);
   float* pv = p.pk + (long long)row * 2 * p.kl;
   int* pp = reinterpret_cast<int*>(pv + p.kl);
   for (int s = tid; s < p.kl; s += TK_NT) {
