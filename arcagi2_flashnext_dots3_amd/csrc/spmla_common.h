@@ -98,4 +98,32 @@ enum : int {
   SPMLA_ELIMIT = -5,    // size beyond what the kernel supports
 };
 
+// ---- LDS DMA and hand-counted waits (shared by the attention and indexer kernels) ----------------------------
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"   // m0 is reserved; nothing else in these kernels uses it
+// Direct global->LDS copy (lane l's 16 bytes land at lds + 16 * l). Issued through inline asm so that the
+// compiler does not track it: it would otherwise drain every outstanding copy (vmcnt(0)) at the first
+// s_waitcnt it places for its own loads. Completion is tracked by hand with wait_vm<>(). The LDS destination is
+// wave-uniform; readfirstlane pins it to an SGPR for m0; one wait state separates the m0 write from the
+// LDS-DMA instruction that reads it (an SALU m0 write -> LDS DMA hazard the assembler does not resolve).
+__device__ inline void dma16(const void* g, SPMLA_LDS void* l) {
+  const uint32_t a = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)l);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(a) : "memory", "m0");
+}
+__device__ inline void dma4(const void* g, SPMLA_LDS void* l) {
+  const uint32_t a = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)l);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(a) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Workgroup barrier for data exchanged through LDS only (no vector-memory drain).
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// vmcnt-only wait (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 }  // namespace spmla

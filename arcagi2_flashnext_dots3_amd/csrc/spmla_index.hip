@@ -19,13 +19,14 @@
 //   ties on the final key take the lowest columns. The K winners are bitonic-sorted in LDS (only the stages whose
 //   pairs cross waves take a workgroup barrier).
 #include "spmla_common.h"
+#include <limits.h>
 
 namespace spmla {
 namespace idx {
 
 // ------------------------------------------------------------------------------------------------ logits
-constexpr int LG_TPW = 4;   // 32-key tiles per wave
-constexpr int LG_KPB = 4 * LG_TPW * 32;   // keys per 256-thread block
+constexpr int LG_TPW = 8;                 // 32-key tiles per wave
+constexpr int LG_KPB = 4 * LG_TPW * 32;   // keys per 4-wave workgroup
 
 struct LogitParams {
   const uint16_t* q; long long q_st, q_sh;   // q[row][64][128] bf16
@@ -35,6 +36,8 @@ struct LogitParams {
   const int* req; const int* ctx;            // per row
   int rows, Lc, P, rank, noinf;
   float* out; long long out_st;
+  int bs_sh, rpb_sh, p_sh;                   // log2 of bs, rpb, P when a power of two, else -1
+  long long lim;                             // R_local * P (< 2^31): valid block-table positions lie below
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -45,19 +48,85 @@ __device__ inline uint32_t fp8hi_bf16x2(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
 }
 
+// Logits workgroup: 4 independent waves, wave w computing all 64 heads for keys j_blk + 256w + [0, 256) in eight
+// 32-key tiles. Per tile the key codes (32 rows x 128 B, 16-byte chunks XOR-swizzled by row so the MFMA operand
+// reads are bank-conflict free), the key scales and the block-table entries are copied global -> LDS by LDS DMA
+// into the wave's private rings: the codes of tiles t + 1 and t + 2 and the block-table entries of tiles t + 3 and
+// t + 4 are in flight while tile t is computed. Completion is counted by hand (no other global load in the loop),
+// and no wave waits for another.
+constexpr int LG_NBUF = 3;                  // code / scale ring depth
+constexpr int LG_NBT = 4;                   // block-table ring depth
+constexpr int LG_CODES = 32 * 128;
+constexpr int LG_OFF_SC = LG_NBUF * LG_CODES;
+constexpr int LG_OFF_BT = LG_OFF_SC + LG_NBUF * 128;
+constexpr int LG_WAVE = LG_OFF_BT + LG_NBT * 128;   // LDS bytes per wave
+constexpr int LG_WAVES = 4;
+
+template <bool POW2>
 __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LG_WAVES * LG_WAVE];
   const int row = blockIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  SPMLA_LDS uint8_t* lds = (SPMLA_LDS uint8_t*)lds_raw + wv * LG_WAVE;
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5, l32 = lane & 31;
   const int ctx = p.ctx[row];
-  const int j_blk = blockIdx.y * LG_KPB;
+  const int j_wv = blockIdx.y * LG_KPB + wv * LG_TPW * 32;   // first key of this wave
   float* orow = p.out + (long long)row * p.out_st;
-  if ((long long)j_blk * p.P + p.rank >= ctx) {   // whole block beyond the context
+  if (j_wv >= p.Lc) return;
+  const int nt = min(LG_TPW, (p.Lc - j_wv + 31) >> 5);        // tiles of this wave (uniform)
+  if ((long long)j_wv * p.P + p.rank >= ctx || p.lim == 0) {   // no key of this wave has a row
     if (!p.noinf)
-      for (int j = j_blk + threadIdx.x; j < j_blk + LG_KPB && j < p.Lc; j += 256) orow[j] = -__builtin_inff();
+      for (int j = j_wv + lane; j < j_wv + 32 * nt && j < p.Lc; j += 64) orow[j] = -__builtin_inff();
     return;
   }
+  const int* btr = p.bt + (long long)p.req[row] * p.bt_st;
+  // n / d, n % d: shifts when every divisor is a power of two (POW2), else 32-bit division
+  auto dv = [&](uint32_t n, uint32_t d, int sh) -> uint32_t { return POW2 ? n >> sh : n / d; };
+  auto md = [&](uint32_t n, uint32_t d, int sh) -> uint32_t { return POW2 ? n & (d - 1u) : n % d; };
+  // positions without a block-table entry read the wave's first entry (in range)
+  const int* bt_dummy = btr + dv((uint32_t)(j_wv * p.P + p.rank), (uint32_t)p.bs, p.bs_sh);
+  auto key_pos = [&](int t, int r, uint32_t& pos) -> bool {
+    const int j = j_wv + 32 * t + r;
+    const long long ps = (long long)j * p.P + p.rank;
+    pos = (uint32_t)ps;
+    return t < nt && j < p.Lc && ps < ctx;
+  };
+  // LDS DMA of the block-table entries of tile t (lanes 0..31: key l32)
+  auto issue_bt = [&](int t) {
+    if (lane < 32) {
+      uint32_t pos;
+      const bool in = key_pos(t, l32, pos);
+      dma4(in ? btr + dv(pos, (uint32_t)p.bs, p.bs_sh) : bt_dummy, lds + LG_OFF_BT + (t & (LG_NBT - 1)) * 128);
+    }
+  };
+  // LDS DMA of the codes and scales of tile t (its block-table entries already in LDS). Lane l32 maps key l32 to
+  // its row; the copying lanes take the row addresses from those lanes. Returns the lane's key-valid flag.
+  auto issue_codes = [&](int t) -> bool {
+    const int blk = ((const SPMLA_LDS int*)(lds + LG_OFF_BT + (t & (LG_NBT - 1)) * 128))[l32];
+    uint32_t pos;
+    bool ok = key_pos(t, l32, pos) && blk >= 0;
+    const long long tt = (long long)blk * p.bs + md(pos, (uint32_t)p.bs, p.bs_sh);
+    ok = ok && tt < p.lim;
+    const uint32_t lrow = ok ? dv((uint32_t)tt, (uint32_t)p.P, p.p_sh) : 0u;   // p.lim > 0: row 0 exists
+    const uint8_t* rp = p.store + (long long)dv(lrow, (uint32_t)p.rpb, p.rpb_sh) * p.blk_stride +
+                        md(lrow, (uint32_t)p.rpb, p.rpb_sh) * 132u;
+    const long long ra = (long long)(uintptr_t)rp;
+    SPMLA_LDS uint8_t* cb = lds + (t % LG_NBUF) * LG_CODES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 8 * i + (lane >> 3);
+      const int c = (lane & 7) ^ (r & 7);               // chunk that lands in 16-byte slot lane & 7 of row r
+      const long long a = __shfl(ra, r, 64);
+      dma16((const uint8_t*)(uintptr_t)a + 16 * c, cb + 8 * i * 128);
+    }
+    if (lane < 32) dma4(rp + 128, lds + LG_OFF_SC + (t % LG_NBUF) * 128);
+    return ok;
+  };
+
+  // prologue: block-table entries of tiles 0..3 (waited for), then the codes of tiles 0 and 1; the query loads
+  // overlap the copies
+  for (int t = 0; t < LG_NBT; ++t) issue_bt(t);
   // query fragments (bf16 A operand): M block m = heads 32m..32m+31 (lane head 32m + l32); k-pair kp covers dims
   // 32kp + 16half + 0..15, MFMA 2kp taking the first 8 and 2kp+1 the next 8 (same permutation as the key operand)
   const uint16_t* qr = p.q + (long long)row * p.q_st;
@@ -76,61 +145,65 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) wl[m][i] = __shfl(myw, 8 * (i >> 2) + 4 * half + (i & 3), 64);
   }
-  const int* btr = p.bt + (long long)p.req[row] * p.bt_st;
+  wait_vm<0>();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // DMA'd entries read below after the wait
+  bool ok0 = issue_codes(0);
+  bool ok1 = issue_codes(1);
+  int nprev = 5;                                            // copies issued by the previous step
+
 #pragma unroll 1
-  for (int tt = 0; tt < LG_TPW; ++tt) {
-    const int j0 = j_blk + (wave * LG_TPW + tt) * 32;
-    if (j0 >= p.Lc) break;
-    const int j = j0 + l32;
-    const long long pos = (long long)j * p.P + p.rank;
-    bool ok = j < p.Lc && pos < ctx;
-    long long lrow = 0;
-    if (ok) {
-      const int blk = btr[pos / p.bs];
-      lrow = ((long long)blk * p.bs + pos % p.bs) / p.P;
-      ok = blk >= 0 && lrow < p.R_local;
-    }
-    const uint8_t* kr = p.store + (ok ? (lrow / p.rpb) * p.blk_stride + (lrow % p.rpb) * 132 : 0);
-    uint32_t kw[4][4];
-    float ksc = 0.f;
-    if (ok) {
-#pragma unroll
-      for (int kp = 0; kp < 4; ++kp)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kw[kp][i] = *(const uint32_t*)(kr + 32 * kp + 16 * half + 4 * i);
-      ksc = *(const float*)(kr + 128);
-    } else {
-#pragma unroll
-      for (int kp = 0; kp < 4; ++kp)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kw[kp][i] = 0u;
-    }
+  for (int t = 0; t < nt; ++t) {
+    // codes / scales of tile t and block-table entries of tile t + 2 are complete once at most the previous
+    // step's copies are outstanding
+    if (nprev == 6) wait_vm<6>();
+    else if (nprev == 5) wait_vm<5>();
+    else wait_vm<0>();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    bool ok2 = false;
+    nprev = 0;
+    if (t + 2 < nt) { ok2 = issue_codes(t + 2); nprev = 5; }
+    if (t + 4 < nt) { issue_bt(t + 4); nprev += 1; }
+    // tile t
+    const SPMLA_LDS uint8_t* cb = lds + (t % LG_NBUF) * LG_CODES + l32 * 128;
     bf16x8 kb[8];
 #pragma unroll
     for (int kp = 0; kp < 4; ++kp) {
+      const u32x4 w4 = *(const SPMLA_LDS u32x4*)(cb + 16 * ((2 * kp + half) ^ (l32 & 7)));
       i32x4 a0, a1;
-      a0[0] = (int)fp8lo_bf16x2(kw[kp][0]); a0[1] = (int)fp8hi_bf16x2(kw[kp][0]);
-      a0[2] = (int)fp8lo_bf16x2(kw[kp][1]); a0[3] = (int)fp8hi_bf16x2(kw[kp][1]);
-      a1[0] = (int)fp8lo_bf16x2(kw[kp][2]); a1[1] = (int)fp8hi_bf16x2(kw[kp][2]);
-      a1[2] = (int)fp8lo_bf16x2(kw[kp][3]); a1[3] = (int)fp8hi_bf16x2(kw[kp][3]);
+      a0[0] = (int)fp8lo_bf16x2(w4[0]); a0[1] = (int)fp8hi_bf16x2(w4[0]);
+      a0[2] = (int)fp8lo_bf16x2(w4[1]); a0[3] = (int)fp8hi_bf16x2(w4[1]);
+      a1[0] = (int)fp8lo_bf16x2(w4[2]); a1[1] = (int)fp8hi_bf16x2(w4[2]);
+      a1[2] = (int)fp8lo_bf16x2(w4[3]); a1[3] = (int)fp8hi_bf16x2(w4[3]);
       kb[2 * kp] = __builtin_bit_cast(bf16x8, a0);
       kb[2 * kp + 1] = __builtin_bit_cast(bf16x8, a1);
     }
-    float part = 0.f;
+    const float sc = *(const SPMLA_LDS float*)(lds + LG_OFF_SC + (t % LG_NBUF) * 128 + 4 * l32);
+    f32x16 acc0 = f32x16{}, acc1 = f32x16{};
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      f32x16 acc = f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[m][ks], kb[ks], acc, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) part = __builtin_fmaf(wl[m][i], fmaxf(acc[i], 0.f), part);
+    for (int ks = 0; ks < 8; ++ks) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[0][ks], kb[ks], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[1][ks], kb[ks], acc1, 0, 0, 0);
     }
+    // relu as an integer max on the bit pattern (one instruction; fmaxf would also canonicalize its operand):
+    // non-negative floats keep their value, negative ones (sign bit set: negative as int) become +0
+    // (elements are copied out first: __builtin_bit_cast on an ext_vector element subscript reads element 0)
+    float pa = 0.f, pb = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float s0 = acc0[i], s1 = acc1[i];
+      pa = __builtin_fmaf(wl[0][i], __builtin_bit_cast(float, max(__builtin_bit_cast(int, s0), 0)), pa);
+      pb = __builtin_fmaf(wl[1][i], __builtin_bit_cast(float, max(__builtin_bit_cast(int, s1), 0)), pb);
+    }
+    float part = pa + pb;
     part += __shfl_xor(part, 32, 64);
+    const int j = j_wv + 32 * t + l32;
     if (half == 0 && j < p.Lc) {
-      const float lg = fminf(part * ksc, 60000.f);
-      if (ok) orow[j] = lg;
+      const float lg = fminf(part * sc, 60000.f);
+      if (ok0) orow[j] = lg;
       else if (!p.noinf) orow[j] = -__builtin_inff();
     }
+    ok0 = ok1;
+    ok1 = ok2;
   }
 }
 
@@ -625,6 +698,7 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
   if (rows < 0 || Lc < 0 || P <= 0 || rank < 0 || rank >= P || block_size <= 0 || rows_per_block <= 0) return SPMLA_EARG;
   if (rows == 0 || Lc == 0) return SPMLA_OK;
   if (H != 64 || D != 128) return SPMLA_ELIMIT;
+  if (R_local < 0 || R_local > (long long)INT_MAX / P) return SPMLA_ELIMIT;   // 32-bit row arithmetic
   if (!q || !w || !store || !block_table || !req || !ctx || !out) return SPMLA_EARG;
   if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)store & 3) || (block_stride & 3))
     return SPMLA_EALIGN;
@@ -633,8 +707,14 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
   p.store = (const uint8_t*)store; p.R_local = R_local; p.rpb = rows_per_block; p.blk_stride = block_stride;
   p.bt = block_table; p.bt_st = bt_st; p.bs = block_size; p.req = req; p.ctx = ctx;
   p.rows = rows; p.Lc = Lc; p.P = P; p.rank = rank; p.noinf = noinf; p.out = out; p.out_st = out_st;
+  auto log2_or = [](long long v) { return (v & (v - 1)) == 0 ? __builtin_ctzll((unsigned long long)v) : -1; };
+  p.bs_sh = log2_or(block_size); p.rpb_sh = log2_or(rows_per_block); p.p_sh = log2_or(P);
+  p.lim = R_local * P;
   dim3 grid(rows, (Lc + idx::LG_KPB - 1) / idx::LG_KPB);
-  hipLaunchKernelGGL(idx::logits_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+  if (p.bs_sh >= 0 && p.rpb_sh >= 0 && p.p_sh >= 0)
+    hipLaunchKernelGGL(idx::logits_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(idx::logits_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 
