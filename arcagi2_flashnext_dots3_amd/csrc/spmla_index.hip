@@ -4,9 +4,10 @@
 // dotsnote/training/finetune/student.py:219-222):
 //   logit[row][j] = min(sum_h w[row][h] * relu(q[row][h] . kcode[j]) * ks[j], 60000) for positions j < ctx[row]
 //   (column j holds position j * P + rank of this rank's key store), -inf for j >= ctx (unless noinf).
-//   gfx950: one wave per 32-key tile; S = Q K^T on bf16 MFMA (32x32x16; e4m3 key codes convert exactly to bf16,
-//   two per instruction), 64 heads = 2 M blocks, keys as the B operand; the head reduction is in-lane plus one
-//   cross-half exchange. (The fp8 MFMA would take the codes directly, but its internal accumulation keeps only
+//   gfx950: each wave streams 8 tiles of 32 keys through a private LDS ring filled by LDS DMA (codes, scales and
+//   block-table entries; two tiles in flight); S = Q K^T on bf16 MFMA (32x32x16; e4m3 key codes convert exactly to
+//   bf16, two per instruction), 64 heads = 2 M blocks, keys as the B operand; the head reduction is in-lane plus
+//   one cross-half exchange. (The fp8 MFMA would take the codes directly, but its internal accumulation keeps only
 //   ~2^-12 of the largest product on gfx950, too coarse for the selection.)
 //
 // Top-k (dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:1-15, csrc/topk_select.cu:1-30 semantics):

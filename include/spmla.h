@@ -43,7 +43,8 @@ int spmla_index_key_write(const void* k, long long k_st, const long long* slots,
 /* Indexer logits: out[row][j] = min(sum_h w[row][h] * relu(q[row][h] . kcode) * kscale, 60000) for the key at
  * position pos = j * P + rank < ctx[row] (located through block_table[req[row]][pos / block_size]), -inf for
  * pos >= ctx (columns j < Lc; noinf != 0 leaves tiles wholly beyond ctx unwritten). q [rows][H][D] bf16 with H = 64,
- * D = 128; w [rows][H] fp32; out [rows][Lc] fp32. ctx[row] <= block_size * (columns of the block table).
+ * D = 128; w [rows][H] fp32; out [rows][Lc] fp32. ctx[row] <= block_size * (columns of the block table);
+ * R_local * P <= 2^31 - 1 (SPMLA_ELIMIT otherwise).
  * Replaces ShardStore.logits / _shard_logits_kernel and shard_logits_v2 'grp' / 'row8'
  * (dotsnote/engine/arcstats_pkg/arcstats/shard_indexer.py:63-91, :118-143; shard_logits_v2.py:15-138). */
 int spmla_index_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
