@@ -269,55 +269,95 @@ __device__ inline void bitonic_desc(unsigned long long* a, int n) {
   __syncthreads();
 }
 
-__device__ inline unsigned long long shfl_xor64(unsigned long long v, int m) {
-  const int lo = __shfl_xor((int)(uint32_t)v, m, 64), hi = __shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+// Lane-xor exchange of a 64-bit value: ds_swizzle (bit mode, xor within 32 lanes) for masks below 32, one
+// ds_bpermute with a precomputed address for 32.
+template <int M>
+__device__ inline unsigned long long xchg64(unsigned long long v, int perm32) {
+  int lo, hi;
+  if constexpr (M < 32) {
+    lo = __builtin_amdgcn_ds_swizzle((int)(uint32_t)v, (M << 10) | 0x1f);
+    hi = __builtin_amdgcn_ds_swizzle((int)(uint32_t)(v >> 32), (M << 10) | 0x1f);
+  } else {
+    lo = __builtin_amdgcn_ds_bpermute(perm32, (int)(uint32_t)v);
+    hi = __builtin_amdgcn_ds_bpermute(perm32, (int)(uint32_t)(v >> 32));
+  }
   return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
-// Bitonic sort of a[0, 2048) descending with the data in VGPRs: thread t of wave w holds elements 128w + l and
-// 128w + 64 + l (l = lane). Stride 64 is an in-thread exchange, strides 1..32 are lane-xor shuffles, and only the
-// strides >= 128 (10 of the 66 stages) go through LDS with workgroup barriers.
+// One compare-exchange stage of the bitonic network held in VGPRs (block size SIZE, lane-xor stride S < 64);
+// thread t of wave w holds entries e0 = 128w + l and e0 + 64 (l = lane).
+template <int SIZE, int S>
+__device__ inline void bstage(unsigned long long& x0, unsigned long long& x1, int e0, int l, int perm32) {
+  const bool d0 = (e0 & SIZE) == 0, d1 = ((e0 + 64) & SIZE) == 0;
+  const unsigned long long y0 = xchg64<S>(x0, perm32), y1 = xchg64<S>(x1, perm32);
+  const bool lower = (l & S) == 0;
+  // the lower element of a pair keeps the max when descending, the upper one the min (and the reverse)
+  x0 = ((lower == d0) == (x0 > y0)) ? x0 : y0;
+  x1 = ((lower == d1) == (x1 > y1)) ? x1 : y1;
+}
+
+// The stages of a SIZE block with strides <= 64 (stride 64: the thread's own two entries, same block).
+template <int SIZE>
+__device__ inline void bmerge(unsigned long long& x0, unsigned long long& x1, int e0, int l, int perm32) {
+  if constexpr (SIZE >= 128) {
+    if ((x0 < x1) == ((e0 & SIZE) == 0)) { const unsigned long long t = x0; x0 = x1; x1 = t; }
+  }
+  if constexpr (SIZE >= 64) bstage<SIZE, 32>(x0, x1, e0, l, perm32);
+  if constexpr (SIZE >= 32) bstage<SIZE, 16>(x0, x1, e0, l, perm32);
+  if constexpr (SIZE >= 16) bstage<SIZE, 8>(x0, x1, e0, l, perm32);
+  if constexpr (SIZE >= 8) bstage<SIZE, 4>(x0, x1, e0, l, perm32);
+  if constexpr (SIZE >= 4) bstage<SIZE, 2>(x0, x1, e0, l, perm32);
+  bstage<SIZE, 1>(x0, x1, e0, l, perm32);
+}
+
+// The stages of a SIZE block with strides >= 128, through LDS (one pair per thread, a barrier per stage).
+template <int SIZE>
+__device__ inline void bmerge_lds(unsigned long long* a, unsigned long long& x0, unsigned long long& x1, int e0) {
+  const int t = threadIdx.x;
+  a[e0] = x0;
+  a[e0 + 64] = x1;
+  __syncthreads();
+#pragma unroll
+  for (int stride = SIZE >> 1; stride >= 128; stride >>= 1) {
+    const int lo = 2 * t - (t & (stride - 1)), hi = lo + stride;
+    const bool desc = (lo & SIZE) == 0;
+    const unsigned long long x = a[lo], y = a[hi];
+    if ((x < y) == desc) { a[lo] = y; a[hi] = x; }
+    __syncthreads();
+  }
+  x0 = a[e0];
+  x1 = a[e0 + 64];
+}
+
+// Bitonic sort of a[0, 2048) descending with the data in VGPRs: 56 of the 66 stages are in-thread or lane-xor
+// exchanges (ds_swizzle), the 10 with strides >= 128 go through LDS.
 __device__ inline void sort2048_desc(unsigned long long* a) {
   const int t = threadIdx.x, l = t & 63;
   const int e0 = 128 * (t >> 6) + l;
+  const int perm32 = (l ^ 32) << 2;
   unsigned long long x0 = a[e0], x1 = a[e0 + 64];
-  for (int size = 2; size <= 2048; size <<= 1) {
-    int stride = size >> 1;
-    if (stride >= 128) {
-      a[e0] = x0;
-      a[e0 + 64] = x1;
-      __syncthreads();
-      for (; stride >= 128; stride >>= 1) {
-        const int lo = 2 * t - (t & (stride - 1)), hi = lo + stride;
-        const bool desc = (lo & size) == 0;
-        const unsigned long long x = a[lo], y = a[hi];
-        if ((x < y) == desc) { a[lo] = y; a[hi] = x; }
-        __syncthreads();
-      }
-      x0 = a[e0];
-      x1 = a[e0 + 64];
-    }
-    if (stride == 64) {
-      const bool desc = (e0 & size) == 0;
-      if ((x0 < x1) == desc) { const unsigned long long tmp = x0; x0 = x1; x1 = tmp; }
-      stride = 32;
-    }
-    const bool d0 = (e0 & size) == 0, d1 = ((e0 + 64) & size) == 0;
-    for (; stride > 0; stride >>= 1) {
-      const unsigned long long y0 = shfl_xor64(x0, stride), y1 = shfl_xor64(x1, stride);
-      const bool lower = (l & stride) == 0;
-      // the lower element of a pair keeps the max when descending, the upper one the min (and the reverse)
-      x0 = ((lower == d0) == (x0 > y0)) ? x0 : y0;
-      x1 = ((lower == d1) == (x1 > y1)) ? x1 : y1;
-    }
-  }
+  bmerge<2>(x0, x1, e0, l, perm32);
+  bmerge<4>(x0, x1, e0, l, perm32);
+  bmerge<8>(x0, x1, e0, l, perm32);
+  bmerge<16>(x0, x1, e0, l, perm32);
+  bmerge<32>(x0, x1, e0, l, perm32);
+  bmerge<64>(x0, x1, e0, l, perm32);
+  bmerge<128>(x0, x1, e0, l, perm32);
+  bmerge_lds<256>(a, x0, x1, e0);
+  bmerge<256>(x0, x1, e0, l, perm32);
+  bmerge_lds<512>(a, x0, x1, e0);
+  bmerge<512>(x0, x1, e0, l, perm32);
+  bmerge_lds<1024>(a, x0, x1, e0);
+  bmerge<1024>(x0, x1, e0, l, perm32);
+  bmerge_lds<2048>(a, x0, x1, e0);
+  bmerge<2048>(x0, x1, e0, l, perm32);
   __syncthreads();                                   // every thread has read a: write the sorted data back
   a[e0] = x0;
   a[e0 + 64] = x1;
   __syncthreads();
 }
 
-// Sorts a[0, n) descending (entries are nonzero); pads with zeros to the sorting network's size.
+// Sorts a[0, n) descending (entries nonzero); pads with zeros to the sorting network's size.
 __device__ inline void tk_sort_desc(unsigned long long* a, int n) {
   int np2 = 1;
   while (np2 < n) np2 <<= 1;
