@@ -25,6 +25,8 @@ SIGNATURES = {
     "spmla_topk_merge": [P, I, I, I, I, I, P, LL, P],
     "spmla_rows_from_topk": [P, LL, P, P, LL, I, I, LL, I, I, P, LL, P, P],
     "spmla_gather": [P, LL, I, P, I, P, LL, P],
+    "spmla_gather_pcie": [P, LL, I, P, I, P, LL, P],
+    "spmla_gather_tiers": [P, LL, I, P, LL, P, I, I, P, LL, P],
     "spmla_copy_rows": [P, LL, P, P, LL, P, I, I, P],
     "spmla_tier_split": [P, LL, I, I, P, LL, P, LL, P, P, LL, P, P],
     "spmla_compact_stage": [P, I, P, LL, I, I, P, P, P, P, LL, P],

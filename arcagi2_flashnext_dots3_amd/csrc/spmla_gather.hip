@@ -6,24 +6,99 @@
 // sparse_offload.py:454-456: a row lives in an HBM line or is read from host memory); compact_stage
 // (dsa_sm89.py:27-35: distinct selected positions, sorted, and the selection remapped into them).
 //
-// Rows are moved in 16-byte chunks, one chunk per thread: a warp-free, fully coalesced pattern that works the same
-// for HBM sources and for pinned host memory mapped into the device address space (reads then cross PCIe).
+// Rows are moved in 16-byte chunks, a wave per row for the gather: the same code serves HBM sources and pinned host
+// memory mapped into the device address space (reads then cross PCIe).
 #include "spmla_common.h"
 
 namespace spmla {
 namespace gth {
 
-// dst row i = src row rows[i] (0 <= rows[i] < R), zero row otherwise; row_bytes % 16 == 0.
-__global__ void gather_kernel(const uint8_t* src, long long R, int row_bytes, const long long* rows, int n,
-                              uint8_t* dst, long long dst_stride) {
+// dst row i = src row rows[i] (0 <= rows[i] < R), zero row otherwise; row_bytes % 16 == 0. One wave per row, lane
+// c moving 16-byte chunks c, c + 64, ...: each row is read as one contiguous run per instruction, which measured
+// 45.5 GB/s from pinned host memory over PCIe for 656-byte rows against 42.2 GB/s with consecutive threads taking
+// consecutive chunks across row boundaries (the rows' start addresses then split more requests).
+__global__ void __launch_bounds__(256) gather_kernel(const uint8_t* src, long long R, int row_bytes,
+                                                     const long long* rows, int n, uint8_t* dst, long long dst_stride) {
+  const int lane = threadIdx.x & 63;
   const int chunks = row_bytes >> 4;
-  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= (long long)n * chunks) return;
-  const int i = (int)(g / chunks), c = (int)(g % chunks);
-  const long long r = rows[i];
-  u32x4 v = u32x4{0, 0, 0, 0};
-  if (r >= 0 && r < R) v = *(const u32x4*)(src + r * row_bytes + c * 16);
-  *(u32x4*)(dst + (long long)i * dst_stride + c * 16) = v;
+  for (int i = blockIdx.x * 4 + (int)(threadIdx.x >> 6); i < n; i += gridDim.x * 4) {
+    const long long r = rows[i];
+    const bool ok = r >= 0 && r < R;
+    const uint8_t* s = src + (ok ? r : 0) * row_bytes;
+    uint8_t* d = dst + (long long)i * dst_stride;
+    for (int c = lane; c < chunks; c += 64) {
+      u32x4 v = u32x4{0, 0, 0, 0};
+      if (ok) v = *(const u32x4*)(s + c * 16);
+      *(u32x4*)(d + c * 16) = v;
+    }
+  }
+}
+
+// Host-tier staging: dst row t * K + k = src row rows[t][k] for k < counts[t] (zero row if rows[t][k] is outside
+// [0, R)); other rows untouched, except that row 0 is zeroed when token 0 has no rows (the attention reads row 0 of
+// its pool for masked entries, which must then be finite). Persistent grid: tokens are taken 1024 at a time, the
+// counts' prefix sum goes to LDS and every wave copies rows v = wave, wave + waves, ... of the chunk, locating its
+// token by binary search in the prefix (uniform per wave).
+__global__ void __launch_bounds__(256) gather_tiers_kernel(const uint8_t* src, long long R, int row_bytes,
+                                                           const int* rows, long long r_st, const int* counts, int T,
+                                                           int K, uint8_t* dst, long long dst_stride) {
+  __shared__ int pre[1025];
+  __shared__ int wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int chunks = row_bytes >> 4;
+  const int nw = gridDim.x * 4, gw = blockIdx.x * 4 + wv;
+  if (gw == 0 && counts[0] <= 0)
+    for (int c = lane; c < chunks; c += 64) *(u32x4*)(dst + c * 16) = u32x4{0, 0, 0, 0};
+  for (int t0 = 0; t0 < T; t0 += 1024) {
+    const int nt = min(1024, T - t0);
+    // inclusive prefix of clamp(counts[t0 + t], 0, K): thread tid sums tokens 4 tid .. 4 tid + 3
+    int c4[4], s = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = 4 * tid + u;
+      c4[u] = t < nt ? min(max(counts[t0 + t], 0), K) : 0;
+      s += c4[u];
+    }
+    int inc = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += y;
+    }
+    if (lane == 63) wsum[wv] = inc;
+    __syncthreads();
+    int base = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) base += w < wv ? wsum[w] : 0;
+    int run = base + inc - s;
+    if (tid == 0) pre[0] = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      run += c4[u];
+      if (4 * tid + u < nt) pre[4 * tid + u + 1] = run;
+    }
+    __syncthreads();
+    const int tot = pre[nt];
+    for (int v = gw; v < tot; v += nw) {
+      int lo = 0, hi = nt - 1;                       // largest t with pre[t] <= v
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (pre[mid] <= v) lo = mid;
+        else hi = mid - 1;
+      }
+      const int t = t0 + lo, k = v - pre[lo];
+      const long long r = rows[(long long)t * r_st + k];
+      const bool ok = r >= 0 && r < R;
+      const uint8_t* sp = src + (ok ? r : 0) * row_bytes;
+      uint8_t* d = dst + ((long long)t * K + k) * dst_stride;
+      for (int c = lane; c < chunks; c += 64) {
+        u32x4 x = u32x4{0, 0, 0, 0};
+        if (ok) x = *(const u32x4*)(sp + c * 16);
+        *(u32x4*)(d + c * 16) = x;
+      }
+    }
+    __syncthreads();                                 // pre[] is rewritten for the next chunk
+  }
 }
 
 // dst row dst_rows[i] = src row src_rows[i]; pairs with an invalid side are skipped.
@@ -157,16 +232,40 @@ using namespace spmla;
 
 extern "C" {
 
-int spmla_gather(const void* src, long long R, int row_bytes, const long long* rows, int n, void* dst,
-                 long long dst_stride, void* stream) {
+static int gather_launch(const void* src, long long R, int row_bytes, const long long* rows, int n, void* dst,
+                         long long dst_stride, unsigned max_wg, void* stream) {
   if (n < 0 || R < 0 || row_bytes <= 0 || (row_bytes & 15)) return SPMLA_EARG;
   if (n == 0) return SPMLA_OK;
   if (!src || !rows || !dst) return SPMLA_EARG;
   if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < row_bytes) return SPMLA_EALIGN;
-  const long long work = (long long)n * (row_bytes >> 4);
-  hipLaunchKernelGGL(gth::gather_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     (const uint8_t*)src, R, row_bytes, rows, n, (uint8_t*)dst, dst_stride);
+  unsigned grid = (unsigned)((n + 3) / 4);
+  if (grid > max_wg) grid = max_wg;
+  hipLaunchKernelGGL(gth::gather_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src, R,
+                     row_bytes, rows, n, (uint8_t*)dst, dst_stride);
   return (int)hipGetLastError();
+}
+
+int spmla_gather(const void* src, long long R, int row_bytes, const long long* rows, int n, void* dst,
+                 long long dst_stride, void* stream) {
+  return gather_launch(src, R, row_bytes, rows, n, dst, dst_stride, 0xffffffffu, stream);
+}
+
+int spmla_gather_tiers(const void* src, long long R, int row_bytes, const int* rows, long long r_st, const int* counts,
+                       int T, int K, void* dst, long long dst_stride, void* stream) {
+  if (T < 0 || K < 0 || R < 0 || row_bytes <= 0 || (row_bytes & 15) || r_st < K) return SPMLA_EARG;
+  if (T == 0 || K == 0) return SPMLA_OK;
+  if (!src || !rows || !counts || !dst) return SPMLA_EARG;
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < row_bytes) return SPMLA_EALIGN;
+  hipLaunchKernelGGL(gth::gather_tiers_kernel, dim3(64), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src, R,
+                     row_bytes, rows, r_st, counts, T, K, (uint8_t*)dst, dst_stride);
+  return (int)hipGetLastError();
+}
+
+// 64 workgroups x 4 waves = 256 rows in flight: 45.7 GB/s from pinned host memory (the full grid: 45.8 GB/s), on a
+// quarter of the CUs.
+int spmla_gather_pcie(const void* src, long long R, int row_bytes, const long long* rows, int n, void* dst,
+                      long long dst_stride, void* stream) {
+  return gather_launch(src, R, row_bytes, rows, n, dst, dst_stride, 64u, stream);
 }
 
 int spmla_copy_rows(const void* src, long long R_src, const long long* src_rows, void* dst, long long R_dst,

@@ -134,14 +134,27 @@ def rows_from_topk(topk_pos, req, block_table, block_size, stride_rows=None, row
 
 
 # ---------------------------------------------------------------------------------------------- rows
-def gather(src, rows, out, R=None):
-    """out[i] = src[rows[i]] (zero row when rows[i] is outside [0, R)); src [R, row] uint8 (device or mapped host)."""
+def gather(src, rows, out, R=None, pcie=False):
+    """out[i] = src[rows[i]] (zero row when rows[i] is outside [0, R)); src [R, row] uint8 (device or mapped host).
+    pcie: src is pinned host memory; the copy then runs on a fixed 64-workgroup grid (spmla_gather_pcie)."""
     n = rows.shape[0]
     rowb = out.shape[-1]
     _need(rows.dtype == torch.int64, "rows int64")
-    _lib.call("spmla_gather", src.data_ptr() if torch.is_tensor(src) else int(src),
+    _lib.call("spmla_gather_pcie" if pcie else "spmla_gather", src.data_ptr() if torch.is_tensor(src) else int(src),
               int(R if R is not None else src.shape[0]), rowb, rows.data_ptr(), n, out.data_ptr(), out.stride(0),
               _stream(out))
+    return out
+
+
+def gather_tiers(src, rows, counts, out, R=None):
+    """Host-tier staging: out[t * K + k] = src[rows[t, k]] for k < counts[t] (rows int32 [T, K], counts int32 [T]);
+    other rows of out untouched (row 0 zeroed when counts[0] <= 0). src: pinned host memory (or HBM)."""
+    T, K = rows.shape
+    _need(rows.dtype == torch.int32 and rows.stride(1) == 1 and counts.dtype == torch.int32, "int32 rows / counts")
+    _need(out.shape[0] >= T * K, "out holds T * K rows")
+    _lib.call("spmla_gather_tiers", src.data_ptr() if torch.is_tensor(src) else int(src),
+              int(R if R is not None else src.shape[0]), out.shape[-1], rows.data_ptr(), rows.stride(0),
+              counts.data_ptr(), T, K, out.data_ptr(), out.stride(0), _stream(out))
     return out
 
 

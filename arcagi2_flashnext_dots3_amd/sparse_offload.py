@@ -70,7 +70,7 @@ class LayerOffload:
         """out[i] = host row rows[i] (int64; zero row when outside [0, R)); out [N, 656] uint8 in HBM
         (reference LayerOffload.gather, sparse_offload.py:1157-1163)."""
         if rows.shape[0]:
-            kernels.gather(self.host, rows.to(torch.int64), out)
+            kernels.gather(self.host, rows.to(torch.int64), out, pcie=True)
         return out
 
     def set_hot_rows(self, rows):
@@ -100,6 +100,20 @@ class LayerOffload:
             self._ws[name] = b
         return b[:n].view(shape)
 
+    def _side(self, device):
+        """Second stream (default priority) and the two events that order it against the caller's stream."""
+        if getattr(self, "_side_sync", None) is None:
+            self._side_sync = (torch.cuda.Stream(device=device), torch.cuda.Event(), torch.cuda.Event())
+        return self._side_sync
+
+    def _identity(self, T, K, device):
+        key = ("ident", T, K)
+        b = self._ws.get(key)
+        if b is None:
+            b = torch.arange(T * K, dtype=torch.int32, device=device).view(T, K)
+            self._ws[key] = b
+        return b
+
     def attend(self, q, idx, sm_scale, kv_scale=1.0, num_heads=None, ql=1, mkey=None, slots=None, out=None,
                lse=None, return_lse=False):
         """q [T, H, 576] bf16, idx [T, K] int32 host rows (-1 / out of range = none) -> out [T, H, 512] bf16
@@ -127,17 +141,30 @@ class LayerOffload:
             mcnt = None
         # host tier: copy the missed rows over PCIe into HBM staging, then attend there
         staged = self._buf("staged", (T * K, ROW), torch.uint8)
-        kernels.gather(self.host, host.reshape(-1).to(torch.int64), staged)
-        sidx = self._buf("sidx", (T, K), torch.int32)
-        ar = torch.arange(T * K, dtype=torch.int32, device=q.device).view(T, K)
-        torch.where((host >= 0) & (host < self.R), ar, torch.full_like(ar, -1), out=sidx)
         if not self.C:
+            kernels.gather(self.host, host.reshape(-1).to(torch.int64), staged, pcie=True)
+            sidx = self._buf("sidx", (T, K), torch.int32)
+            ar = torch.arange(T * K, dtype=torch.int32, device=q.device).view(T, K)
+            torch.where((host >= 0) & (host < self.R), ar, torch.full_like(ar, -1), out=sidx)
             kernels.attend(q, staged, sidx, sm_scale, kv_scale, out=out, lse=lse)
             return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+        # the host list of token t is compacted (its mcnt[t] valid rows first): staged rows t * K + k, k < mcnt[t];
+        # the attention's per-token count masks the rest, so the index map is the fixed identity
+        sidx = self._identity(T, K, q.device)
         op = self._buf("opart", (2, T, H, kernels.D_LAT), torch.float32)
         lp = self._buf("lpart", (2, T, H), torch.float32)
-        kernels.attend_partial(q, self.cache[:self.C], hbm, sm_scale, kv_scale, op[0:1], lp[0:1], kcount=hcnt)
+        # the PCIe copy (64 workgroups) runs beside the HBM-tier attention, which is queued on a second stream of
+        # default priority; the main stream waits for it before the merge
+        main = torch.cuda.current_stream(q.device)
+        side, ev_split, ev_hbm = self._side(q.device)
+        ev_split.record(main)
+        kernels.gather_tiers(self.host, host, mcnt, staged)
+        side.wait_event(ev_split)
+        with torch.cuda.stream(side):
+            kernels.attend_partial(q, self.cache[:self.C], hbm, sm_scale, kv_scale, op[0:1], lp[0:1], kcount=hcnt)
+            ev_hbm.record(side)
         kernels.attend_partial(q, staged, sidx, sm_scale, kv_scale, op[1:2], lp[1:2], kcount=mcnt)
+        main.wait_event(ev_hbm)
         kernels.lse_merge(op, lp, out=out, lse=lse)
         return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
 

@@ -93,6 +93,23 @@ int spmla_rows_from_topk(const int* topk, long long tk_st, const int* req, const
 int spmla_gather(const void* src, long long R, int row_bytes, const long long* rows, int n, void* dst,
                  long long dst_stride, void* stream);
 
+/* spmla_gather for a source in pinned host memory: the same result from a fixed grid of 64 workgroups that loops over
+ * the rows. Reads over PCIe saturate the link from a quarter of the CUs, so kernels on other streams (the HBM-tier
+ * attention of the same decode step) run beside it. Replaces the host-row path of LayerOffload.gather
+ * (dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:1157-1163) and the miss fill's host reads
+ * (offload_fill.py:204-248). */
+int spmla_gather_pcie(const void* src, long long R, int row_bytes, const long long* rows, int n, void* dst,
+                      long long dst_stride, void* stream);
+
+/* Host-tier staging of a decode step: for each token t < T and k < counts[t] (clipped to K), dst row t * K + k
+ * (row stride dst_stride bytes) = src row rows[t * r_st + k] (zero row when outside [0, R)); the other dst rows are
+ * left as they are, except that dst row 0 is zeroed when counts[0] <= 0. rows / counts are spmla_tier_split's host
+ * lists (compacted per token) and counts. Same 64-workgroup grid as spmla_gather_pcie. Replaces the miss copy of
+ * the reference's tiered fill (dotsnote/engine/arcstats_pkg/arcstats/offload_fill.py:204-248; sparse_offload.py
+ * :1157-1163 for one row). */
+int spmla_gather_tiers(const void* src, long long R, int row_bytes, const int* rows, long long r_st, const int* counts,
+                       int T, int K, void* dst, long long dst_stride, void* stream);
+
 /* Row copy: dst row dst_rows[i] = src row src_rows[i] (pairs with an out-of-range side skipped); fills the HBM hot-row
  * cache from the host pool. Replaces the row-cache fill copies (offload_fill.py:311-333, csrc/offload_attn.cu:522-584). */
 int spmla_copy_rows(const void* src, long long R_src, const long long* src_rows, void* dst, long long R_dst,

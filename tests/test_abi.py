@@ -40,6 +40,8 @@ def test_version():
     (("spmla_topk_merge", None, 4, 2, 16, 33, 33, None, 0, None), -2),
     (("spmla_topk_merge", None, 4, 2, 2048, 4000, 4000, None, 0, None), -5),
     (("spmla_gather", None, 0, 650, None, 1, None, 0, None), -2),
+    (("spmla_gather_pcie", None, 0, 650, None, 1, None, 0, None), -2),
+    (("spmla_gather_tiers", None, 0, 656, None, 4, None, 1, 4, None, 656, None), -2),
     (("spmla_cache_write", None, 0, None, 0, None, 1, None, 10, 64, 0, 7, 1.0, None), -2),
     (("spmla_index_logits", None, 0, 0, None, 0, None, 0, 64, 0, None, 0, 64, None, None, 1, 32, 128, 10, 1, 0, 0,
       None, 0, None), -5),

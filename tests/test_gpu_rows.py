@@ -53,6 +53,30 @@ def test_gather_from_pinned_host(dev):
     assert np.array_equal(out.cpu().numpy(), host.numpy()[rows.numpy()])
 
 
+@pytest.mark.parametrize("T,K,zero0", [(9, 300, False), (1100, 7, True)])
+def test_gather_tiers(dev, T, K, zero0):
+    """Host-tier staging from pinned memory: rows k < counts[t] of each token land at t * K + k, out-of-range rows as
+    zero rows, untouched rows keep their bytes, row 0 is zeroed when token 0 has none (T > 1024: two token chunks)."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    g = np.random.default_rng(7)
+    R = 3000
+    host = torch.from_numpy(g.integers(0, 256, (R, 656)).astype(np.uint8)).pin_memory()
+    rows = g.integers(-2, R + 2, (T, K)).astype(np.int32)
+    counts = g.integers(-1, K + 3, T).astype(np.int32)
+    counts[0] = 0 if zero0 else K
+    out = torch.full((T * K, 656), 9, dtype=torch.uint8, device=dev)
+    kernels.gather_tiers(host, torch.from_numpy(rows).to(dev), torch.from_numpy(counts).to(dev), out)
+    torch.cuda.synchronize()
+    exp = np.full((T * K, 656), 9, dtype=np.uint8)
+    for t in range(T):
+        for k in range(min(max(int(counts[t]), 0), K)):
+            r = int(rows[t, k])
+            exp[t * K + k] = host.numpy()[r] if 0 <= r < R else 0
+    if zero0:
+        exp[0] = 0
+    assert np.array_equal(out.cpu().numpy(), exp)
+
+
 def test_tier_split(dev):
     from arcagi2_flashnext_dots3_amd import kernels
     g = np.random.default_rng(3)
