@@ -21,6 +21,8 @@ SIGNATURES = {
     "spmla_index_key_write": [P, LL, P, I, P, LL, I, I, I, LL, I, P],
     "spmla_index_logits": [P, LL, LL, P, LL, P, LL, I, LL, P, LL, I, P, P, I, I, I, I, I, I, I, P, LL, P],
     "spmla_topk": [P, LL, P, I, I, I, P, LL, P],
+    "spmla_topk_ws_bytes": [I, I, I],
+    "spmla_topk_ws": [P, LL, P, I, I, I, P, LL, P, LL, P],
     "spmla_topk_local": [P, LL, P, I, I, I, I, I, P, P],
     "spmla_topk_merge": [P, I, I, I, I, I, P, LL, P],
     "spmla_rows_from_topk": [P, LL, P, P, LL, I, I, LL, I, I, P, LL, P, P],
@@ -35,7 +37,7 @@ SIGNATURES = {
     "spmla_version": [],
     "spmla_host_e4m3_encode": [P, P, LL],
 }
-_RESTYPE = {"spmla_version": ctypes.c_char_p, "spmla_host_e4m3_encode": None}
+_RESTYPE = {"spmla_version": ctypes.c_char_p, "spmla_host_e4m3_encode": None, "spmla_topk_ws_bytes": LL}
 
 ERRORS = {-2: "bad argument", -3: "misaligned pointer or stride", -5: "size beyond the kernel's limit"}
 

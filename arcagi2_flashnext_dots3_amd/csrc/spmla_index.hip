@@ -644,6 +644,237 @@ __global__ void __launch_bounds__(TK_NT) topk_kernel(TopkParams p) {
   tk_emit_sorted(src, nsel, p.K, p.out + (long long)row * p.out_st, L);
 }
 
+// ---- top-k over several workgroups per row (workspace variant) -------------------------------------------
+// Two radix levels run across G workgroups per row (chunks of at most CL columns):
+//   hist:    the histogram of the level-0 11-bit digit over each chunk's keys;
+//   collect: every workgroup sums the G histograms of the level and finds the boundary bin b of the row's
+//            remaining need; it writes its chunk's keys above b (and in b when that completes the need) to the row's
+//            winner list, and the keys in b to the candidate list when the bin holds at most TK_CAP keys, at offsets
+//            given by the histograms of the chunks before it (no atomics; the lists are unordered). Otherwise the
+//            next level narrows the prefix to b, and this pass also builds its chunk's histogram of that level
+//            (into the other half of the histogram buffer, which no workgroup of the row is reading).
+// A finishing pass (one workgroup per row) resolves the candidates' remaining levels, sorts the K winners and
+// writes the positions. Rows with n <= K, and rows whose bin is still too large after two levels (heavy ties), run
+// the one-workgroup selection there. Per-row state lives in the workspace, one header per level (the collect pass
+// of level L reads header L and its first workgroup writes header L + 1).
+enum : int { TKW_SELECT = 0, TKW_WHOLE = 1, TKW_CANDS = 2, TKW_FALLBACK = 3 };
+struct TkwHdr { int state, prefix, mask, need, sb, binc, lvl, pad; };   // 32 bytes
+
+struct TopkWs {
+  int G, CL;                                      // chunks per row, columns per chunk (multiple of 1024)
+  long long row_bytes;                            // workspace bytes per row
+  __host__ __device__ TkwHdr* hdr(uint8_t* ws, int row) const { return (TkwHdr*)(ws + row * row_bytes); }
+  __host__ __device__ unsigned long long* sel(uint8_t* ws, int row) const {
+    return (unsigned long long*)(ws + row * row_bytes + 3 * sizeof(TkwHdr));
+  }
+  __host__ __device__ unsigned long long* cand(uint8_t* ws, int row) const { return sel(ws, row) + TK_KMAX; }
+  __host__ __device__ uint32_t* hist(uint8_t* ws, int row) const { return (uint32_t*)(cand(ws, row) + TK_CAP); }
+};
+
+__host__ inline TopkWs topk_ws_layout(int Lc) {
+  TopkWs w;
+  // chunks of 8192 columns, at most 8 per row (every collect workgroup reads all G histograms of its row)
+  int G = (Lc + 8191) / 8192;
+  if (G > 8) G = 8;
+  if (G < 1) G = 1;
+  int CL = (Lc + G - 1) / G;
+  CL = (CL + 1023) / 1024 * 1024;
+  w.G = G; w.CL = CL;
+  w.row_bytes = 3 * (long long)sizeof(TkwHdr) + (long long)(TK_KMAX + TK_CAP) * 8 + 2LL * G * 2048 * 4 + 16;
+  w.row_bytes = (w.row_bytes + 15) / 16 * 16;
+  return w;
+}
+
+struct TopkWsParams {
+  const float* lg; long long lg_st;
+  const int* ctx; int rows, Lc, K;
+  int* out; long long out_st;
+  uint8_t* ws; TopkWs w;
+  int level;
+};
+
+__device__ inline int tkw_n(const TopkWsParams& p, int row) {
+  const int n = p.ctx[row];
+  return n < 0 ? 0 : (n > p.Lc ? p.Lc : n);
+}
+
+// the row's state entering level p.level (level 0: select everything, need K)
+__device__ inline TkwHdr tkw_state(const TopkWsParams& p, int row) {
+  if (p.level == 0) return TkwHdr{TKW_SELECT, 0, 0, p.K, 0, 0, 0, 0};
+  return p.w.hdr(p.ws, row)[p.level];
+}
+
+__global__ void __launch_bounds__(TK_NT) topk_hist_kernel(TopkWsParams p) {
+  __shared__ uint32_t hist[TK_HCOPY * TK_HSTR];
+  const int row = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  const int n = tkw_n(p, row);
+  if (n <= p.K) return;
+  const TkwHdr st = tkw_state(p, row);
+  if (st.state != TKW_SELECT) return;
+  const int shift = tk_shift(p.level);
+  const uint32_t prefix = (uint32_t)st.prefix, mask = (uint32_t)st.mask;
+  for (int i = tid; i < TK_HCOPY * TK_HSTR; i += TK_NT) hist[i] = 0;
+  __syncthreads();
+  const float* x = p.lg + (long long)row * p.lg_st;
+  const int c0 = g * p.w.CL, c1 = min(c0 + p.w.CL, n);
+  for (int base = c0; base < c1; base += 8 * TK_NT) {
+    uint32_t k[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = base + i * TK_NT + tid;
+      k[i] = j < c1 ? okey(x[j]) : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (base + i * TK_NT + tid < c1 && (k[i] & mask) == prefix)
+        atomicAdd(&hist[(tid & (TK_HCOPY - 1)) * TK_HSTR + ((k[i] >> shift) & 0x7ffu)], 1u);
+  }
+  __syncthreads();
+  uint32_t* out = p.w.hist(p.ws, row) + (long long)g * 2048;
+  for (int b = tid; b < 2048; b += TK_NT) {
+    uint32_t h = 0;
+#pragma unroll
+    for (int c = 0; c < TK_HCOPY; ++c) h += hist[c * TK_HSTR + b];
+    out[b] = h;
+  }
+}
+
+__global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
+  __shared__ uint32_t wsum[17];
+  __shared__ uint32_t sh[8];
+  __shared__ uint32_t nh[TK_HCOPY * TK_HSTR];       // the next level's histogram of this chunk (when narrowing)
+  const int row = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  const int n = tkw_n(p, row);
+  if (n <= p.K) return;
+  const TkwHdr st = tkw_state(p, row);
+  TkwHdr* next = p.w.hdr(p.ws, row) + p.level + 1;
+  if (st.state != TKW_SELECT) {                     // settled at an earlier level: carry the state forward
+    if (g == 0 && tid == 0) *next = st;
+    return;
+  }
+  const int shift = tk_shift(p.level);
+  const uint32_t prefix = (uint32_t)st.prefix, mask = (uint32_t)st.mask, need = (uint32_t)st.need;
+  // thread t owns bins 2047 - 2t, 2046 - 2t: totals over the G chunks and over the chunks before g
+  const int b0 = 2047 - 2 * tid, b1 = b0 - 1;
+  const uint32_t* hs = p.w.hist(p.ws, row) + (long long)(p.level & 1) * p.w.G * 2048;
+  uint32_t t0 = 0, t1 = 0, q0 = 0, q1 = 0;
+  for (int c = 0; c < p.w.G; ++c) {
+    const uint32_t h0 = hs[(long long)c * 2048 + b0], h1 = hs[(long long)c * 2048 + b1];
+    t0 += h0; t1 += h1;
+    if (c < g) { q0 += h0; q1 += h1; }
+  }
+  uint32_t tot;
+  const uint32_t before = block_excl_scan(t0 + t1, wsum, &tot);
+  if (before < need && before + t0 >= need) { sh[1] = (uint32_t)b0; sh[2] = before; sh[3] = t0; }
+  if (before + t0 < need && before + t0 + t1 >= need) { sh[1] = (uint32_t)b1; sh[2] = before + t0; sh[3] = t1; }
+  __syncthreads();
+  const uint32_t b = sh[1], above = sh[2], binc = sh[3];
+  const bool whole = above + binc == need;
+  const bool fits = !whole && binc <= (uint32_t)TK_CAP;
+  // this chunk's offsets: winners of the chunks before g (bins above b, and b itself when whole); candidates in b
+  const uint32_t mine = ((uint32_t)b0 > b || (whole && (uint32_t)b0 == b) ? q0 : 0u) +
+                        ((uint32_t)b1 > b || (whole && (uint32_t)b1 == b) ? q1 : 0u);
+  uint32_t sum;
+  (void)block_excl_scan(mine, wsum, &sum);
+  if ((uint32_t)b0 == b) sh[4] = q0;
+  if ((uint32_t)b1 == b) sh[4] = q1;
+  __syncthreads();
+  uint32_t sb = (uint32_t)st.sb + sum, cb = sh[4];
+  const bool narrow = !whole && !fits && p.level + 1 < 2;   // uniform per row: the next level runs on bin b
+  const int nshift = tk_shift(p.level + 1);
+  if (narrow) {
+    for (int i = tid; i < TK_HCOPY * TK_HSTR; i += TK_NT) nh[i] = 0;
+    __syncthreads();
+  }
+  if (g == 0 && tid == 0) {
+    TkwHdr h = st;
+    h.prefix = (int)(prefix | (b << shift));
+    h.mask = (int)(mask | (0x7ffu << shift));
+    h.need = (int)(need - above);
+    h.sb = st.sb + (int)above;
+    h.binc = (int)binc;
+    h.lvl = p.level + 1;
+    if (whole) { h.state = TKW_WHOLE; h.sb = st.sb + (int)need; }
+    else if (fits) h.state = TKW_CANDS;
+    else h.state = p.level + 1 < 2 ? TKW_SELECT : TKW_FALLBACK;
+    *next = h;
+  }
+  unsigned long long* sel = p.w.sel(p.ws, row);
+  unsigned long long* cand = p.w.cand(p.ws, row);
+  const float* x = p.lg + (long long)row * p.lg_st;
+  const int c0 = g * p.w.CL, c1 = min(c0 + p.w.CL, n);
+  for (int base = c0; base < c1; base += 8 * TK_NT) {
+    uint32_t k[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = base + i * TK_NT + tid;
+      k[i] = j < c1 ? okey(x[j]) : 0u;
+    }
+    uint32_t selm = 0, candm = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool in = base + i * TK_NT + tid < c1 && (k[i] & mask) == prefix;
+      const uint32_t d = (k[i] >> shift) & 0x7ffu;
+      selm |= (uint32_t)(in && (d > b || (whole && d == b))) << i;
+      candm |= (uint32_t)(in && fits && d == b) << i;
+    }
+    uint32_t tt;
+    const uint32_t off = block_excl_scan((uint32_t)__popc(selm) | ((uint32_t)__popc(candm) << 16), wsum, &tt);
+    uint32_t so = sb + (off & 0xffffu), co = cb + (off >> 16);
+    sb += tt & 0xffffu;
+    cb += tt >> 16;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = base + i * TK_NT + tid;
+      if ((selm >> i) & 1u) sel[so++] = tk_pack(k[i], j);
+      if ((candm >> i) & 1u) cand[co++] = tk_pack(k[i], j);
+      if (narrow && base + i * TK_NT + tid < c1 && (k[i] & mask) == prefix && ((k[i] >> shift) & 0x7ffu) == b)
+        atomicAdd(&nh[(tid & (TK_HCOPY - 1)) * TK_HSTR + ((k[i] >> nshift) & 0x7ffu)], 1u);
+    }
+  }
+  if (narrow) {                                     // level L + 1's histograms go to the other half of the buffer
+    __syncthreads();
+    uint32_t* out = p.w.hist(p.ws, row) + (long long)(((p.level + 1) & 1) * p.w.G + g) * 2048;
+    for (int bb = tid; bb < 2048; bb += TK_NT) {
+      uint32_t h = 0;
+#pragma unroll
+      for (int c = 0; c < TK_HCOPY; ++c) h += nh[c * TK_HSTR + bb];
+      out[bb] = h;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
+  __shared__ TopkLds L;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const int n = tkw_n(p, row);
+  const RowSrc src{p.lg + (long long)row * p.lg_st, n};
+  int* o = p.out + (long long)row * p.out_st;
+  int nsel = 0;
+  bool full = n <= p.K;
+  TkwHdr st{};
+  if (!full) {
+    st = p.w.hdr(p.ws, row)[p.level];
+    full = st.state != TKW_WHOLE && st.state != TKW_CANDS;
+  }
+  if (full) {
+    nsel = tk_select(src, p.K, L);                  // few columns, or ties too heavy for the lists
+  } else {
+    const unsigned long long* sel = p.w.sel(p.ws, row);
+    for (int i = tid; i < st.sb; i += TK_NT) L.sel[i] = sel[i];
+    if (st.state == TKW_CANDS) {
+      const unsigned long long* cand = p.w.cand(p.ws, row);
+      for (int i = tid; i < st.binc; i += TK_NT) L.cand[i] = cand[i];
+    }
+    __syncthreads();
+    if (st.state == TKW_CANDS)
+      tk_resolve_cands(L, st.binc, st.lvl, (uint32_t)st.prefix, (uint32_t)st.mask, (uint32_t)st.need,
+                       (uint32_t)st.sb);
+    nsel = p.K;
+  }
+  tk_emit_sorted(src, nsel, p.K, o, L);
+}
+
 // fast_topk.local (dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:52-66, csrc/topk_select.cu:1-13, :75-201):
 // the row's valid columns are j < ceil((ctx - rank) / P) (clipped to Lc); the top kl of them go to the payload
 // pk[row] = [values fp32 | positions j * P + rank as int32 bits] in ascending column order; fewer than kl valid
@@ -768,6 +999,32 @@ int spmla_topk(const float* logits, long long lg_st, const int* ctx, int rows, i
   idx::TopkParams p;
   p.lg = logits; p.lg_st = lg_st; p.ctx = ctx; p.rows = rows; p.Lc = Lc; p.K = K; p.out = out; p.out_st = out_st;
   hipLaunchKernelGGL(idx::topk_kernel, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}
+
+long long spmla_topk_ws_bytes(int rows, int Lc, int K) {
+  if (rows < 0 || Lc < 0 || K <= 0) return 0;
+  return (long long)rows * idx::topk_ws_layout(Lc).row_bytes;
+}
+
+int spmla_topk_ws(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                  long long out_st, void* ws, long long ws_bytes, void* stream) {
+  if (rows < 0 || Lc < 0 || K <= 0) return SPMLA_EARG;
+  if (K > idx::TK_KMAX) return SPMLA_ELIMIT;
+  if (rows == 0) return SPMLA_OK;
+  if (!logits || !ctx || !out || !ws) return SPMLA_EARG;
+  if (((uintptr_t)ws & 15) || ws_bytes < spmla_topk_ws_bytes(rows, Lc, K)) return SPMLA_EARG;
+  idx::TopkWsParams p;
+  p.lg = logits; p.lg_st = lg_st; p.ctx = ctx; p.rows = rows; p.Lc = Lc; p.K = K; p.out = out; p.out_st = out_st;
+  p.ws = (uint8_t*)ws; p.w = idx::topk_ws_layout(Lc);
+  p.level = 0;
+  hipLaunchKernelGGL(idx::topk_hist_kernel, dim3(rows, p.w.G), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  for (int level = 0; level < 2; ++level) {        // the level-1 histograms come from the level-0 collect
+    p.level = level;
+    hipLaunchKernelGGL(idx::topk_collect_kernel, dim3(rows, p.w.G), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  }
+  p.level = 2;                                      // header 2: the state after both levels
+  hipLaunchKernelGGL(idx::topk_finish_kernel, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 

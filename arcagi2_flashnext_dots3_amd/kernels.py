@@ -85,16 +85,36 @@ def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P
     return out
 
 
-def topk(logits, ctx, K, out=None):
-    """logits [rows, Lc] fp32, ctx [rows] int32 -> [rows, K] int32 positions (value desc, position asc; -1 pad)."""
+_TOPK_WS = {}
+
+
+def _topk_ws(device, nbytes):
+    """Per-device workspace of spmla_topk_ws (grown on demand; reused by calls on the same stream)."""
+    key = torch.device(device)
+    b = _TOPK_WS.get(key)
+    if b is None or b.numel() < nbytes:
+        b = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=key)
+        _TOPK_WS[key] = b
+    return b
+
+
+def topk(logits, ctx, K, out=None, single_pass=False):
+    """logits [rows, Lc] fp32, ctx [rows] int32 -> [rows, K] int32 positions (value desc, position asc; -1 pad).
+    Several workgroups per row (spmla_topk_ws) unless single_pass (spmla_topk, one workgroup per row)."""
     rows, Lc = logits.shape
     _need(logits.dtype == torch.float32 and logits.stride(1) == 1, "fp32 logits with contiguous rows")
     _need(ctx.dtype == torch.int32 and ctx.is_contiguous(), "ctx int32")
     if out is None:
         out = torch.empty(rows, K, dtype=torch.int32, device=logits.device)
     _need(out.dtype == torch.int32 and out.stride(1) == 1, "out int32")
-    _lib.call("spmla_topk", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
-              out.stride(0), _stream(logits))
+    if single_pass:
+        _lib.call("spmla_topk", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
+                  out.stride(0), _stream(logits))
+        return out
+    nb = int(_lib.lib().spmla_topk_ws_bytes(rows, Lc, K))
+    ws = _topk_ws(logits.device, nb)
+    _lib.call("spmla_topk_ws", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
+              out.stride(0), ws.data_ptr(), ws.numel(), _stream(logits))
     return out
 
 

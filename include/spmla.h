@@ -61,6 +61,18 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
 int spmla_topk(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
                long long out_st, void* stream);
 
+/* Bytes of workspace spmla_topk_ws needs for rows x Lc (0 for invalid sizes). */
+long long spmla_topk_ws_bytes(int rows, int Lc, int K);
+
+/* spmla_topk with the same result, spread over several workgroups per row: a histogram pass and a collect pass over
+ * chunks of 8192 or more columns (at most 8 chunks per row), then one workgroup per row that resolves the boundary bin
+ * and sorts. ws: device memory of at least spmla_topk_ws_bytes(rows, Lc, K) bytes, 16-byte aligned, any contents
+ * (every pass writes what the next reads); calls that share a workspace must not overlap. Same replacement as
+ * spmla_topk (fast_topk.local + merge at P = 1, dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:52-78;
+ * csrc/topk_select.cu:251-286; shard_indexer.py:194-221). */
+int spmla_topk_ws(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                  long long out_st, void* ws, long long ws_bytes, void* stream);
+
 /* fast_topk.local at rank `rank` of P: the row's valid columns are j < ceil((ctx[row] - rank) / P) (clipped to Lc);
  * the top kl of them by the same key and tie rule as spmla_topk go to pk[row] = [kl values fp32 | kl positions
  * j * P + rank as int32 bits] (pk row stride 2 * kl floats) in ascending column order; rows with fewer than kl valid

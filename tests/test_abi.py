@@ -35,6 +35,8 @@ def test_version():
       None, None), -2),
     (("spmla_topk", None, 0, None, 1, 10, 5000, None, 0, None), -5),
     (("spmla_topk", None, 0, None, 1, 10, 0, None, 0, None), -2),
+    (("spmla_topk_ws", None, 0, None, 1, 10, 5000, None, 0, None, 0, None), -5),
+    (("spmla_topk_ws", None, 0, None, 1, 10, 16, None, 0, None, 0, None), -2),
     (("spmla_topk_local", None, 0, None, 1, 0, 1, 100, 4096, None, None), -5),
     (("spmla_topk_local", None, 0, None, 1, 2, 2, 100, 16, None, None), -2),
     (("spmla_topk_merge", None, 4, 2, 16, 33, 33, None, 0, None), -2),
@@ -50,6 +52,15 @@ def test_version():
 def test_argument_rejection(call, code):
     from arcagi2_flashnext_dots3_amd import _lib
     assert getattr(_lib.lib(), call[0])(*call[1:]) == code
+
+
+def test_topk_workspace_size():
+    from arcagi2_flashnext_dots3_amd import _lib
+    L = _lib.lib()
+    assert L.spmla_topk_ws_bytes(-1, 10, 16) == 0
+    one = L.spmla_topk_ws_bytes(1, 32768, 2048)
+    assert one > 0 and one % 16 == 0 and L.spmla_topk_ws_bytes(64, 32768, 2048) == 64 * one
+    assert L.spmla_topk_ws_bytes(1, 131072, 2048) > one          # more chunks per row, more histograms
 
 
 def test_zero_sized_calls_are_noops():

@@ -51,13 +51,15 @@ def test_index_logits(dev, rows, L, seed):
 
 
 def _topk_check(dev, lg, ctx, K):
+    """Both top-k paths (several workgroups per row with a workspace; one workgroup per row) against the oracle."""
     from arcagi2_flashnext_dots3_amd import kernels
-    out = kernels.topk(torch.from_numpy(lg).to(dev), torch.from_numpy(ctx).to(dev), K)
-    torch.cuda.synchronize()
-    got = out.cpu().numpy()
     exp = ref.topk(lg, ctx, K)
-    bad = np.where((got != exp).any(1))[0]
-    assert bad.size == 0, f"rows {bad[:8]} differ"
+    for single in (False, True):
+        out = kernels.topk(torch.from_numpy(lg).to(dev), torch.from_numpy(ctx).to(dev), K, single_pass=single)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        bad = np.where((got != exp).any(1))[0]
+        assert bad.size == 0, f"single_pass={single}: rows {bad[:8]} differ"
 
 
 def test_topk_random_and_lengths(dev):
