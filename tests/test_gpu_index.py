@@ -94,6 +94,20 @@ def test_topk_ties_and_specials(dev):
     _topk_check(dev, lg, ctx, 2048)
 
 
+def test_topk_concentrated_values(dev):
+    """Logits like the indexer's (mean 280, sd 56): the first 11-bit digit bin of the 2048th value holds more than
+    4096 keys, so the workspace path narrows a second level across workgroups; one row of few distinct values falls
+    back to the one-workgroup selection; L = 40000 leaves a short last chunk."""
+    g = np.random.default_rng(5)
+    rows, L = 8, 40000
+    lg = (280.0 + 56.0 * g.standard_normal((rows, L))).astype(np.float32)
+    lg[1] = np.round(lg[1] / 64) * 64                                   # a handful of distinct values
+    ctx = np.full(rows, L, dtype=np.int32)
+    ctx[2] = 33000
+    print("[topk] concentrated", flush=True)
+    _topk_check(dev, lg, ctx, 2048)
+
+
 def test_topk_ctx_lengths_fixture(dev):
     # context lengths from the reference's own fixture (runtime_dataset/ctx_lengths.json), clipped to L
     with open(os.path.join(HERE, "golden", "ctx_lengths.json")) as f:
