@@ -181,13 +181,15 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   const int* idxrow = p.idx + (long long)t * p.idx_st + kb;
   const int h = hg * HG + l32;
   const bool hval = h < p.H;
-  auto row_id = [&](int tile) -> int {        // row id of this lane's row in `tile` (-1: none / invalid)
+  auto row_raw = [&](int tile) -> int {       // index entry of this lane's row in `tile` (-1: past the end)
     const int i = tile * TR + l32;
     int x = -1;
     if (i < nrow) x = idxrow[i];
-    return (x >= 0 && (long long)x < p.R) ? x : -1;
+    return x;
   };
-  int rcur = row_id(w), rnxt = row_id(w + NW);
+  auto row_ok = [&](int x) -> int { return (x >= 0 && (long long)x < p.R) ? x : -1; };   // -1: none / invalid
+  int rcur = row_ok(row_raw(w)), rnxt = row_ok(row_raw(w + NW));
+  int rnn = -1;                        // raw entry two tiles ahead: loaded in one iteration, checked in the next
   {
     u32x4 qv[HG * QPIECES / 256];
 #pragma unroll
@@ -261,7 +263,10 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
 #pragma unroll
     for (int kq = 0; kq < 4; ++kq) kr[kq] = *(SPMLA_LDS u32x4*)(tb + (2 * kq + half) * 512 + l32 * 16);
     const bool more = j + 1 < ntw;
-    const int rnn = j + 2 < ntw ? row_id(tix + 2 * NW) : -1;   // row ids two tiles ahead (used next iteration)
+    // the entries loaded one iteration ago are checked only now, after the wait above: checking them where they
+    // are loaded would stall every tile on a global-memory round trip
+    if (j > 0) rnxt = row_ok(rnn);
+    rnn = j + 2 < ntw ? row_raw(tix + 2 * NW) : -1;
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- rope part of S^T (operands in VGPRs / LDS)
@@ -413,7 +418,6 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
       }
     }
     rcur = rnxt;
-    rnxt = rnn;
   }
 
   // ---- merge the 4 waves: per head M = max m_w, L = sum l_w 2^(m_w - M), O = sum O_w 2^(m_w - M) / L
