@@ -30,6 +30,9 @@ SIGNATURES = {
     "spmla_gather_pcie": [P, LL, I, P, I, P, LL, P],
     "spmla_gather_tiers": [P, LL, I, P, LL, P, I, I, P, LL, P],
     "spmla_copy_rows": [P, LL, P, P, LL, P, I, I, P],
+    "spmla_row400_gather": [P, LL, P, I, P, LL, I, I, P],
+    "spmla_row400_copy": [P, LL, P, P, LL, P, I, I, P],
+    "spmla_row400_gather_tiers": [P, LL, P, LL, P, I, I, P, LL, I, P],
     "spmla_tier_split": [P, LL, I, I, P, LL, P, LL, P, P, LL, P, P],
     "spmla_compact_stage": [P, I, P, LL, I, I, P, P, P, P, LL, P],
     "spmla_attn_splitk": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, I, P, LL, LL, P, LL, P, P, P],

@@ -79,6 +79,26 @@ __host__ __device__ inline float e4m3_to_f32(uint8_t c) {
   return u2f(s | ((e + 120u) << 23) | (m << 20));
 }
 
+// ---- Row400: the reference's compact e2m2b32 host row (dotsnote/engine/arcstats_pkg/arcstats/offload_rowfmt.py:1-22)
+// [256 B low nibbles | 64 B sign bits | 16 x int8 block exponent k | 64 B e4m3fn rope]. Latent value e (0..511) has the
+// 5-bit code (sign << 4) | mag, mag = nibble e % 2 of byte e / 2, sign = bit e % 8 of byte 256 + e / 8; the 32
+// values of block b = e / 32 share k = byte 320 + b. mag = (e2 << 2) | m: value = (e2 ? 4 + m : m) *
+// 2^(max(e2, 1) - 3 + k) (exponent clamped to [-126, 127]), clamped to +-448; the row's GPU form is the e4m3 code
+// of that value (offload_rowfmt.py:131-160), exact whenever it lies in e4m3's range.
+constexpr int ROW400 = 400, R4_SIGN = 256, R4_K = 320, R4_ROPE = 336;
+
+// e2m2 code (5 bits) and block exponent -> e4m3fn code of the dequantized value (offload_rowfmt.py:149-158).
+__host__ __device__ inline uint8_t e2m2_to_e4m3(uint32_t code, int k) {
+  const uint32_t mag = code & 15u, e2 = mag >> 2, mm = mag & 3u;
+  const uint32_t mant = e2 ? mm + 4u : mm;
+  int ex = (e2 > 1u ? (int)e2 : 1) - 3 + k;
+  ex = ex < -126 ? -126 : (ex > 127 ? 127 : ex);
+  float v = (float)mant * u2f((uint32_t)(ex + 127) << 23);
+  v = v > 448.f ? 448.f : v;                       // v >= 0 (or +inf, which the clamp also catches)
+  const uint8_t c = e4m3_rne(v);
+  return (uint8_t)(c | ((code & 16u) << 3));     // the sign survives rounding to zero (-0 -> 0x80)
+}
+
 // ---- XCD-aware workgroup order ---------------------------------------------------------------------------
 // The dispatcher hands workgroup i to XCD (i % 8). remap_xcd(i, n) gives the logical work index so that
 // each XCD receives a contiguous block of ceil(n / 8) logical items: consecutive logical items (e.g. the

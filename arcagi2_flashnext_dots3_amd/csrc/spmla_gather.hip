@@ -7,48 +7,173 @@
 // (dsa_sm89.py:27-35: distinct selected positions, sorted, and the selection remapped into them).
 //
 // Rows are moved in 16-byte chunks, a wave per row for the gather: the same code serves HBM sources and pinned host
-// memory mapped into the device address space (reads then cross PCIe).
+// memory mapped into the device address space (reads then cross PCIe). The gathers also read the reference's compact
+// Row400 host rows (offload_rowfmt.py: _rows_kernel / _put_rows / _copy_kernel, :163-275) and write them out in the
+// GPU row formats, decoded on the way.
 #include "spmla_common.h"
 
 namespace spmla {
 namespace gth {
 
-// dst row i = src row rows[i] (0 <= rows[i] < R), zero row otherwise; row_bytes % 16 == 0. One wave per row, lane
-// c moving 16-byte chunks c, c + 64, ...: each row is read as one contiguous run per instruction, which measured
-// 45.5 GB/s from pinned host memory over PCIe for 656-byte rows against 42.2 GB/s with consecutive threads taking
-// consecutive chunks across row boundaries (the rows' start addresses then split more requests).
-__global__ void __launch_bounds__(256) gather_kernel(const uint8_t* src, long long R, int row_bytes,
-                                                     const long long* rows, int n, uint8_t* dst, long long dst_stride) {
-  const int lane = threadIdx.x & 63;
-  const int chunks = row_bytes >> 4;
-  for (int i = blockIdx.x * 4 + (int)(threadIdx.x >> 6); i < n; i += gridDim.x * 4) {
-    const long long r = rows[i];
-    const bool ok = r >= 0 && r < R;
-    const uint8_t* s = src + (ok ? r : 0) * row_bytes;
-    uint8_t* d = dst + (long long)i * dst_stride;
-    for (int c = lane; c < chunks; c += 64) {
-      u32x4 v = u32x4{0, 0, 0, 0};
-      if (ok) v = *(const u32x4*)(s + c * 16);
-      *(u32x4*)(d + c * 16) = v;
+// Row reads: one 16-byte chunk per lane through a buffer resource that spans exactly the row (none for a zero row),
+// so the load has no branch: lanes past the row's end, and every lane of an absent row, read zeros. A branch-free
+// load keeps the compiler's vmcnt accounting exact, which the two-rows-in-flight loops below depend on (a load
+// under a branch makes every later wait drain all loads). The row address is wave-uniform (readfirstlane).
+__device__ inline u32x4 load_row(const uint8_t* s, int bytes, int lane) {
+  const uint64_t a = (uint64_t)(uintptr_t)s;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const int nb = __builtin_amdgcn_readfirstlane(s ? bytes : 0);
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)(((uint64_t)hi << 32) | lo), (short)0, nb, 0x00020000);
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16, 0, 0));
+}
+
+// Row operations of the wave-per-row kernels. load() issues the reads of one source row (nullptr: a zero row) into
+// registers, one 16-byte chunk per lane (rows of at most 64 chunks); emit() writes the destination row from them.
+// The kernels keep two rows in flight per wave: the next row's load is issued before the current row is emitted,
+// and its row id one step earlier still, so a wave waits on one memory round trip per row, not two.
+struct CopyRow {                 // byte copy
+  int chunks;                    // <= 64
+  static constexpr int LDS = 0;  // LDS bytes per wave
+  __device__ u32x4 load(const uint8_t* s, int lane) const { return load_row(s, chunks * 16, lane); }
+  __device__ void emit(u32x4 v, bool, uint8_t* d, int lane, SPMLA_LDS uint8_t*) const {
+    if (lane < chunks) *(u32x4*)(d + lane * 16) = v;
+  }
+};
+
+// e2m2 code -> e4m3 code for a block exponent k >= -4, where every nonzero magnitude lands in e4m3's normal range
+// (or above 448, clamped to 0x7e): the value's exponent and its 2 mantissa bits move over as they are. Equal to
+// e2m2_to_e4m3 on that range.
+__device__ inline uint32_t e2m2_to_e4m3_normal(uint32_t code, int k) {
+  const uint32_t mag = code & 15u, e2 = mag >> 2, m = mag & 3u;
+  int E;
+  uint32_t mt;
+  if (e2) { E = (int)e2 + k + 6; mt = m << 1; }              // (4 + m) 2^(e2 - 3 + k) = (1 + m / 4) 2^(e2 - 1 + k)
+  else { E = k + 5 + (m > 1u); mt = m == 3u ? 4u : 0u; }     // m 2^(k - 2): 2^(k - 2), 2^(k - 1), 1.5 * 2^(k - 1)
+  uint32_t c = mag == 0u ? 0u : (E > 15 ? 0x7eu : ((uint32_t)E << 3) | mt);
+  return c | ((code & 16u) << 3);
+}
+
+// Row400 -> Row656 (fmt 0: the e4m3 codes, scales 1.0, the rope widened to bf16, which holds every e4m3 value
+// exactly; the two NaN codes widen to the canonical bf16 NaN 0x7fc0, as torch's float8_e4m3fn -> bfloat16 does)
+// or Row576 (fmt 1: the reference's GPU row, offload_rowfmt.py:163-171). The row arrives as 25 chunks in lanes
+// 0..24 and is spread through the wave's LDS slot: lane l then decodes latent values 8l .. 8l + 7 (nibble dword l,
+// sign byte l, block exponent l / 4) and lanes 0..15 move 4 rope codes each. An invalid source gives a zero row
+// (scales 0, like the byte gather).
+struct DecodeRow400 {
+  int fmt;
+  static constexpr int LDS = 416;
+  __device__ u32x4 load(const uint8_t* s, int lane) const { return load_row(s, ROW400, lane); }
+  __device__ void emit(u32x4 v, bool valid, uint8_t* d, int lane, SPMLA_LDS uint8_t* w) const {
+    if (lane < ROW400 / 16) *(SPMLA_LDS u32x4*)(w + 16 * lane) = v;
+    // LDS instructions of one wave complete in order: the reads below see every lane's write above
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const uint32_t lo = *(const SPMLA_LDS uint32_t*)(w + 4 * lane);
+    const uint32_t sg = w[R4_SIGN + lane];
+    const int k = (int)(int8_t)w[R4_K + (lane >> 2)];
+    const uint32_t rp = lane < 16 ? *(const SPMLA_LDS uint32_t*)(w + R4_ROPE + 4 * lane) : 0u;
+    uint32_t c[2] = {0u, 0u};
+    if (k >= -4) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t code = ((lo >> (4 * i)) & 15u) | (((sg >> i) & 1u) << 4);
+        c[i >> 2] |= e2m2_to_e4m3_normal(code, k) << (8 * (i & 3));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t code = ((lo >> (4 * i)) & 15u) | (((sg >> i) & 1u) << 4);
+        c[i >> 2] |= (uint32_t)e2m2_to_e4m3(code, k) << (8 * (i & 3));
+      }
     }
+    *(uint2*)(d + 8 * lane) = make_uint2(c[0], c[1]);
+    if (fmt == 0) {
+      if (lane < 4) *(float*)(d + SC_OFF + 4 * lane) = valid ? 1.0f : 0.0f;
+      if (lane < 16) {
+        uint32_t b[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint8_t x = (uint8_t)(rp >> (8 * e));
+          b[e] = (x & 0x7fu) == 0x7fu ? 0x7fc0u : f2u(e4m3_to_f32(x)) >> 16;
+        }
+        *(uint2*)(d + ROPE_OFF + 8 * lane) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+      }
+    } else if (lane < 16) {
+      *(uint32_t*)(d + D_LAT + 4 * lane) = rp;
+    }
+  }
+};
+
+__device__ inline long long readlane64(long long x, int j) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)x, j), hi = __builtin_amdgcn_readlane((uint32_t)(x >> 32), j);
+  return (long long)(((uint64_t)hi << 32) | lo);
+}
+
+// The rows of one wave are processed in batches of up to 64: lane j of the wave first reads the ids of the batch's
+// row j (one vector load for the whole batch, one memory round trip per 64 rows), then the rows are streamed with
+// the next row's data load issued before the current row is emitted (two rows in flight per wave).
+template <class Op>
+__device__ inline void stream_batch(const Op& op, const uint8_t* src, long long R, int src_bytes, long long r_l,
+                                    long long d_l, bool skip_invalid, long long R_dst, int nb, uint8_t* dst,
+                                    long long dst_stride, int lane, SPMLA_LDS uint8_t* wl) {
+  auto src_of = [&](long long r) -> const uint8_t* { return (r >= 0 && r < R) ? src + r * src_bytes : nullptr; };
+  long long r = readlane64(r_l, 0);
+  u32x4 cur = op.load(src_of(r), lane);
+  for (int j = 0; j < nb; ++j) {
+    const long long rn = j + 1 < nb ? readlane64(r_l, j + 1) : -1;
+    const u32x4 nxt = op.load(src_of(rn), lane);
+    const long long d = readlane64(d_l, j);
+    const bool ok = r >= 0 && r < R;
+    if (!skip_invalid || (ok && d >= 0 && d < R_dst)) op.emit(cur, ok, dst + d * dst_stride, lane, wl);
+    cur = nxt;
+    r = rn;
+  }
+}
+
+// dst row i (or dst_rows[i]) = src row rows[i] (0 <= rows[i] < R), zero row otherwise. One wave per row, lane c
+// moving 16-byte chunk c: each row is read as one contiguous run per instruction, which measured 45.5 GB/s from
+// pinned host memory over PCIe for 656-byte rows against 42.2 GB/s with consecutive threads taking consecutive chunks
+// across row boundaries (the rows' start addresses then split more requests). With dst_rows, pairs whose
+// destination is outside [0, R_dst) or whose source is invalid are skipped instead.
+template <class Op>
+__global__ void __launch_bounds__(256) gather_kernel(const uint8_t* __restrict__ src, long long R, int src_bytes,
+                                                     const long long* __restrict__ rows, int n,
+                                                     uint8_t* __restrict__ dst, long long dst_stride,
+                                                     const long long* __restrict__ dst_rows, long long R_dst, Op op) {
+  __shared__ __attribute__((aligned(16))) uint8_t wl_all[4 * Op::LDS + 16];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  SPMLA_LDS uint8_t* wl = (SPMLA_LDS uint8_t*)wl_all + wv * Op::LDS;
+  const int step = gridDim.x * 4;
+  for (int i0 = blockIdx.x * 4 + wv; i0 < n; i0 += 64 * step) {
+    const int il = i0 + lane * step;                  // this lane's row of the batch
+    long long r_l = -1, d_l = il;
+    if (il < n) {
+      r_l = rows[il];
+      if (dst_rows) d_l = dst_rows[il];
+    }
+    const int nb = min(64, (n - i0 + step - 1) / step);
+    stream_batch(op, src, R, src_bytes, r_l, d_l, dst_rows != nullptr, R_dst, nb, dst, dst_stride, lane, wl);
   }
 }
 
 // Host-tier staging: dst row t * K + k = src row rows[t][k] for k < counts[t] (zero row if rows[t][k] is outside
 // [0, R)); other rows untouched, except that row 0 is zeroed when token 0 has no rows (the attention reads row 0 of
 // its pool for masked entries, which must then be finite). Persistent grid: tokens are taken 1024 at a time, the
-// counts' prefix sum goes to LDS and every wave copies rows v = wave, wave + waves, ... of the chunk, locating its
-// token by binary search in the prefix (uniform per wave).
-__global__ void __launch_bounds__(256) gather_tiers_kernel(const uint8_t* src, long long R, int row_bytes,
-                                                           const int* rows, long long r_st, const int* counts, int T,
-                                                           int K, uint8_t* dst, long long dst_stride) {
+// counts' prefix sum goes to LDS and every wave copies entries v = wave, wave + waves, ... of the chunk, each lane
+// locating its batch entry's token by binary search in the prefix.
+template <class Op>
+__global__ void __launch_bounds__(256) gather_tiers_kernel(const uint8_t* __restrict__ src, long long R, int src_bytes,
+                                                           const int* __restrict__ rows, long long r_st,
+                                                           const int* __restrict__ counts, int T, int K,
+                                                           uint8_t* __restrict__ dst, long long dst_stride, Op op) {
   __shared__ int pre[1025];
   __shared__ int wsum[4];
+  __shared__ __attribute__((aligned(16))) uint8_t wl_all[4 * Op::LDS + 16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int chunks = row_bytes >> 4;
-  const int nw = gridDim.x * 4, gw = blockIdx.x * 4 + wv;
-  if (gw == 0 && counts[0] <= 0)
-    for (int c = lane; c < chunks; c += 64) *(u32x4*)(dst + c * 16) = u32x4{0, 0, 0, 0};
+  const int wu = __builtin_amdgcn_readfirstlane(wv);
+  SPMLA_LDS uint8_t* wl = (SPMLA_LDS uint8_t*)wl_all + wu * Op::LDS;
+  const int nw = gridDim.x * 4, gw = blockIdx.x * 4 + wu;
+  if (gw == 0 && counts[0] <= 0) op.emit(op.load(nullptr, lane), false, dst, lane, wl);
   for (int t0 = 0; t0 < T; t0 += 1024) {
     const int nt = min(1024, T - t0);
     // inclusive prefix of clamp(counts[t0 + t], 0, K): thread tid sums tokens 4 tid .. 4 tid + 3
@@ -79,23 +204,22 @@ __global__ void __launch_bounds__(256) gather_tiers_kernel(const uint8_t* src, l
     }
     __syncthreads();
     const int tot = pre[nt];
-    for (int v = gw; v < tot; v += nw) {
-      int lo = 0, hi = nt - 1;                       // largest t with pre[t] <= v
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (pre[mid] <= v) lo = mid;
-        else hi = mid - 1;
+    for (int v0 = gw; v0 < tot; v0 += 64 * nw) {
+      const int vl = v0 + lane * nw;                 // this lane's entry of the batch
+      long long r_l = -1, d_l = 0;
+      if (vl < tot) {
+        int lo = 0, hi = nt - 1;                     // largest t with pre[t] <= vl
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (pre[mid] <= vl) lo = mid;
+          else hi = mid - 1;
+        }
+        const int t = t0 + lo, k = vl - pre[lo];
+        r_l = rows[(long long)t * r_st + k];
+        d_l = (long long)t * K + k;
       }
-      const int t = t0 + lo, k = v - pre[lo];
-      const long long r = rows[(long long)t * r_st + k];
-      const bool ok = r >= 0 && r < R;
-      const uint8_t* sp = src + (ok ? r : 0) * row_bytes;
-      uint8_t* d = dst + ((long long)t * K + k) * dst_stride;
-      for (int c = lane; c < chunks; c += 64) {
-        u32x4 x = u32x4{0, 0, 0, 0};
-        if (ok) x = *(const u32x4*)(sp + c * 16);
-        *(u32x4*)(d + c * 16) = x;
-      }
+      const int nb = min(64, (tot - v0 + nw - 1) / nw);
+      stream_batch(op, src, R, src_bytes, r_l, d_l, false, 0ll, nb, dst, dst_stride, lane, wl);
     }
     __syncthreads();                                 // pre[] is rewritten for the next chunk
   }
@@ -235,13 +359,15 @@ extern "C" {
 static int gather_launch(const void* src, long long R, int row_bytes, const long long* rows, int n, void* dst,
                          long long dst_stride, unsigned max_wg, void* stream) {
   if (n < 0 || R < 0 || row_bytes <= 0 || (row_bytes & 15)) return SPMLA_EARG;
+  if (row_bytes > 1024) return SPMLA_ELIMIT;          // one 16-byte chunk per lane
   if (n == 0) return SPMLA_OK;
   if (!src || !rows || !dst) return SPMLA_EARG;
   if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < row_bytes) return SPMLA_EALIGN;
   unsigned grid = (unsigned)((n + 3) / 4);
   if (grid > max_wg) grid = max_wg;
-  hipLaunchKernelGGL(gth::gather_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src, R,
-                     row_bytes, rows, n, (uint8_t*)dst, dst_stride);
+  hipLaunchKernelGGL(gth::gather_kernel<gth::CopyRow>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)src, R, row_bytes, rows, n, (uint8_t*)dst, dst_stride, (const long long*)nullptr,
+                     0ll, gth::CopyRow{row_bytes >> 4});
   return (int)hipGetLastError();
 }
 
@@ -253,11 +379,57 @@ int spmla_gather(const void* src, long long R, int row_bytes, const long long* r
 int spmla_gather_tiers(const void* src, long long R, int row_bytes, const int* rows, long long r_st, const int* counts,
                        int T, int K, void* dst, long long dst_stride, void* stream) {
   if (T < 0 || K < 0 || R < 0 || row_bytes <= 0 || (row_bytes & 15) || r_st < K) return SPMLA_EARG;
+  if (row_bytes > 1024) return SPMLA_ELIMIT;
   if (T == 0 || K == 0) return SPMLA_OK;
   if (!src || !rows || !counts || !dst) return SPMLA_EARG;
   if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < row_bytes) return SPMLA_EALIGN;
-  hipLaunchKernelGGL(gth::gather_tiers_kernel, dim3(64), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src, R,
-                     row_bytes, rows, r_st, counts, T, K, (uint8_t*)dst, dst_stride);
+  hipLaunchKernelGGL(gth::gather_tiers_kernel<gth::CopyRow>, dim3(64), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)src, R, row_bytes, rows, r_st, counts, T, K, (uint8_t*)dst, dst_stride,
+                     gth::CopyRow{row_bytes >> 4});
+  return (int)hipGetLastError();
+}
+
+// ---- Row400 (compact host rows) in, Row656 / Row576 out
+static int row400_dst_bytes(int dst_fmt) { return dst_fmt == 0 ? ROW656 : (dst_fmt == 1 ? ROW576 : 0); }
+
+int spmla_row400_gather(const void* src, long long R, const long long* rows, int n, void* dst, long long dst_stride,
+                        int dst_fmt, int pcie, void* stream) {
+  const int db = row400_dst_bytes(dst_fmt);
+  if (n < 0 || R < 0 || db == 0) return SPMLA_EARG;
+  if (n == 0) return SPMLA_OK;
+  if (!src || !rows || !dst) return SPMLA_EARG;
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < db) return SPMLA_EALIGN;
+  unsigned grid = (unsigned)((n + 3) / 4);
+  if (pcie && grid > 64u) grid = 64u;
+  hipLaunchKernelGGL(gth::gather_kernel<gth::DecodeRow400>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)src, R, ROW400, rows, n, (uint8_t*)dst, dst_stride, (const long long*)nullptr,
+                     0ll, gth::DecodeRow400{dst_fmt});
+  return (int)hipGetLastError();
+}
+
+int spmla_row400_copy(const void* src, long long R_src, const long long* src_rows, void* dst, long long R_dst,
+                      const long long* dst_rows, int n, int dst_fmt, void* stream) {
+  const int db = row400_dst_bytes(dst_fmt);
+  if (n < 0 || R_src < 0 || R_dst < 0 || db == 0) return SPMLA_EARG;
+  if (n == 0) return SPMLA_OK;
+  if (!src || !dst || !src_rows || !dst_rows) return SPMLA_EARG;
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15)) return SPMLA_EALIGN;
+  hipLaunchKernelGGL(gth::gather_kernel<gth::DecodeRow400>, dim3((unsigned)((n + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)src, R_src, ROW400, src_rows, n, (uint8_t*)dst,
+                     (long long)db, dst_rows, R_dst, gth::DecodeRow400{dst_fmt});
+  return (int)hipGetLastError();
+}
+
+int spmla_row400_gather_tiers(const void* src, long long R, const int* rows, long long r_st, const int* counts, int T,
+                              int K, void* dst, long long dst_stride, int dst_fmt, void* stream) {
+  const int db = row400_dst_bytes(dst_fmt);
+  if (T < 0 || K < 0 || R < 0 || r_st < K || db == 0) return SPMLA_EARG;
+  if (T == 0 || K == 0) return SPMLA_OK;
+  if (!src || !rows || !counts || !dst) return SPMLA_EARG;
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < db) return SPMLA_EALIGN;
+  hipLaunchKernelGGL(gth::gather_tiers_kernel<gth::DecodeRow400>, dim3(64), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)src, R, ROW400, rows, r_st, counts, T, K, (uint8_t*)dst, dst_stride,
+                     gth::DecodeRow400{dst_fmt});
   return (int)hipGetLastError();
 }
 

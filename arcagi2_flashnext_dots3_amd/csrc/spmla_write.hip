@@ -6,6 +6,11 @@
 //   656-byte layout: dotsnote/engine/vllm_patch/vllm/v1/hisparse/runtime.py:35-36.
 // Row576 (the reference's deployed offload row, dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:252-270):
 //   code = e4m3fn_rne(clamp(x * inv_scale, -448, 448)) for the 512 latent and the 64 rope values.
+// Row400 (the reference's compact e2m2b32 host row, dotsnote/engine/arcstats_pkg/arcstats/offload_rowfmt.py:81-129,
+//   torch statement ref_quant / ref_pack :336-388): x = clamp(v * inv_scale, +-448); per 32 values
+//   k = smallest integer with 2^k >= amax / 7 (fp32 amax / 7; zero or subnormal quotients give k = -126), y = |x| 2^-k,
+//   mag = floor(4y + 0.5) for y < 1, else ((e2 + 1) << 2) + floor(y / 2^(e2 - 2) + 0.5) - 4 with e2 = [y >= 2] +
+//   [y >= 4], capped at 15; the sign bit is set for x < 0 with mag > 0. Rope as in Row576.
 // Index key (dotsnote/engine/arcstats_pkg/arcstats/shard_indexer.py:42-60): s = max(amax, 1e-4) / 448 (optionally
 //   rounded up to a power of two, UE8M0), code = e4m3fn_rne(k / s); 132-byte row [128 codes | fp32 s].
 //
@@ -23,13 +28,23 @@ __device__ inline float wave_max16(float v) {   // max over aligned groups of 16
   return v;
 }
 
+// e2m2 magnitude index of y = |x| 2^-k >= 0 (offload_rowfmt.py:93-101 with M = 2). The products are exact
+// (powers of two), so the one rounding is the fp32 add of 0.5, as in the reference.
+__device__ inline uint32_t e2m2_mag(float y) {
+  if (y < 1.0f) return (uint32_t)floorf(y * 4.0f + 0.5f);       // 0 .. 4
+  const int e2 = (y >= 2.0f) + (y >= 4.0f);
+  const float inv_stp = u2f((uint32_t)(127 + 2 - e2) << 23);     // 2^(2 - e2)
+  const uint32_t nrm = ((uint32_t)(e2 + 1) << 2) + (uint32_t)floorf(y * inv_stp + 0.5f) - 4u;
+  return nrm < 15u ? nrm : 15u;
+}
+
 struct WriteParams {
   const uint16_t* kv; long long kv_st;      // kv_c_normed[n][512] bf16
   const uint16_t* pe; long long pe_st;      // k_pe[n][64] bf16
   const long long* slots; int n;
   uint8_t* cache; long long R; int bs; long long blk_stride;   // row of slot: (slot / bs) * blk_stride + (slot % bs) * row
-  int fmt;                                  // 0: Row656, 1: Row576
-  float inv_scale;                          // Row576 only
+  int fmt;                                  // 0: Row656, 1: Row576, 2: Row400
+  float inv_scale;                          // Row576 / Row400
 };
 
 __global__ void __launch_bounds__(256) cache_write_kernel(WriteParams p) {
@@ -38,7 +53,7 @@ __global__ void __launch_bounds__(256) cache_write_kernel(WriteParams p) {
   if (tok >= p.n) return;
   const long long slot = p.slots[tok];
   if (slot < 0 || slot >= p.R) return;
-  const int rowb = p.fmt == 0 ? ROW656 : ROW576;
+  const int rowb = p.fmt == 0 ? ROW656 : (p.fmt == 1 ? ROW576 : ROW400);
   uint8_t* row = p.cache + (slot / p.bs) * p.blk_stride + (slot % p.bs) * rowb;
   const uint16_t* src = p.kv + (long long)tok * p.kv_st + lane * 8;
   const u32x4 raw = *(const u32x4*)src;
@@ -62,6 +77,39 @@ __global__ void __launch_bounds__(256) cache_write_kernel(WriteParams p) {
     if (lane < 16) {   // rope: 64 bf16 = 16 x 8 bytes
       const uint2 r = *(const uint2*)(p.pe + (long long)tok * p.pe_st + lane * 4);
       *(uint2*)(row + ROPE_OFF + lane * 8) = r;
+    }
+  } else if (p.fmt == 2) {
+    // Row400: lane l holds values 8l .. 8l + 7; the 4 lanes 4b .. 4b + 3 form exponent block b
+    float am = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = fminf(fmaxf(x[e] * p.inv_scale, -448.f), 448.f);
+      am = fmaxf(am, fabsf(x[e]));
+    }
+    am = fmaxf(am, __shfl_xor(am, 1, 64));
+    am = fmaxf(am, __shfl_xor(am, 2, 64));
+    const uint32_t rb = f2u(am / 7.0f);
+    const int ex = (int)((rb >> 23) & 255u) - 127;
+    int k = ex + ((rb & 0x7fffffu) != 0u);
+    k = ex < -126 ? -126 : (k < 127 ? k : 127);
+    const float inv = u2f((uint32_t)(127 - k) << 23);                // 2^-k
+    uint32_t nib = 0, sgn = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t mag = e2m2_mag(fabsf(x[e]) * inv);
+      nib |= mag << (4 * e);
+      sgn |= (x[e] < 0.f && mag > 0u ? 1u : 0u) << e;
+    }
+    *(uint32_t*)(row + 4 * lane) = nib;
+    row[R4_SIGN + lane] = (uint8_t)sgn;
+    if ((lane & 3) == 0) row[R4_K + (lane >> 2)] = (uint8_t)(int8_t)k;
+    if (lane < 16) {   // rope: 64 values -> 64 e4m3 codes, 4 per lane
+      const uint2 r = *(const uint2*)(p.pe + (long long)tok * p.pe_st + lane * 4);
+      const float y[4] = {u2f(r.x << 16), u2f(r.x & 0xffff0000u), u2f(r.y << 16), u2f(r.y & 0xffff0000u)};
+      uint32_t c = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c |= (uint32_t)e4m3_rne(fminf(fmaxf(y[e] * p.inv_scale, -448.f), 448.f)) << (8 * e);
+      *(uint32_t*)(row + R4_ROPE + lane * 4) = c;
     }
   } else {
 #pragma unroll
@@ -125,17 +173,17 @@ extern "C" {
 int spmla_cache_write(const void* kv_c, long long kv_st, const void* k_pe, long long pe_st, const long long* slots,
                       int n, void* cache, long long R, int block_size, long long block_stride, int fmt,
                       float kv_scale, void* stream) {
-  if (n < 0 || R < 0 || (fmt != 0 && fmt != 1) || block_size <= 0) return SPMLA_EARG;
+  if (n < 0 || R < 0 || fmt < 0 || fmt > 2 || block_size <= 0) return SPMLA_EARG;
   if (n == 0) return SPMLA_OK;
   if (!kv_c || !k_pe || !slots || !cache) return SPMLA_EARG;
   if (((uintptr_t)kv_c & 15) || (kv_st & 7) || ((uintptr_t)k_pe & 7) || (pe_st & 3)) return SPMLA_EALIGN;
-  const int rowb = fmt == 0 ? ROW656 : ROW576;
+  const int rowb = fmt == 0 ? ROW656 : (fmt == 1 ? ROW576 : ROW400);
   if (((uintptr_t)cache & 7) || (block_stride & 7) || block_stride < (long long)block_size * rowb) return SPMLA_EALIGN;
-  if (fmt == 1 && !(kv_scale > 0.f)) return SPMLA_EARG;
+  if (fmt != 0 && !(kv_scale > 0.f)) return SPMLA_EARG;
   wr::WriteParams p;
   p.kv = (const uint16_t*)kv_c; p.kv_st = kv_st; p.pe = (const uint16_t*)k_pe; p.pe_st = pe_st;
   p.slots = slots; p.n = n; p.cache = (uint8_t*)cache; p.R = R; p.bs = block_size; p.blk_stride = block_stride;
-  p.fmt = fmt; p.inv_scale = fmt == 1 ? 1.0f / kv_scale : 1.0f;
+  p.fmt = fmt; p.inv_scale = fmt != 0 ? 1.0f / kv_scale : 1.0f;
   hipLaunchKernelGGL(wr::cache_write_kernel, dim3((n + 3) / 4), dim3(256), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }

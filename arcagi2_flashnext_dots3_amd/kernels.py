@@ -9,7 +9,8 @@ import torch
 from . import _lib
 
 D_LAT, D_ROPE, D_QK = 512, 64, 576
-ROW656, ROW576, KEYROW = 656, 576, 132
+ROW656, ROW576, ROW400, KEYROW = 656, 576, 400, 132
+_ROWB = {0: ROW656, 1: ROW576, 2: ROW400}        # cache_write formats
 LOG2E = 1.4426950408889634
 
 
@@ -29,10 +30,12 @@ def _need(cond, msg):
 # ---------------------------------------------------------------------------------------------- cache write
 def cache_write(kv_c, k_pe, slots, cache, fmt=0, kv_scale=1.0, block_size=None, block_stride=None):
     """kv_c [n, 512] bf16, k_pe [n, 64] or [n, 1, 64] bf16, slots [n] int64 -> rows of `cache` (uint8, Row656
-    (fmt 0) or Row576 (fmt 1)). cache is [R, row] or paged [blocks, block_size, row] (block stride may be padded)."""
+    (fmt 0), Row576 (fmt 1) or Row400 (fmt 2, the compact e2m2b32 row)). cache is [R, row] or paged
+    [blocks, block_size, row] (block stride may be padded)."""
     kpe = k_pe.reshape(k_pe.shape[0], -1)
     n = min(kv_c.shape[0], slots.shape[0])
-    rowb = ROW656 if fmt == 0 else ROW576
+    _need(fmt in _ROWB, f"fmt must be one of {sorted(_ROWB)}")
+    rowb = _ROWB[fmt]
     _need(kv_c.dtype == torch.bfloat16 and kpe.dtype == torch.bfloat16, "kv_c / k_pe must be bf16")
     _need(kv_c.shape[1] == D_LAT and kpe.shape[1] == D_ROPE and kv_c.stride(1) == 1 and kpe.stride(1) == 1,
           "kv_c [n, 512] / k_pe [n, 64] with contiguous rows")
@@ -175,6 +178,42 @@ def gather_tiers(src, rows, counts, out, R=None):
     _lib.call("spmla_gather_tiers", src.data_ptr() if torch.is_tensor(src) else int(src),
               int(R if R is not None else src.shape[0]), out.shape[-1], rows.data_ptr(), rows.stride(0),
               counts.data_ptr(), T, K, out.data_ptr(), out.stride(0), _stream(out))
+    return out
+
+
+def _dst_fmt(out):
+    _need(out.dtype == torch.uint8 and out.shape[-1] in (ROW656, ROW576), "out rows: uint8 Row656 or Row576")
+    return 0 if out.shape[-1] == ROW656 else 1
+
+
+def row400_gather(src, rows, out, R=None, pcie=False):
+    """out[i] = the GPU row (Row656 or Row576, by out's row width) of compact Row400 row src[rows[i]]; zero row when
+    rows[i] is outside [0, R). src [R, 400] uint8 (pinned host memory with pcie=True, or HBM)."""
+    n = rows.shape[0]
+    _need(rows.dtype == torch.int64, "rows int64")
+    _lib.call("spmla_row400_gather", src.data_ptr() if torch.is_tensor(src) else int(src),
+              int(R if R is not None else src.shape[0]), rows.data_ptr(), n, out.data_ptr(), out.stride(0),
+              _dst_fmt(out), int(bool(pcie)), _stream(out))
+    return out
+
+
+def row400_copy(src, src_rows, dst, dst_rows, R_src=None):
+    """dst[dst_rows[i]] = the GPU row of Row400 row src[src_rows[i]] (pairs with an invalid side skipped)."""
+    n = src_rows.shape[0]
+    _need(src_rows.dtype == torch.int64 and dst_rows.dtype == torch.int64, "int64 rows")
+    _lib.call("spmla_row400_copy", src.data_ptr() if torch.is_tensor(src) else int(src),
+              int(R_src if R_src is not None else src.shape[0]), src_rows.data_ptr(), dst.data_ptr(), dst.shape[0],
+              dst_rows.data_ptr(), n, _dst_fmt(dst), _stream(dst))
+
+
+def row400_gather_tiers(src, rows, counts, out, R=None):
+    """gather_tiers from compact Row400 host rows, decoded to out's row format (Row656 / Row576)."""
+    T, K = rows.shape
+    _need(rows.dtype == torch.int32 and rows.stride(1) == 1 and counts.dtype == torch.int32, "int32 rows / counts")
+    _need(out.shape[0] >= T * K, "out holds T * K rows")
+    _lib.call("spmla_row400_gather_tiers", src.data_ptr() if torch.is_tensor(src) else int(src),
+              int(R if R is not None else src.shape[0]), rows.data_ptr(), rows.stride(0), counts.data_ptr(), T, K,
+              out.data_ptr(), out.stride(0), _dst_fmt(out), _stream(out))
     return out
 
 

@@ -4,7 +4,9 @@
 Tiers
   host pool   [R, 656] uint8 Row656 rows in pinned host memory (torch's pinned allocator = hipHostMalloc; the kernels
               read and write it through its device-visible address, 16-byte accesses over PCIe). This replaces the
-              reference's cudaHostRegister'ed buffer (_HostReg, sparse_offload.py:917-980).
+              reference's cudaHostRegister'ed buffer (_HostReg, sparse_offload.py:917-980). With row_fmt="e2m2" the
+              pool holds the reference's compact Row400 rows instead (offload_rowfmt.py, ARC_OFFLOAD_ROW_FMT=e2m2):
+              every host read decodes them into Row656 on the way, so 39% fewer bytes cross PCIe per row.
   HBM cache   [C, 656] uint8 hot rows with tag[line] = host row and rowmap[row] = line (-1 = host only). The hot set
               is chosen by the caller (set_hot_rows, e.g. hot_rows_by_frequency over recent selections); the
               reference's dynamic W-way cache (offload_fill.py) is not part of this build.
@@ -19,6 +21,7 @@ import torch
 from . import kernels
 
 ROW = kernels.ROW656
+HOST_ROW = {"row656": kernels.ROW656, "e2m2": kernels.ROW400}
 
 
 def hot_rows_by_frequency(counts, C):
@@ -33,14 +36,19 @@ class LayerOffload:
     """One DSA layer's offloaded KV rows (reference LayerOffload, sparse_offload.py:1051).
 
     num_host_rows: R, the number of cache slots (every slot id written by store() is a host row id);
-    device: the GPU; key: the layer's cache prefix (identification only); cache_rows: C lines of HBM hot-row cache.
+    device: the GPU; key: the layer's cache prefix (identification only); cache_rows: C lines of HBM hot-row cache;
+    row_fmt: "row656" (host rows as the GPU reads them) or "e2m2" (the reference's compact Row400 host rows,
+    offload_rowfmt.py:1-22; values = code * kv_scale, so store and attend take the same kv_scale).
     """
 
-    def __init__(self, num_host_rows, device, key=None, cache_rows=0):
+    def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656"):
+        if row_fmt not in HOST_ROW:
+            raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         self.R = int(num_host_rows)
         self.device = torch.device(device)
         self.key = key
-        self.host = torch.zeros((self.R, ROW), dtype=torch.uint8, pin_memory=True)
+        self.row_fmt = row_fmt
+        self.host = torch.zeros((self.R, HOST_ROW[row_fmt]), dtype=torch.uint8, pin_memory=True)
         self.C = min(int(cache_rows), self.R)
         self.cache = torch.zeros((max(self.C, 1), ROW), dtype=torch.uint8, device=self.device)
         self.tag = torch.full((max(self.C, 1),), -1, dtype=torch.int64, device=self.device)
@@ -50,27 +58,41 @@ class LayerOffload:
     # ------------------------------------------------------------------------------------------------ rows in
     def store(self, kv_c_normed, k_pe, slots, kv_scale=1.0):
         """Quantize-and-pack n tokens (kv_c_normed [n, 512] bf16, k_pe [n, 64] / [n, 1, 64] bf16) into host rows
-        `slots` [n] int64 (reference LayerOffload.store, sparse_offload.py:1131-1155). Rows are Row656 (per-128
-        scales of their own); kv_scale is accepted for the reference's signature and must be 1. Cached copies of the
-        written rows are rewritten in HBM too (write-through), so both tiers hold identical bytes."""
+        `slots` [n] int64 (reference LayerOffload.store, sparse_offload.py:1131-1155). Row656 rows carry per-128
+        scales of their own and kv_scale must be 1; Row400 rows quantize x / kv_scale (offload_rowfmt.store). Cached
+        copies of the written rows are rewritten in HBM too (write-through), so both tiers hold the same values."""
         n = min(kv_c_normed.shape[0], slots.shape[0])
         if n == 0:
             return
-        if float(kv_scale) != 1.0:
+        compact = self.row_fmt == "e2m2"
+        if not compact and float(kv_scale) != 1.0:
             raise ValueError("LayerOffload.store: Row656 rows carry their own scales; kv_scale must be 1")
         kpe = k_pe.reshape(k_pe.shape[0], -1)
         slots = slots[:n].to(torch.int64)
-        kernels.cache_write(kv_c_normed[:n], kpe[:n], slots, self.host)
+        fmt = 2 if compact else 0
+        kernels.cache_write(kv_c_normed[:n], kpe[:n], slots, self.host, fmt=fmt, kv_scale=kv_scale)
         if self.C:
             ok = (slots >= 0) & (slots < self.R)
             lines = torch.where(ok, self.rowmap[slots.clamp(0, self.R - 1)].to(torch.int64), -1)
-            kernels.cache_write(kv_c_normed[:n], kpe[:n], lines, self.cache[:self.C])
+            if compact:
+                # the cache lines get the decoded compact rows: encode the same tokens again into HBM scratch (the
+                # encoder is deterministic) and decode them into their lines
+                tmp = self._buf("wt", (n, kernels.ROW400), torch.uint8)
+                ident = torch.arange(n, dtype=torch.int64, device=self.device)
+                kernels.cache_write(kv_c_normed[:n], kpe[:n], ident, tmp, fmt=2, kv_scale=kv_scale)
+                kernels.row400_copy(tmp, ident, self.cache[:self.C], lines)
+            else:
+                kernels.cache_write(kv_c_normed[:n], kpe[:n], lines, self.cache[:self.C])
 
     def gather(self, rows, out):
         """out[i] = host row rows[i] (int64; zero row when outside [0, R)); out [N, 656] uint8 in HBM
-        (reference LayerOffload.gather, sparse_offload.py:1157-1163)."""
+        (reference LayerOffload.gather, sparse_offload.py:1157-1163). Compact host rows are decoded to out's
+        format: [N, 656] Row656 or [N, 576] the reference's Row576 (offload_rowfmt.gather)."""
         if rows.shape[0]:
-            kernels.gather(self.host, rows.to(torch.int64), out, pcie=True)
+            if self.row_fmt == "e2m2":
+                kernels.row400_gather(self.host, rows.to(torch.int64), out, pcie=True)
+            else:
+                kernels.gather(self.host, rows.to(torch.int64), out, pcie=True)
         return out
 
     def set_hot_rows(self, rows):
@@ -85,7 +107,10 @@ class LayerOffload:
         m = rows.numel()
         if m:
             lines = torch.arange(m, dtype=torch.int64, device=self.device)
-            kernels.copy_rows(self.host, rows, self.cache[:self.C], lines)
+            if self.row_fmt == "e2m2":
+                kernels.row400_copy(self.host, rows, self.cache[:self.C], lines)
+            else:
+                kernels.copy_rows(self.host, rows, self.cache[:self.C], lines)
             self.tag[:m] = rows
             self.rowmap[rows] = lines.to(torch.int32)
 
@@ -141,8 +166,12 @@ class LayerOffload:
             mcnt = None
         # host tier: copy the missed rows over PCIe into HBM staging, then attend there
         staged = self._buf("staged", (T * K, ROW), torch.uint8)
+        compact = self.row_fmt == "e2m2"
         if not self.C:
-            kernels.gather(self.host, host.reshape(-1).to(torch.int64), staged, pcie=True)
+            if compact:
+                kernels.row400_gather(self.host, host.reshape(-1).to(torch.int64), staged, pcie=True)
+            else:
+                kernels.gather(self.host, host.reshape(-1).to(torch.int64), staged, pcie=True)
             sidx = self._buf("sidx", (T, K), torch.int32)
             ar = torch.arange(T * K, dtype=torch.int32, device=q.device).view(T, K)
             torch.where((host >= 0) & (host < self.R), ar, torch.full_like(ar, -1), out=sidx)
@@ -158,7 +187,10 @@ class LayerOffload:
         main = torch.cuda.current_stream(q.device)
         side, ev_split, ev_hbm = self._side(q.device)
         ev_split.record(main)
-        kernels.gather_tiers(self.host, host, mcnt, staged)
+        if compact:
+            kernels.row400_gather_tiers(self.host, host, mcnt, staged)
+        else:
+            kernels.gather_tiers(self.host, host, mcnt, staged)
         side.wait_event(ev_split)
         with torch.cuda.stream(side):
             kernels.attend_partial(q, self.cache[:self.C], hbm, sm_scale, kv_scale, op[0:1], lp[0:1], kcount=hcnt)

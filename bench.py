@@ -11,7 +11,8 @@ GB/s = algorithmic bytes / step time, algorithmic bytes = 131072 rows x 656 B + 
 `roofline` is timed live with HIP events on the stream the kernel is launched on; `cpu_baseline` times the float32
 torch-CPU restatement (oracle/cpu_port.py) of the same step on this host's cores. Unless --no-variant, the line also
 carries `host_tier_variant`: BASELINE config 3 (same shapes, 2M-row pool in pinned host memory, 25% HBM hot set,
-Zipf(1.1) selections) measured in the same run.
+Zipf(1.1) selections) measured in the same run, and `host_tier_compact_variant`: the same with the host pool in the
+reference's compact Row400 rows (decoded on the way in; 400 instead of 656 bytes per row over PCIe).
 
 Other configs print their own JSON line (same keys): 1 = B=1 / 16 heads / K=256 check + timing, 3 = offload split-K,
 4 = indexer logits + top-2048 at L = 32768 and 131072, 5 = chunked prefill (8192 queries) + cache write.
@@ -62,9 +63,9 @@ def _line(metric, value, unit, a, ms, dtype, config, roofline, cpu=None, hib=Tru
     return res
 
 
-def _cache_fill(pool_u8, nrows, seed, dev):
+def _cache_fill(pool_u8, nrows, seed, dev, fmt=0):
     """Rows 0..nrows of pool_u8 (device or pinned host) written from seeded N(0,1) bf16 latents / ropes by the
-    library's cache-write kernel."""
+    library's cache-write kernel (fmt 0 = Row656, 2 = compact Row400 with kv_scale 1)."""
     import torch
     from arcagi2_flashnext_dots3_amd import kernels
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -74,7 +75,7 @@ def _cache_fill(pool_u8, nrows, seed, dev):
         kv = torch.randn(n, 512, generator=g, device=dev).to(torch.bfloat16)
         pe = torch.randn(n, 64, generator=g, device=dev).to(torch.bfloat16)
         slots = torch.arange(r0, r0 + n, dtype=torch.int64, device=dev)
-        kernels.cache_write(kv, pe, slots, pool_u8)
+        kernels.cache_write(kv, pe, slots, pool_u8, fmt=fmt)
     torch.cuda.synchronize()
 
 
@@ -182,14 +183,15 @@ def zipf_selections(nseq, K, R, seed, s=1.1, perm=None, device="cpu"):
     return out
 
 
-def run_config3(a, dev, steps=None):
+def run_config3(a, dev, steps=None, row_fmt="row656"):
     import torch
     from arcagi2_flashnext_dots3_amd import kernels
-    from arcagi2_flashnext_dots3_amd.sparse_offload import LayerOffload, hot_rows_by_frequency
+    from arcagi2_flashnext_dots3_amd.sparse_offload import HOST_ROW, LayerOffload, hot_rows_by_frequency
     steps = steps or a.steps
     C = R3 // 4
-    lo = LayerOffload(R3, dev, cache_rows=C)
-    _cache_fill(lo.host, R3, 1, dev)
+    compact = row_fmt == "e2m2"
+    lo = LayerOffload(R3, dev, cache_rows=C, row_fmt=row_fmt)
+    _cache_fill(lo.host, R3, 1, dev, fmt=2 if compact else 0)
     perm = torch.randperm(R3, generator=torch.Generator().manual_seed(3))
     warm = zipf_selections(64 * B, K, R3, seed=4, perm=perm, device=dev)   # 64 warm-up steps of B sequences
     counts = torch.bincount(warm.reshape(-1), minlength=R3)
@@ -205,7 +207,10 @@ def run_config3(a, dev, steps=None):
     o_t, l_t = lo.attend(q, idx, SM_SCALE, 1.0, H, return_lse=True)
     # single-tier check: the same rows gathered into HBM and attended in one pass
     staged = torch.empty(B * K, ROWB, dtype=torch.uint8, device=dev)
-    kernels.gather(lo.host, idx.reshape(-1).to(torch.int64), staged)
+    if compact:
+        kernels.row400_gather(lo.host, idx.reshape(-1).to(torch.int64), staged)
+    else:
+        kernels.gather(lo.host, idx.reshape(-1).to(torch.int64), staged)
     sidx = torch.arange(B * K, dtype=torch.int32, device=dev).view(B, K)
     o_1, l_1 = kernels.attend(q, staged, sidx, SM_SCALE)
     torch.cuda.synchronize()
@@ -216,15 +221,18 @@ def run_config3(a, dev, steps=None):
     db = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
     h2d_ms = _timed(lambda: db.copy_(hb, non_blocking=True), 5, 2)
     h2d = (1 << 28) / (h2d_ms * 1e-3) / 1e9
-    miss_bytes = (1.0 - hit) * B * K * ROWB
+    miss_bytes = (1.0 - hit) * B * K * HOST_ROW[row_fmt]
     gbs = ALG_BYTES / (ms * 1e-3) / 1e9
     res = {"value": round(gbs, 3), "unit": "GB/s (algorithmic bytes of the config-2 step / step time)",
            "ms_per_step": round(ms, 4), "hit_rate": round(hit, 4), "host_rows_per_step": int(round((1 - hit) * B * K)),
            "pcie_bytes_per_step": int(miss_bytes), "pcie_gbs_achieved": round(miss_bytes / (ms * 1e-3) / 1e9, 2),
            "h2d_copy_gbs": round(h2d, 2), "max_abs_diff_vs_single_tier": {"out": d_o, "lse": d_l},
-           "workload": "BASELINE config 3: B=64, H=128, top-2048 Zipf(1.1) rows of a 2,097,152-row Row656 pool in "
-                       "pinned host memory, HBM hot set = 524,288 most frequent rows over 64 warm-up steps; tier split "
-                       "-> HBM-tier attention + host rows gathered over PCIe -> host-tier attention -> LSE merge"}
+           "host_row_format": row_fmt,
+           "workload": "BASELINE config 3: B=64, H=128, top-2048 Zipf(1.1) rows of a 2,097,152-row "
+                       + ("compact Row400 (e2m2b32)" if compact else "Row656") +
+                       " pool in pinned host memory, HBM hot set = 524,288 most frequent rows over 64 warm-up steps "
+                       "(Row656 in HBM); tier split -> HBM-tier attention + host rows gathered over PCIe"
+                       + (" and decoded" if compact else "") + " -> host-tier attention -> LSE merge"}
     del lo, hb, db, staged
     torch.cuda.empty_cache()
     return res
@@ -410,6 +418,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-variant", action="store_true", help="config 2 only: skip the host-tier (config 3) variant")
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--host-rows", default="row656", choices=["row656", "e2m2"],
+                    help="config 3: host pool row format (Row656, or the reference's compact Row400 e2m2b32 rows)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
                     help="only run 5 plain device-to-device copies of BYTES bytes (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -434,12 +444,13 @@ def main():
     if a.config == 2:
         res = run_config2(a, dev)
         if not a.no_variant:
-            try:
-                res["host_tier_variant"] = run_config3(a, dev, steps=min(a.steps, 20))
-            except Exception as e:   # the primary line must still print
-                res["host_tier_variant"] = {"error": repr(e)[:300]}
+            for key, fmt in (("host_tier_variant", "row656"), ("host_tier_compact_variant", "e2m2")):
+                try:
+                    res[key] = run_config3(a, dev, steps=min(a.steps, 20), row_fmt=fmt)
+                except Exception as e:   # the primary line must still print
+                    res[key] = {"error": repr(e)[:300]}
     elif a.config == 3:
-        r = run_config3(a, dev)
+        r = run_config3(a, dev, row_fmt=a.host_rows)
         res = _line("offload split-K decode step us (host tier + HBM hot rows), B=64 top2048", r["ms_per_step"] * 1e3,
                     "us", a, r["ms_per_step"], "bf16 / f16 MFMA, fp32 accumulate", {"workload": r["workload"]},
                     {"bound": "pcie", "achieved": r["pcie_gbs_achieved"], "peak": r["h2d_copy_gbs"], "unit": "GB/s",

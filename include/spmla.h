@@ -8,7 +8,11 @@
  * of the pointed-to type unless stated otherwise. bf16 tensors are passed as void* (uint16 bit patterns).
  *
  * Row formats: Row656 = [512 B e4m3fn latent | 4 x fp32 scale, one per 128 latent values | 64 x bf16 rope];
- *              Row576 = [512 B e4m3fn latent | 64 B e4m3fn rope], one per-tensor kv_scale.
+ *              Row576 = [512 B e4m3fn latent | 64 B e4m3fn rope], one per-tensor kv_scale;
+ *              Row400 = the reference's compact e2m2b32 host row [256 B magnitude nibbles | 64 B sign bits |
+ *                       16 x int8 block exponent (one per 32 latent values) | 64 B e4m3fn rope], one per-tensor
+ *                       kv_scale; its latent values decode exactly to e4m3fn codes
+ *                       (dotsnote/engine/arcstats_pkg/arcstats/offload_rowfmt.py:1-22).
  */
 #ifndef SPMLA_H
 #define SPMLA_H
@@ -23,7 +27,9 @@ extern "C" {
 
 /* KV-cache write: quantize and pack n tokens into rows at slots[i] (slot < 0 or >= R: skipped).
  * Row of a slot: cache + (slot / block_size) * block_stride + (slot % block_size) * row_bytes (block_stride in bytes).
- * fmt 0 = Row656 (per-128 absmax scales, kv_scale unused), fmt 1 = Row576 (clamp(x / kv_scale, +-448) -> e4m3).
+ * fmt 0 = Row656 (per-128 absmax scales, kv_scale unused), fmt 1 = Row576 (clamp(x / kv_scale, +-448) -> e4m3),
+ * fmt 2 = Row400 (clamp(x / kv_scale, +-448) -> sign + e2m2 with a power-of-two scale per 32 values; rope as Row576;
+ * offload_rowfmt.py:81-129 _quant / _store_kernel, torch statement ref_quant / ref_pack :336-388).
  * kv_c: [n][512] bf16 (row stride kv_st), k_pe: [n][64] bf16 (row stride pe_st).
  * Replaces LayerOffload.store (dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:1131-1155, kernels :252-290)
  * and PortableSparseImpl.do_kv_cache_update (dsa_sm89.py:281-290); Row656 closed form
@@ -121,6 +127,27 @@ int spmla_gather_pcie(const void* src, long long R, int row_bytes, const long lo
  * :1157-1163 for one row). */
 int spmla_gather_tiers(const void* src, long long R, int row_bytes, const int* rows, long long r_st, const int* counts,
                        int T, int K, void* dst, long long dst_stride, void* stream);
+
+/* Row400 gather: dst row i (stride dst_stride bytes) = the GPU row of src Row400 row rows[i] (zero row when outside
+ * [0, R)): dst_fmt 0 = Row656 (the decoded e4m3 codes, scales 1.0, rope widened to bf16: the same values, so the
+ * attention reads it with the Row576 kv_scale), 1 = Row576 (the reference's GPU row, byte for byte). pcie != 0 runs
+ * the fixed 64-workgroup grid of spmla_gather_pcie for a pinned host source. Replaces offload_rowfmt.gather /
+ * _rows_kernel MODE 0 (dotsnote/engine/arcstats_pkg/arcstats/offload_rowfmt.py:163-185, :252-256, decode :131-160). */
+int spmla_row400_gather(const void* src, long long R, const long long* rows, int n, void* dst, long long dst_stride,
+                        int dst_fmt, int pcie, void* stream);
+
+/* Row400 copy with decode: dst row dst_rows[i] (rows of dst_fmt's size) = the GPU row of src row src_rows[i]; pairs
+ * with a side outside its range ([0, R_src), [0, R_dst)) are skipped. Fills GPU-format cache lines from compact host
+ * rows. Replaces offload_rowfmt.refill / write_through (_rows_kernel MODE 1 and _wt_kernel, offload_rowfmt.py:187-249,
+ * :258-267). */
+int spmla_row400_copy(const void* src, long long R_src, const long long* src_rows, void* dst, long long R_dst,
+                      const long long* dst_rows, int n, int dst_fmt, void* stream);
+
+/* spmla_gather_tiers for Row400 host rows: the host-tier staging of a decode step with each row decoded to dst_fmt
+ * (0 = Row656, 1 = Row576) on the way. Replaces the compact-row miss copy (offload_rowfmt.copy / _copy_kernel,
+ * offload_rowfmt.py:187-221, :252-253). */
+int spmla_row400_gather_tiers(const void* src, long long R, const int* rows, long long r_st, const int* counts, int T,
+                              int K, void* dst, long long dst_stride, int dst_fmt, void* stream);
 
 /* Row copy: dst row dst_rows[i] = src row src_rows[i] (pairs with an out-of-range side skipped); fills the HBM hot-row
  * cache from the host pool. Replaces the row-cache fill copies (offload_fill.py:311-333, csrc/offload_attn.cu:522-584). */

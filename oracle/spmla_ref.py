@@ -11,19 +11,30 @@ tests/test_oracle.py.
 import numpy as np
 
 D_LAT, D_ROPE, D_QK = 512, 64, 576
-ROW656, ROW576, KEYROW = 656, 576, 132
+ROW656, ROW576, ROW400, KEYROW = 656, 576, 400, 132
 SC_OFF, ROPE_OFF = 512, 528
+R4_SIGN, R4_K, R4_ROPE = 256, 320, 336
 LOG2E = 1.4426950408889634
 LN2 = 0.6931471805599453
 
 PINS = {
     "e4m3_encode": "torch.Tensor.to(float8_e4m3fn) over every fp32 with |x| in [2^-12, 512) and signed specials",
     "e4m3_decode": "torch float8_e4m3fn -> float32 on all 256 codes",
+    "e4m3_to_bf16_bits": "torch float8_e4m3fn -> bfloat16 on all 256 codes",
     "bf16": "torch bfloat16 conversions",
     "cache_write_656": "dequantized row within half an e4m3 ulp of x / s; per-group max code == 448 (0x7e); "
                        "zero groups; rope bit copy; slot skipping",
     "cache_write_576": "e4m3 of the clamped value (library encoder) ; rope codes",
     "index_key_write": "same closed-form checks as cache_write_656 with s = max(amax, 1e-4) / 448; UE8M0 power of 2",
+    "row400_quant": "float64 brute force: k = smallest integer with fp32(amax / 7) <= 2^k (IEEE division from numpy), "
+                    "magnitude = nearest point of the 16-value e2m2 grid x 2^k with ties to the larger (and the one "
+                    "fp32 rounding of z + 0.5 the reference's arithmetic makes, shown by hand examples)",
+    "row400_pack": "the byte layout written out element by element (nibble / bit / exponent / rope positions); "
+                   "unpack(pack(x)) == x",
+    "row400_to_e4m3": "the dequantized value has at most 3 mantissa bits: e4m3 decode of the code equals it exactly "
+                      "in e4m3's normal range; round trip |dequant(quant(x)) - x| <= half a grid step",
+    "cache_write_400": "row400_quant + row400_pack of the scaled, clamped input; rope as cache_write_576",
+    "row400_gather": "decode of every row equals the Row576 row a direct Row576 write of the dequantized values gives",
     "attention": "torch.nn.functional.scaled_dot_product_attention (float64) on dequantized rows + torch.logsumexp;"
                  " brute-force python loops on tiny cases; invariance under permutation of the selected rows",
     "lse_merge": "merge of disjoint splits == single-pass attention (exact math), single part == identity",
@@ -84,6 +95,14 @@ def e4m3_encode(x):
 
 
 _E4M3_TABLE = None
+
+
+def e4m3_to_bf16_bits(c):
+    """e4m3fn codes -> bf16 bit patterns (exact: e4m3 values have at most 4 significant bits); the NaN codes 0x7f /
+    0xff -> the canonical bf16 NaN 0x7fc0 (torch's float8_e4m3fn -> bfloat16 conversion)."""
+    c = np.asarray(c, dtype=np.uint8)
+    b = (e4m3_decode(c).view(np.uint32) >> 16).astype(np.uint16)
+    return np.where((c & 0x7F) == 0x7F, np.uint16(0x7FC0), b).astype(np.uint16)
 
 
 def e4m3_decode(c):
@@ -164,6 +183,116 @@ def index_key_write(k_bits, slots, store, P=1, rank=0, ue8m0=False):
         store[r, :128] = codes[i]
         store[r, 128:132] = s[i:i + 1].view(np.uint8)
     return store
+
+
+# ------------------------------------------------------------------------------------------------ Row400 codec
+def row400_quant(x):
+    """x float32 [N, 512] (already scaled by 1 / kv_scale and clamped to +-448) -> (codes int64 [N, 512]: sign << 4 |
+    magnitude index, k int64 [N, 16]: block exponents). The reference's compact-row quantizer with M = 2, BLK = 32
+    (dotsnote/engine/arcstats_pkg/arcstats/offload_rowfmt.py:81-104 _quant, torch statement ref_quant :336-360),
+    in fp32 arithmetic: k is the smallest integer with 2^k >= fp32(amax / 7) (zero / subnormal quotients: -126),
+    y = |x| 2^-k; y < 1: floor(4y + 0.5); else e2 = [y >= 2] + [y >= 4], ((e2 + 1) << 2) + floor(y / 2^(e2-2) + 0.5)
+    - 4; capped at 15; the sign bit only for x < 0 with a nonzero magnitude."""
+    x = np.asarray(x, dtype=np.float32)
+    N = x.shape[0]
+    ax = np.abs(x).reshape(N, 16, 32)
+    r = (ax.max(-1) / np.float32(7.0)).astype(np.float32)
+    rb = r.view(np.uint32).astype(np.int64)
+    e = ((rb >> 23) & 255) - 127
+    k = e + ((rb & 0x7FFFFF) != 0).astype(np.int64)
+    k = np.where(e < -126, -126, np.minimum(k, 127))
+    inv = ((127 - k).astype(np.uint32) << 23).view(np.float32)           # 2^-k
+    y = (ax * inv[..., None]).astype(np.float32).reshape(N, 512)
+    sub = np.floor((y * np.float32(4.0) + np.float32(0.5)).astype(np.float32)).astype(np.int64)
+    e2 = (y >= 2).astype(np.int64) + (y >= 4).astype(np.int64)
+    inv_stp = ((127 + 2 - e2).astype(np.uint32) << 23).view(np.float32)  # 2^(2 - e2)
+    mant = np.floor((y * inv_stp + np.float32(0.5)).astype(np.float32)).astype(np.int64)
+    nrm = ((e2 + 1) << 2) + mant - 4
+    mag = np.minimum(np.where(y < 1, sub, nrm), 15)
+    code = np.where((x < 0) & (mag > 0), mag | 16, mag)
+    return code.astype(np.int64), k.astype(np.int64)
+
+
+def row400_pack(code, k, rope_codes):
+    """codes [N, 512], k [N, 16], rope e4m3 codes [N, 64] -> Row400 bytes [N, 400] (offload_rowfmt.py:118-128 and
+    ref_pack :366-388 with M = 2): byte e/2 holds the magnitude nibble of value e (low nibble for even e), byte
+    256 + e/8 bit e%8 its sign, bytes 320 + b the int8 exponents, 336.. the rope codes."""
+    code = np.asarray(code, dtype=np.int64)
+    N = code.shape[0]
+    out = np.zeros((N, ROW400), dtype=np.uint8)
+    lo = (code & 15).reshape(N, 256, 2)
+    out[:, :256] = (lo[..., 0] | (lo[..., 1] << 4)).astype(np.uint8)
+    sg = ((code >> 4) & 1).reshape(N, 64, 8)
+    out[:, R4_SIGN:R4_K] = sum(sg[..., j] << j for j in range(8)).astype(np.uint8)
+    out[:, R4_K:R4_ROPE] = np.asarray(k, dtype=np.int64).astype(np.int8).view(np.uint8)
+    out[:, R4_ROPE:] = np.asarray(rope_codes, dtype=np.uint8)
+    return out
+
+
+def row400_unpack(rows):
+    """Row400 bytes [N, 400] -> (codes [N, 512], k [N, 16], rope codes [N, 64])."""
+    rows = np.asarray(rows, dtype=np.uint8)
+    N = rows.shape[0]
+    b = rows[:, :256].astype(np.int64)
+    lo = np.stack([b & 15, b >> 4], -1).reshape(N, 512)
+    sb = rows[:, R4_SIGN:R4_K].astype(np.int64)
+    sg = np.stack([(sb >> j) & 1 for j in range(8)], -1).reshape(N, 512)
+    k = rows[:, R4_K:R4_ROPE].copy().view(np.int8).astype(np.int64)
+    return lo | (sg << 4), k, rows[:, R4_ROPE:].copy()
+
+
+def row400_dequant(code, k):
+    """codes / block exponents -> float32 values before the e4m3 cast (offload_rowfmt.py:149-157, ref_dequant
+    :363-372): mant = (e2 ? 4 + m : m), value = mant * 2^clamp(max(e2, 1) - 3 + k, -126, 127), signed, clamped to
+    +-448 (fp32: an exponent of 127 with mant >= 2 overflows to inf and clamps to 448)."""
+    code = np.asarray(code, dtype=np.int64)
+    mag = code & 15
+    e2, mm = mag >> 2, mag & 3
+    mant = np.where(e2 > 0, mm + 4, mm)
+    ex = np.clip(np.maximum(e2, 1) - 3 + np.repeat(np.asarray(k, dtype=np.int64), 32, axis=1), -126, 127)
+    with np.errstate(over="ignore"):
+        v = np.ldexp(mant.astype(np.float32), ex.astype(np.int32)).astype(np.float32)
+    v = np.where(((code >> 4) & 1) != 0, -v, v)
+    return np.clip(v, -448, 448).astype(np.float32)
+
+
+def row400_to_e4m3(code, k):
+    """The GPU (Row576) latent codes of compact values: e4m3 RNE of row400_dequant (offload_rowfmt.py:158)."""
+    return e4m3_encode(row400_dequant(code, k))
+
+
+def cache_write_400(kv_bits, pe_bits, slots, cache, kv_scale=1.0):
+    """Row400 quantize-and-pack (offload_rowfmt.py:107-129 _store_kernel): x = clamp(v * inv_scale, +-448) (fp32,
+    inv_scale = 1 / kv_scale in fp32), latent by row400_quant, rope e4m3_rne of the same clamp as Row576."""
+    R = cache.shape[0]
+    inv = np.float32(1.0) / np.float32(kv_scale)
+    x = np.clip((bf16_bits_to_f32(kv_bits) * inv).astype(np.float32), -448, 448).astype(np.float32)
+    y = np.clip((bf16_bits_to_f32(pe_bits).reshape(x.shape[0], -1) * inv).astype(np.float32), -448, 448)
+    code, k = row400_quant(x)
+    rows = row400_pack(code, k, e4m3_encode(y.astype(np.float32)))
+    for i, slot in enumerate(np.asarray(slots).tolist()[: x.shape[0]]):
+        if 0 <= slot < R:
+            cache[slot] = rows[i]
+    return cache
+
+
+def row400_gather(src, rows, fmt=576):
+    """GPU rows of compact rows src[rows[i]] (zero row outside [0, R)): fmt 576 = the reference's Row576 GPU row
+    (offload_rowfmt.py:163-185 _put_rows / _rows_kernel MODE 0), fmt 656 = the same values as Row656 (e4m3 codes,
+    scales 1.0, rope widened to bf16)."""
+    src = np.asarray(src, dtype=np.uint8)
+    rows = np.asarray(rows, dtype=np.int64)
+    ok = (rows >= 0) & (rows < src.shape[0])
+    code, k, rope = row400_unpack(src[np.where(ok, rows, 0)])
+    lat = row400_to_e4m3(code, k)
+    if fmt == 576:
+        out = np.concatenate([lat, rope], 1).astype(np.uint8)
+    else:
+        sc = np.ones((rows.shape[0], 4), dtype=np.float32).view(np.uint8)
+        rb = e4m3_to_bf16_bits(rope).view(np.uint8)
+        out = np.concatenate([lat, sc, rb], 1).astype(np.uint8)
+    out[~ok] = 0
+    return out
 
 
 # ------------------------------------------------------------------------------------------------ dequant
