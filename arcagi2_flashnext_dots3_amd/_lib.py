@@ -36,6 +36,7 @@ SIGNATURES = {
     "spmla_tier_split": [P, LL, I, I, P, LL, P, LL, P, P, LL, P, P],
     "spmla_compact_stage": [P, I, P, LL, I, I, P, P, P, P, LL, P],
     "spmla_attn_splitk": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, I, P, LL, LL, P, LL, P, P, P],
+    "spmla_attn_merge": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, P, LL, LL, P, LL, P, LL, LL, P, LL, P],
     "spmla_lse_merge": [P, I, LL, LL, LL, P, LL, LL, I, I, I, P, LL, LL, P, P, LL, P],
     "spmla_version": [],
     "spmla_host_e4m3_encode": [P, P, LL],

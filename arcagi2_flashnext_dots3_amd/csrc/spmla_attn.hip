@@ -129,6 +129,9 @@ struct Params {
   uint16_t* out; long long o_st, o_sh;            // bf16 out[t][h][512] (when opart is null)
   float* lse; long long lse_st;                   // lse[t][h]
   float* opart; float* lsepart;                   // fp32 partials: opart[s][t][h][512], lsepart[s][t][h]
+  // optional prior partial merged into the bf16 output (S == 1): normalized fp32 o and natural-log lse
+  const float* prior_o; long long po_st, po_sh;
+  const float* prior_lse; long long pl_st;
 };
 
 // Copy one tile (32 rows: codes + scales) into the wave's buffer and load the rows' rope into VGPRs.
@@ -439,10 +442,24 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     fv[v] = mv > -__builtin_inff() ? __builtin_amdgcn_exp2f(mv - M) : 0.f;
     L += s_ml[v * 64 + 32 + l32] * fv[v];
   }
-  const float inv = L > 0.f ? p.kv_scale / L : 0.f;
+  float inv = L > 0.f ? p.kv_scale / L : 0.f;
+  float lse_v = L > 0.f ? (M + log2f(L)) * 0.69314718055994531f : -__builtin_inff();
+  // merge with a prior partial of the same (token, head): weights exp(lse_i - max) / sum, the lse of the union
+  float wp = 0.f;
+  if (p.prior_o) {
+    const int hh = hg * HG + (lane & 31);
+    const float lp = hh < p.H ? p.prior_lse[(long long)t * p.pl_st + hh] : -__builtin_inff();
+    const float mf = fmaxf(lse_v, lp);
+    if (mf > -__builtin_inff()) {
+      const float a = expf(lse_v - mf), b = expf(lp - mf);     // exp(-inf) = 0
+      const float z = a + b;
+      inv *= a / z;
+      wp = b / z;
+      lse_v = mf + logf(z);
+    }
+  }
 #pragma unroll
   for (int v = 0; v < NW; ++v) fv[v] *= inv;
-  const float lse_v = L > 0.f ? (M + log2f(L)) * 0.69314718055994531f : -__builtin_inff();
 
   SPMLA_LDS f32x4* xo = (SPMLA_LDS f32x4*)(lds + L_TILES);   // [wave][tile 0..7][qd][lane]
   // output head of this lane, recomputed from the lane id (cheaper than keeping it live across the loop)
@@ -474,6 +491,11 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
         }
         if (hoval) {
           const int col = 32 * mt + 8 * qd + 4 * half;      // C-layout rows of values 4qd .. 4qd + 3
+          if (p.prior_o) {
+            const f32x4 x = *(const f32x4*)(p.prior_o + (long long)t * p.po_st + (long long)ho * p.po_sh + col);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(x[e], wp, acc[e]);
+          }
           if (p.opart == nullptr) {
             uint16_t* orow = p.out + (long long)t * p.o_st + (long long)ho * p.o_sh;
             *(uint2*)(orow + col) = make_uint2(pk_bf16(acc[0], acc[1]), pk_bf16(acc[2], acc[3]));
@@ -560,11 +582,11 @@ using namespace spmla;
 
 extern "C" {
 
-// See include/spmla.h for the contract.
-int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void* pool, long long R,
-                      const int* idx, long long idx_st, int K, const int* kcount, int T, int H, float sm_scale,
-                      float kv_scale, int S, void* out, long long o_st, long long o_sh, float* lse,
-                      long long lse_st, float* opart, float* lsepart, void* stream) {
+static int attn_launch(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
+                       long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale, int S,
+                       void* out, long long o_st, long long o_sh, float* lse, long long lse_st, float* opart,
+                       float* lsepart, const float* prior_o, long long po_st, long long po_sh, const float* prior_lse,
+                       long long pl_st, void* stream) {
   if (T < 0 || H <= 0 || K < 0 || S <= 0 || R < 0) return SPMLA_EARG;
   if (T == 0) return SPMLA_OK;
   if (!q || !idx || (R > 0 && !pool)) return SPMLA_EARG;
@@ -582,6 +604,7 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
   p.kv_scale = kv_scale;
   p.out = (uint16_t*)out; p.o_st = o_st; p.o_sh = o_sh; p.lse = lse; p.lse_st = lse_st;
   p.opart = f32part ? opart : nullptr; p.lsepart = lsepart;
+  p.prior_o = prior_o; p.po_st = po_st; p.po_sh = po_sh; p.prior_lse = prior_lse; p.pl_st = pl_st;
   const long long nwork = (long long)T * S * p.HGN;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);
@@ -594,6 +617,25 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
   }
   hipLaunchKernelGGL(attn::attn_kernel, dim3(grid), dim3(256), attn::L_TOTAL, (hipStream_t)stream, p);
   return (int)hipGetLastError();
+}
+
+// See include/spmla.h for the contracts.
+int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void* pool, long long R,
+                      const int* idx, long long idx_st, int K, const int* kcount, int T, int H, float sm_scale,
+                      float kv_scale, int S, void* out, long long o_st, long long o_sh, float* lse,
+                      long long lse_st, float* opart, float* lsepart, void* stream) {
+  return attn_launch(q, q_st, q_sh, pool, R, idx, idx_st, K, kcount, T, H, sm_scale, kv_scale, S, out, o_st, o_sh, lse,
+                     lse_st, opart, lsepart, nullptr, 0, 0, nullptr, 0, stream);
+}
+
+int spmla_attn_merge(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
+                     long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale,
+                     const float* prior_o, long long po_st, long long po_sh, const float* prior_lse, long long pl_st,
+                     void* out, long long o_st, long long o_sh, float* lse, long long lse_st, void* stream) {
+  if (T > 0 && (!prior_o || !prior_lse)) return SPMLA_EARG;
+  if (((uintptr_t)prior_o & 15) || (po_st & 3) || (po_sh & 3)) return SPMLA_EALIGN;
+  return attn_launch(q, q_st, q_sh, pool, R, idx, idx_st, K, kcount, T, H, sm_scale, kv_scale, 1, out, o_st, o_sh, lse,
+                     lse_st, nullptr, nullptr, prior_o, po_st, po_sh, prior_lse, pl_st, stream);
 }
 
 int spmla_lse_merge(const void* parts, int parts_bf16, long long o_ps, long long o_st, long long o_sh,

@@ -239,37 +239,60 @@ __global__ void copy_kernel(const uint8_t* src, long long R_src, const long long
 
 // Per token (one 256-thread block): entries of idx[t] in order; a valid host row h with rowmap[h] >= 0 goes to
 // the HBM tier as line rowmap[h], other valid rows to the host tier as h. Both lists are compacted stably and padded
-// with -1 to K; counts[t] = number of entries of each list.
-__global__ void __launch_bounds__(256) tier_split_kernel(const int* idx, long long idx_st, int K, const int* rowmap,
-                                                         long long R, int* hbm, long long hbm_st, int* hcnt,
-                                                         int* host, long long host_st, int* scnt) {
-  __shared__ uint32_t wsum[2][5];
+// with -1 to K; counts[t] = number of entries of each list. Thread tid takes 8 consecutive entries of each
+// 2048-entry chunk, so all of its index and rowmap reads are in flight together (one dependent pair of memory round
+// trips per chunk), and one block scan of the packed per-thread counts places them.
+__global__ void __launch_bounds__(256) tier_split_kernel(const int* __restrict__ idx, long long idx_st, int K,
+                                                         const int* __restrict__ rowmap, long long R,
+                                                         int* __restrict__ hbm, long long hbm_st, int* __restrict__ hcnt,
+                                                         int* __restrict__ host, long long host_st,
+                                                         int* __restrict__ scnt) {
+  __shared__ uint32_t wsum[4];
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int* ir = idx + (long long)t * idx_st;
   int* hr = hbm + (long long)t * hbm_st;
   int* sr = host + (long long)t * host_st;
   uint32_t nh = 0, ns = 0;
-  for (int k0 = 0; k0 < K; k0 += 256) {
-    const int k = k0 + tid;
-    int h = k < K ? ir[k] : -1;
-    const bool valid = h >= 0 && (long long)h < R;
-    const int line = valid ? rowmap[h] : -1;
-    const bool isH = valid && line >= 0, isS = valid && line < 0;
-    const unsigned long long bh = __ballot(isH), bs = __ballot(isS);
-    const unsigned long long lm = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    const uint32_t ph = __popcll(bh & lm), ps = __popcll(bs & lm);
-    if (lane == 0) { wsum[0][wv] = __popcll(bh); wsum[1][wv] = __popcll(bs); }
+  for (int k0 = 0; k0 < K; k0 += 2048) {
+    int h[8], line[8];
+    bool ok[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + 8 * tid + u;
+      h[u] = k < K ? ir[k] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      ok[u] = h[u] >= 0 && (long long)h[u] < R;
+      line[u] = ok[u] ? rowmap[h[u]] : -1;
+    }
+    uint32_t c = 0;                                  // hbm count | host count << 16
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c += ok[u] ? (line[u] >= 0 ? 1u : 0x10000u) : 0u;
+    uint32_t inc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += y;
+    }
+    if (lane == 63) wsum[wv] = inc;
     __syncthreads();
-    uint32_t oh = 0, os = 0, th = 0, ts = 0;
+    uint32_t base = 0, tot = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      if (w < wv) { oh += wsum[0][w]; os += wsum[1][w]; }
-      th += wsum[0][w]; ts += wsum[1][w];
+      base += w < wv ? wsum[w] : 0u;
+      tot += wsum[w];
     }
-    if (isH) hr[nh + oh + ph] = line;
-    if (isS) sr[ns + os + ps] = h;
-    nh += th; ns += ts;
-    __syncthreads();
+    const uint32_t ex = base + inc - c;
+    uint32_t oh = nh + (ex & 0xffffu), os = ns + (ex >> 16);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (ok[u] && line[u] >= 0) hr[oh++] = line[u];
+      else if (ok[u]) sr[os++] = h[u];
+    }
+    nh += tot & 0xffffu;
+    ns += tot >> 16;
+    __syncthreads();                                 // wsum is rewritten for the next chunk
   }
   for (int k = nh + tid; k < K; k += 256) hr[k] = -1;
   for (int k = ns + tid; k < K; k += 256) sr[k] = -1;

@@ -307,6 +307,28 @@ def attend_partial(q, pool, idx, sm_scale, kv_scale=1.0, opart=None, lpart=None,
     return opart, lpart
 
 
+def attend_merge(q, pool, idx, sm_scale, kv_scale, prior_o, prior_lse, out=None, lse=None, kcount=None, R=None):
+    """attend, merged with a prior normalized partial (prior_o [T, H, 512] fp32, prior_lse [T, H]) of the same tokens
+    and heads in the kernel's epilogue: the two-tier decode step's second tier without a separate lse_merge."""
+    T, H, _ = q.shape
+    K = idx.shape[1]
+    _need(attention_ok(q, idx), "attend_merge: q must be bf16 [T, H, 576] with 16-byte aligned rows, idx int32")
+    _need(prior_o.dtype == torch.float32 and prior_o.shape == (T, H, D_LAT) and prior_o.stride(2) == 1,
+          "prior_o fp32 [T, H, 512]")
+    _need(prior_lse.dtype == torch.float32 and prior_lse.shape == (T, H) and prior_lse.stride(1) == 1, "prior_lse")
+    if out is None:
+        out = torch.empty(T, H, D_LAT, dtype=torch.bfloat16, device=q.device)
+    if lse is None:
+        lse = torch.empty(T, H, dtype=torch.float32, device=q.device)
+    Rv = int(R if R is not None else pool.shape[0])
+    pptr = pool.data_ptr() if torch.is_tensor(pool) else int(pool)
+    _lib.call("spmla_attn_merge", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(), idx.stride(0), K,
+              _ptr(kcount), T, H, float(sm_scale), float(kv_scale), prior_o.data_ptr(), prior_o.stride(0),
+              prior_o.stride(1), prior_lse.data_ptr(), prior_lse.stride(0), out.data_ptr(), out.stride(0),
+              out.stride(1), lse.data_ptr(), lse.stride(0), _stream(q))
+    return out, lse
+
+
 def lse_merge(parts, lses, out=None, out_f32=None, lse=None):
     """parts [n, T, H, 512] fp32 or bf16 (any strides with contiguous rows), lses [n, T, H] -> merged (out, lse)."""
     n, T, H, _ = parts.shape

@@ -12,9 +12,10 @@ Tiers
               reference's dynamic W-way cache (offload_fill.py) is not part of this build.
 
 Decode (attend): the selected host rows of each token are split by tier (spmla_tier_split: cache hits -> lines,
-misses -> host rows, both compacted in order); the HBM tier is attended in place; the host tier's rows are first
-copied over PCIe into an HBM staging area (spmla_gather, the reference's miss fill) and attended there; the two fp32
-partials (o, lse) are merged exactly by spmla_lse_merge. Without a cache (C = 0) every row takes the host tier.
+misses -> host rows, both compacted in order); the HBM tier is attended in place into an fp32 partial (o, lse); the
+host tier's rows are first copied over PCIe into an HBM staging area (spmla_gather_tiers, the reference's miss fill)
+and attended there by spmla_attn_merge, which merges the HBM tier's partial exactly in its epilogue (the
+reference's tier combine). Without a cache (C = 0) every row takes the host tier.
 """
 import torch
 
@@ -180,10 +181,10 @@ class LayerOffload:
         # the host list of token t is compacted (its mcnt[t] valid rows first): staged rows t * K + k, k < mcnt[t];
         # the attention's per-token count masks the rest, so the index map is the fixed identity
         sidx = self._identity(T, K, q.device)
-        op = self._buf("opart", (2, T, H, kernels.D_LAT), torch.float32)
-        lp = self._buf("lpart", (2, T, H), torch.float32)
+        op = self._buf("opart", (1, T, H, kernels.D_LAT), torch.float32)
+        lp = self._buf("lpart", (1, T, H), torch.float32)
         # the PCIe copy (64 workgroups) runs beside the HBM-tier attention, which is queued on a second stream of
-        # default priority; the main stream waits for it before the merge
+        # default priority; the host-tier attention waits for it and merges its partial in its own epilogue
         main = torch.cuda.current_stream(q.device)
         side, ev_split, ev_hbm = self._side(q.device)
         ev_split.record(main)
@@ -195,9 +196,8 @@ class LayerOffload:
         with torch.cuda.stream(side):
             kernels.attend_partial(q, self.cache[:self.C], hbm, sm_scale, kv_scale, op[0:1], lp[0:1], kcount=hcnt)
             ev_hbm.record(side)
-        kernels.attend_partial(q, staged, sidx, sm_scale, kv_scale, op[1:2], lp[1:2], kcount=mcnt)
         main.wait_event(ev_hbm)
-        kernels.lse_merge(op, lp, out=out, lse=lse)
+        kernels.attend_merge(q, staged, sidx, sm_scale, kv_scale, op[0], lp[0], out=out, lse=lse, kcount=mcnt)
         return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
 
     def hit_rate(self, idx):

@@ -184,6 +184,17 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
                       float kv_scale, int S, void* out, long long o_st, long long o_sh, float* lse,
                       long long lse_st, float* opart, float* lsepart, void* stream);
 
+/* spmla_attn_splitk (S = 1) whose result is merged with a prior partial of the same tokens and heads before the bf16
+ * write: prior_o [T][H][512] fp32 normalized (strides po_st, po_sh; 16-byte aligned), prior_lse [T][H] (stride
+ * pl_st, natural log). out = w o + w' prior_o with w = e^lse / (e^lse + e^lse'), w' = e^lse' / (e^lse + e^lse'),
+ * lse_out = ln(e^lse + e^lse'); both -inf -> o = 0, lse = -inf. The host-tier attention of a decode step merges the
+ * HBM tier's partial this way, in place of spmla_lse_merge over two partials (the reference's tier combine,
+ * dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:519-538, fused into the second tier's kernel). */
+int spmla_attn_merge(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
+                     long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale,
+                     const float* prior_o, long long po_st, long long po_sh, const float* prior_lse, long long pl_st,
+                     void* out, long long o_st, long long o_sh, float* lse, long long lse_st, void* stream);
+
 /* LSE merge of n partial results (splits or tiers): part i of (t, h) at parts + i*o_ps + t*o_st + h*o_sh (512 values,
  * fp32 or bf16), lse[i*l_ps + t*l_st + h]. o = sum_i exp(lse_i - L) o_i, L = ln sum_i exp(lse_i); all parts -inf ->
  * o = 0, L = -inf. out bf16 and/or out_f32 (same strides), lse_out optional.

@@ -47,6 +47,8 @@ def test_version():
     (("spmla_cache_write", None, 0, None, 0, None, 1, None, 10, 64, 0, 7, 1.0, None), -2),
     (("spmla_cache_write", None, 0, None, 0, None, 1, None, 10, 64, 0, 3, 1.0, None), -2),
     (("spmla_row400_gather", None, 0, None, 1, None, 656, 2, 0, None), -2),
+    (("spmla_attn_merge", None, 0, 0, None, 0, None, 0, 0, None, 1, 1, 1.0, 1.0, None, 0, 0, None, 0, None, 0, 0,
+      None, 0, None), -2),
     (("spmla_row400_gather", None, 0, None, -1, None, 656, 0, 0, None), -2),
     (("spmla_row400_copy", None, 0, None, None, 0, None, 1, 5, None), -2),
     (("spmla_row400_gather_tiers", None, 0, None, 4, None, 1, 4, None, 656, 3, None), -2),

@@ -73,3 +73,39 @@ def test_kcount_and_partial_tile(dev):
 
 def test_large_query_scale(dev):
     _check(dev, T=2, H=32, R=4096, K=1024, seed=11, qscale=30.0)
+
+
+def test_attend_merge_two_tiers(dev):
+    """spmla_attn_merge: the second tier's attention merged with the first tier's fp32 partial in the epilogue equals
+    attention over the union of both tiers' rows (fp64 oracle) and the two-partial lse_merge; tokens with an empty
+    tier (and one with both empty) included."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    T, H, R, K = 6, 128, 3000, 512
+    pool, _, _ = make_pool_656(R, seed=9)
+    q = make_q(T, H, seed=8)
+    idx = distinct_idx(T, K, R, seed=7)
+    a = idx.clone()
+    b = idx.clone()
+    a[:, K // 3:] = -1                                     # tier A: the first third of each token's rows
+    b[:, :K // 3] = -1                                     # tier B: the rest
+    a[1] = -1                                              # token 1: tier A empty
+    b[2] = -1                                              # token 2: tier B empty
+    a[3] = -1
+    b[3] = -1                                              # token 3: both empty
+    union = torch.where(a >= 0, a, b)
+    sm = 192 ** -0.5
+    pd = torch.from_numpy(pool).to(dev)
+    qd = q.to(dev)
+    op, lp = kernels.attend_partial(qd, pd, a.to(dev), sm, 0.75)
+    out, lse = kernels.attend_merge(qd, pd, b.to(dev), sm, 0.75, op[0], lp[0])
+    op2, lp2 = kernels.attend_partial(qd, pd, b.to(dev), sm, 0.75)
+    o_m, l_m = kernels.lse_merge(torch.cat([op, op2]), torch.cat([lp, lp2]))
+    torch.cuda.synchronize()
+    o_ref, l_ref = ref.attention(q.float().numpy(), pool, union.numpy(), sm, 0.75)
+    o, l = out.float().cpu().numpy(), lse.cpu().numpy()
+    fin = np.isfinite(l_ref)
+    assert np.array_equal(fin, np.isfinite(l)) and not fin[3].any() and np.all(o[3] == 0)
+    assert (np.abs(o - o_ref) / np.maximum(1.0, np.abs(o_ref))).max() <= OUT_TOL
+    assert np.abs(l[fin] - l_ref[fin]).max() <= LSE_TOL
+    assert np.abs(o - o_m.float().cpu().numpy()).max() <= 2.0 ** -7 * max(1.0, np.abs(o).max())
+    assert np.abs(l[fin] - l_m.cpu().numpy()[fin]).max() <= 1e-5

@@ -77,13 +77,17 @@ def test_gather_tiers(dev, T, K, zero0):
     assert np.array_equal(out.cpu().numpy(), exp)
 
 
-def test_tier_split(dev):
+@pytest.mark.parametrize("K", [2048, 300, 5000])
+def test_tier_split(dev, K):
+    """One and several 2048-entry chunks per token, a K that is not a multiple of 8; rowmap entries with negative
+    values other than -1 count as host rows."""
     from arcagi2_flashnext_dots3_amd import kernels
     g = np.random.default_rng(3)
-    T, K, R = 9, 2048, 50000
+    T, R = 9, 50000
     rowmap = np.full(R, -1, dtype=np.int32)
     hot = g.permutation(R)[: R // 4]
     rowmap[hot] = np.arange(hot.size, dtype=np.int32)
+    rowmap[g.permutation(R)[:100]] = -7
     idx = g.integers(-2, R + 2, (T, K)).astype(np.int32)
     out = kernels.tier_split(torch.from_numpy(idx).to(dev), torch.from_numpy(rowmap).to(dev), R)
     exp = ref.tier_split(idx, rowmap, R)
