@@ -139,8 +139,10 @@ template <class Op>
 __global__ void __launch_bounds__(256) gather_kernel(const uint8_t* __restrict__ src, long long R, int src_bytes,
                                                      const long long* __restrict__ rows, int n,
                                                      uint8_t* __restrict__ dst, long long dst_stride,
-                                                     const long long* __restrict__ dst_rows, long long R_dst, Op op) {
+                                                     const long long* __restrict__ dst_rows, long long R_dst, Op op,
+                                                     const int* __restrict__ n_dev = nullptr) {
   __shared__ __attribute__((aligned(16))) uint8_t wl_all[4 * Op::LDS + 16];
+  if (n_dev) n = min(n, *n_dev);                      // a count produced on the device (the cache's miss list)
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   SPMLA_LDS uint8_t* wl = (SPMLA_LDS uint8_t*)wl_all + wv * Op::LDS;
   const int step = gridDim.x * 4;
@@ -409,6 +411,26 @@ int spmla_gather_tiers(const void* src, long long R, int row_bytes, const int* r
   hipLaunchKernelGGL(gth::gather_tiers_kernel<gth::CopyRow>, dim3(64), dim3(256), 0, (hipStream_t)stream,
                      (const uint8_t*)src, R, row_bytes, rows, r_st, counts, T, K, (uint8_t*)dst, dst_stride,
                      gth::CopyRow{row_bytes >> 4});
+  return (int)hipGetLastError();
+}
+
+// ---- the W-way row cache's fill: every miss m < state[1] with miss_dst[m] >= 0 gets its host row (Row656 bytes, or a
+// Row400 row decoded to Row656) at pool row miss_dst[m]; spmla_wcache_step produced the list
+int spmla_wcache_fill(const void* host, long long R, int host_fmt, const long long* miss_rows, const long long* miss_dst,
+                      const int* state, int n_max, void* pool, long long R_pool, void* stream) {
+  if (R < 0 || n_max < 0 || R_pool < 0 || (host_fmt != 0 && host_fmt != 2)) return SPMLA_EARG;
+  if (n_max == 0) return SPMLA_OK;
+  if (!host || !miss_rows || !miss_dst || !state || !pool) return SPMLA_EARG;
+  if (((uintptr_t)host & 15) || ((uintptr_t)pool & 15)) return SPMLA_EALIGN;
+  const unsigned grid = (unsigned)min(64, (n_max + 3) / 4);
+  if (host_fmt == 0)
+    hipLaunchKernelGGL(gth::gather_kernel<gth::CopyRow>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)host, R, ROW656, miss_rows, n_max, (uint8_t*)pool, (long long)ROW656, miss_dst,
+                       R_pool, gth::CopyRow{ROW656 / 16}, state + 1);
+  else
+    hipLaunchKernelGGL(gth::gather_kernel<gth::DecodeRow400>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)host, R, ROW400, miss_rows, n_max, (uint8_t*)pool, (long long)ROW656, miss_dst,
+                       R_pool, gth::DecodeRow400{0}, state + 1);
   return (int)hipGetLastError();
 }
 

@@ -224,6 +224,83 @@ def copy_rows(src, src_rows, dst, dst_rows, R_src=None):
               dst_rows.data_ptr(), dst.shape[-1], n, _stream(dst))
 
 
+class RowCache:
+    """Device state of a dynamic W-way HBM row cache (spmla_wcache_*): C lines in S = C / W sets plus `cap` spill rows,
+    both in one Row656 pool [C + cap, 656] that the attention reads; tags, round-robin pointers, pins and the
+    epoch-tagged miss table. Everything is zero-initialized once (tags -1); no buffer is cleared between steps."""
+
+    def __init__(self, C, W, cap, device):
+        _need(C > 0 and W > 0 and C % W == 0 and cap >= 0, "RowCache: C a positive multiple of W, cap >= 0")
+        self.C, self.W, self.S, self.cap = int(C), int(W), int(C) // int(W), int(cap)
+        self.device = torch.device(device)
+        i32 = dict(dtype=torch.int32, device=self.device)
+        self.tag = torch.full((self.C,), -1, **i32)
+        self.rr = torch.zeros(self.S, **i32)
+        self.cnt = torch.zeros(self.S, **i32)
+        self.pin = torch.zeros(self.C, **i32)
+        self.state = torch.zeros(4, **i32)              # epoch, misses, spill rows used, hits (of the last step)
+        self.pool = torch.zeros((self.C + self.cap, ROW656), dtype=torch.uint8, device=self.device)
+        self.n = 0
+
+    def _tables(self, n):
+        if n > self.n:
+            log2 = max(10, int(n).bit_length() + 1)       # 2^log2 > 2n: the table stays at most half full
+            dev = self.device
+            self.ht = torch.zeros(1 << log2, dtype=torch.int64, device=dev)
+            self.ht_log2 = log2
+            self.htv = torch.zeros(1 << log2, dtype=torch.int32, device=dev)
+            self.ml = torch.zeros(n, dtype=torch.int64, device=dev)
+            self.mslot = torch.zeros(n, dtype=torch.int32, device=dev)
+            self.mdst = torch.zeros(n, dtype=torch.int64, device=dev)
+            self.n = n
+
+    def lookup(self, rows):
+        """bool per row id (int64 tensor): currently in a cache line (diagnostics; no kernel of its own)."""
+        st = (rows % self.S).long()
+        return (self.tag.view(self.S, self.W)[st] == rows[:, None].to(torch.int32)).any(1) & (rows >= 0)
+
+
+def wcache_step(cache, idx, R, res=None):
+    """One decode step of the row cache for idx [T, K] int32 host rows -> res [T, K] int32: the pool row of each
+    entry (line or C + spill row), -2 for a row left on the host (spill area full), -1 invalid."""
+    T, K = idx.shape
+    _need(idx.dtype == torch.int32 and idx.stride(1) == 1, "idx int32 [T, K]")
+    cache._tables(T * K)
+    if res is None:
+        res = torch.empty(T, K, dtype=torch.int32, device=idx.device)
+    _lib.call("spmla_wcache_step", idx.data_ptr(), idx.stride(0), T, K, int(R), cache.tag.data_ptr(), cache.C,
+              cache.W, cache.rr.data_ptr(), cache.cnt.data_ptr(), cache.pin.data_ptr(), cache.ht.data_ptr(),
+              cache.ht_log2, cache.htv.data_ptr(), cache.ml.data_ptr(), cache.mslot.data_ptr(), cache.mdst.data_ptr(),
+              cache.state.data_ptr(), cache.cap, res.data_ptr(), res.stride(0), _stream(idx))
+    return res
+
+
+def wcache_fill(cache, host, R, host_fmt, n):
+    """The step's row copies from the host pool (Row656 = host_fmt 0, compact Row400 = 2) into cache.pool; n = the
+    step's entry count (bounds the miss list)."""
+    _lib.call("spmla_wcache_fill", host.data_ptr() if torch.is_tensor(host) else int(host), int(R), int(host_fmt),
+              cache.ml.data_ptr(), cache.mdst.data_ptr(), cache.state.data_ptr(), int(n), cache.pool.data_ptr(),
+              cache.pool.shape[0], _stream(cache.pool))
+
+
+def wcache_invalidate(cache, slots, R):
+    _need(slots.dtype == torch.int64, "slots int64")
+    _lib.call("spmla_wcache_invalidate", slots.data_ptr(), slots.shape[0], int(R), cache.tag.data_ptr(), cache.C,
+              cache.W, _stream(slots))
+
+
+def split_res(idx, res, hbm=None, hbm_cnt=None, host=None, host_cnt=None):
+    T, K = idx.shape
+    dev = idx.device
+    hbm = torch.empty(T, K, dtype=torch.int32, device=dev) if hbm is None else hbm
+    host = torch.empty(T, K, dtype=torch.int32, device=dev) if host is None else host
+    hbm_cnt = torch.empty(T, dtype=torch.int32, device=dev) if hbm_cnt is None else hbm_cnt
+    host_cnt = torch.empty(T, dtype=torch.int32, device=dev) if host_cnt is None else host_cnt
+    _lib.call("spmla_split_res", idx.data_ptr(), idx.stride(0), res.data_ptr(), res.stride(0), T, K, hbm.data_ptr(),
+              hbm.stride(0), hbm_cnt.data_ptr(), host.data_ptr(), host.stride(0), host_cnt.data_ptr(), _stream(idx))
+    return hbm, hbm_cnt, host, host_cnt
+
+
 def tier_split(idx, rowmap, R, hbm=None, hbm_cnt=None, host=None, host_cnt=None):
     T, K = idx.shape
     dev = idx.device

@@ -7,9 +7,12 @@ Tiers
               reference's cudaHostRegister'ed buffer (_HostReg, sparse_offload.py:917-980). With row_fmt="e2m2" the
               pool holds the reference's compact Row400 rows instead (offload_rowfmt.py, ARC_OFFLOAD_ROW_FMT=e2m2):
               every host read decodes them into Row656 on the way, so 39% fewer bytes cross PCIe per row.
-  HBM cache   [C, 656] uint8 hot rows with tag[line] = host row and rowmap[row] = line (-1 = host only). The hot set
-              is chosen by the caller (set_hot_rows, e.g. hot_rows_by_frequency over recent selections); the
-              reference's dynamic W-way cache (offload_fill.py) is not part of this build.
+  HBM cache   [C, 656] uint8 hot rows with tag[line] = host row and rowmap[row] = line (-1 = host only). Two modes:
+              cache_mode="static": the hot set is chosen by the caller (set_hot_rows, e.g. hot_rows_by_frequency over
+              recent selections); cache_mode="ways": the reference's dynamic W-way set-associative cache
+              (sparse_offload.py:677-789, :1595-1622): every attend() looks its rows up, gives the distinct misses
+              lines (round-robin over the unpinned ways of the row's set) or spill rows, copies them in over PCIe
+              and attends the whole step from HBM.
 
 Decode (attend): the selected host rows of each token are split by tier (spmla_tier_split: cache hits -> lines,
 misses -> host rows, both compacted in order); the HBM tier is attended in place into an fp32 partial (o, lse); the
@@ -39,22 +42,35 @@ class LayerOffload:
     num_host_rows: R, the number of cache slots (every slot id written by store() is a host row id);
     device: the GPU; key: the layer's cache prefix (identification only); cache_rows: C lines of HBM hot-row cache;
     row_fmt: "row656" (host rows as the GPU reads them) or "e2m2" (the reference's compact Row400 host rows,
-    offload_rowfmt.py:1-22; values = code * kv_scale, so store and attend take the same kv_scale).
+    offload_rowfmt.py:1-22; values = code * kv_scale, so store and attend take the same kv_scale);
+    cache_mode: "static" (set_hot_rows) or "ways" (dynamic W-way cache with `ways` lines per set, C % ways == 0, and
+    `spill_rows` HBM rows for misses that find no free way; a step with more entries than spill rows can leave rows on
+    the host, which then take the host tier).
     """
 
-    def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656"):
+    def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
+                 spill_rows=131072):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
+        if cache_mode not in ("static", "ways"):
+            raise ValueError("cache_mode must be 'static' or 'ways'")
         self.R = int(num_host_rows)
         self.device = torch.device(device)
         self.key = key
         self.row_fmt = row_fmt
         self.host = torch.zeros((self.R, HOST_ROW[row_fmt]), dtype=torch.uint8, pin_memory=True)
         self.C = min(int(cache_rows), self.R)
-        self.cache = torch.zeros((max(self.C, 1), ROW), dtype=torch.uint8, device=self.device)
+        self.cache = torch.zeros((max(self.C, 1) if cache_mode == "static" else 1, ROW), dtype=torch.uint8,
+                                 device=self.device)
         self.tag = torch.full((max(self.C, 1),), -1, dtype=torch.int64, device=self.device)
         self.rowmap = torch.full((max(self.R, 1),), -1, dtype=torch.int32, device=self.device)
         self._ws = {}
+        self.mode = cache_mode
+        self.wc = None
+        if cache_mode == "ways":
+            if self.C <= 0 or self.C % int(ways):
+                raise ValueError("cache_mode='ways' needs cache_rows a positive multiple of ways")
+            self.wc = kernels.RowCache(self.C, int(ways), int(spill_rows), self.device)
 
     # ------------------------------------------------------------------------------------------------ rows in
     def store(self, kv_c_normed, k_pe, slots, kv_scale=1.0):
@@ -72,7 +88,9 @@ class LayerOffload:
         slots = slots[:n].to(torch.int64)
         fmt = 2 if compact else 0
         kernels.cache_write(kv_c_normed[:n], kpe[:n], slots, self.host, fmt=fmt, kv_scale=kv_scale)
-        if self.C:
+        if self.wc is not None:
+            kernels.wcache_invalidate(self.wc, slots, self.R)      # rewritten rows: the next lookup misses
+        elif self.C:
             ok = (slots >= 0) & (slots < self.R)
             lines = torch.where(ok, self.rowmap[slots.clamp(0, self.R - 1)].to(torch.int64), -1)
             if compact:
@@ -98,6 +116,8 @@ class LayerOffload:
 
     def set_hot_rows(self, rows):
         """Make `rows` (distinct host rows, at most C) the HBM-resident set: line i holds rows[i]."""
+        if self.wc is not None:
+            raise ValueError("set_hot_rows: the W-way cache places rows itself (cache_mode='ways')")
         rows = rows.to(device=self.device, dtype=torch.int64).reshape(-1)
         if rows.numel() > self.C:
             raise ValueError(f"set_hot_rows: {rows.numel()} rows > {self.C} cache lines")
@@ -156,6 +176,8 @@ class LayerOffload:
         if T == 0:
             return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
         idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
+        if self.wc is not None:
+            return self._attend_ways(q, idx, sm_scale, kv_scale, out, lse, num_heads, return_lse)
         hbm = self._buf("hbm", (T, K), torch.int32)
         host = self._buf("host", (T, K), torch.int32)
         hcnt = self._buf("hcnt", (T,), torch.int32)
@@ -200,9 +222,42 @@ class LayerOffload:
         kernels.attend_merge(q, staged, sidx, sm_scale, kv_scale, op[0], lp[0], out=out, lse=lse, kcount=mcnt)
         return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
 
+    def _attend_ways(self, q, idx, sm_scale, kv_scale, out, lse, num_heads, return_lse):
+        """W-way cache step: look up / place / resolve, copy the misses in, attend over the pool. Entries left on
+        the host (spill area full) take the host tier, merged in the host-tier attention's epilogue."""
+        T, H, _ = q.shape
+        K = idx.shape[1]
+        wc = self.wc
+        res = self._buf("res", (T, K), torch.int32)
+        kernels.wcache_step(wc, idx, self.R, res)
+        kernels.wcache_fill(wc, self.host, self.R, 2 if self.row_fmt == "e2m2" else 0, T * K)
+        if T * K <= wc.cap:                                  # every miss fits the spill area: one HBM tier
+            kernels.attend(q, wc.pool, res, sm_scale, kv_scale, out=out, lse=lse)
+        else:
+            hbm = self._buf("hbm", (T, K), torch.int32)
+            host = self._buf("host", (T, K), torch.int32)
+            hcnt = self._buf("hcnt", (T,), torch.int32)
+            mcnt = self._buf("mcnt", (T,), torch.int32)
+            kernels.split_res(idx, res, hbm, hcnt, host, mcnt)
+            op = self._buf("opart", (1, T, H, kernels.D_LAT), torch.float32)
+            lp = self._buf("lpart", (1, T, H), torch.float32)
+            kernels.attend_partial(q, wc.pool, hbm, sm_scale, kv_scale, op, lp, kcount=hcnt)
+            staged = self._buf("staged", (T * K, ROW), torch.uint8)
+            if self.row_fmt == "e2m2":
+                kernels.row400_gather_tiers(self.host, host, mcnt, staged)
+            else:
+                kernels.gather_tiers(self.host, host, mcnt, staged)
+            kernels.attend_merge(q, staged, self._identity(T, K, q.device), sm_scale, kv_scale, op[0], lp[0],
+                                 out=out, lse=lse, kcount=mcnt)
+        return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+
     def hit_rate(self, idx):
         """Fraction of the valid selected rows of idx [T, K] that the HBM cache holds."""
         v = (idx >= 0) & (idx < self.R)
+        if self.wc is not None:
+            f = idx.reshape(-1).to(torch.int64)
+            f = f[(f >= 0) & (f < self.R)]
+            return float(self.wc.lookup(f).float().mean()) if f.numel() else 0.0
         if not self.C or not bool(v.any()):
             return 0.0
         hit = self.rowmap[idx.clamp(0, self.R - 1).long()] >= 0

@@ -149,6 +149,42 @@ int spmla_row400_copy(const void* src, long long R_src, const long long* src_row
 int spmla_row400_gather_tiers(const void* src, long long R, const int* rows, long long r_st, const int* counts, int T,
                               int K, void* dst, long long dst_stride, int dst_fmt, void* stream);
 
+/* Dynamic W-way HBM row cache, bookkeeping of one decode step (no row copies). Host row h lives in set h % S
+ * (S = C / W), in any line st * W + w with tag[line] == h (-1 empty). For the selected rows idx [T][K] (invalid =
+ * outside [0, R)): entries whose row is cached pin their line for the step; each distinct missing row takes a ticket
+ * in its set and the ticket-th unpinned way counted round-robin from rr[set] (its tag is set to the row), or, with no
+ * unpinned way left, spill row C + k (k < cap) or the host (-2); rr[set] advances by min(tickets, W). res [T][K]
+ * (stride res_st) = the pool row holding each entry's row (line or C + k), -2 host, -1 invalid. The miss list
+ * (miss_rows, miss_slots, miss_dst: >= T * K entries) and state (int[4]: epoch, misses, spill rows used, hits)
+ * feed spmla_wcache_fill. Caller-owned state, zero-initialized once: tag -1, rr / cnt / pin / state / ht 0; ht
+ * (2^ht_log2 > T * K entries of 8 bytes) and htv (int per entry) are the step's miss table, tagged with the epoch so
+ * that no buffer is cleared between steps. Which ways the misses of a set take, and which misses of an overfull set
+ * spill, follow the order of the device atomics. Replaces the reference's W-way cache step (_sa_prefill and
+ * _sa_scan / _sa_fill / _sa_advance / _sa_resolve kernels, dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:
+ * 677-770, :1595-1622; epoch-tagged miss table offload_fill.py:1-45). */
+int spmla_wcache_step(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
+                      int* cnt, int* pin, unsigned long long* ht, int ht_log2, int* htv, long long* miss_rows,
+                      int* miss_slots, long long* miss_dst, int* state, int cap, int* res, long long res_st,
+                      void* stream);
+
+/* The step's row copies: for each miss m < state[1] with miss_dst[m] >= 0, pool row miss_dst[m] (Row656) = host row
+ * miss_rows[m] (host_fmt 0: Row656 bytes; 2: a compact Row400 row decoded to Row656). n_max bounds the miss count
+ * (T * K of the step). 64 workgroups, rows streamed two per wave (the PCIe gather). Replaces the copy half of the
+ * reference's fill (_sa_fill_kernel sparse_offload.py:722-760; the split fill's gather, offload_fill.py:311-333). */
+int spmla_wcache_fill(const void* host, long long R, int host_fmt, const long long* miss_rows, const long long* miss_dst,
+                      const int* state, int n_max, void* pool, long long R_pool, void* stream);
+
+/* Clear the lines that cache rows slots[i] (a rewritten host row must not be served stale). Replaces
+ * _sa_invalidate_kernel (sparse_offload.py:782-789). */
+int spmla_wcache_invalidate(const long long* slots, int n, long long R, int* tag, int C, int W, void* stream);
+
+/* Tier split by resolution: per token, entries with res >= 0 -> hbm_idx (the pool row), res == -2 -> host_idx (the
+ * entry's host row idx[t][k]); both compacted in order, padded with -1 to K, counts per token. The host tier of a
+ * cache whose spill area overflowed (the reference's attention reads res == -1 entries from the host,
+ * csrc/offload_attn2.cu:1610-1995). */
+int spmla_split_res(const int* idx, long long idx_st, const int* res, long long res_st, int T, int K, int* hbm_idx,
+                    long long hbm_st, int* hbm_cnt, int* host_idx, long long host_st, int* host_cnt, void* stream);
+
 /* Row copy: dst row dst_rows[i] = src row src_rows[i] (pairs with an out-of-range side skipped); fills the HBM hot-row
  * cache from the host pool. Replaces the row-cache fill copies (offload_fill.py:311-333, csrc/offload_attn.cu:522-584). */
 int spmla_copy_rows(const void* src, long long R_src, const long long* src_rows, void* dst, long long R_dst,

@@ -35,6 +35,8 @@ PINS = {
                       "in e4m3's normal range; round trip |dequant(quant(x)) - x| <= half a grid step",
     "cache_write_400": "row400_quant + row400_pack of the scaled, clamped input; rope as cache_write_576",
     "row400_gather": "decode of every row equals the Row576 row a direct Row576 write of the dequantized values gives",
+    "wcache_step": "hand-worked W = 2 examples (hit, pin, round-robin replacement, overflow to spill); a sequential "
+                   "simulation of ticketed placement under random miss orders reproduces every order-independent output",
     "attention": "torch.nn.functional.scaled_dot_product_attention (float64) on dequantized rows + torch.logsumexp;"
                  " brute-force python loops on tiny cases; invariance under permutation of the selected rows",
     "lse_merge": "merge of disjoint splits == single-pass attention (exact math), single part == identity",
@@ -512,3 +514,52 @@ def tier_split(idx, rowmap, R):
         host[t, :len(b)] = b
         hc[t], sc[t] = len(a), len(b)
     return hbm, hc, host, sc
+
+
+# ------------------------------------------------------------------------------------------------ W-way row cache
+def wcache_step(tag, rr, idx, R, W):
+    """One decode step of the W-way set-associative row cache (dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py
+    :677-770, composed by _sa_prefill :1595-1622), for the outputs that do not depend on the order in which the
+    device's atomics serve the misses. tag [C] (-1 empty), rr [S] (S = C / W), idx [T, K] host rows (valid iff in
+    [0, R)). Row h belongs to set h % S. Returns a dict:
+      hits       number of valid entries whose row is in a line of its set before the step;
+      pinned     lines hit (never replaced in this step);
+      misses     distinct valid rows not cached, in ascending order;
+      placed     {set: lines that receive misses} = the first min(m, u) unpinned ways counted from rr[set] (m misses
+                 and u unpinned ways in the set);
+      spills     number of misses that find no way: sum over sets of max(0, m - u);
+      rr_next    rr[set] + min(m, W) mod W;
+      content    {set: sorted tags after the step} for every set with m <= u (the placed lines then hold exactly the
+                 set's misses)."""
+    tag = np.asarray(tag, dtype=np.int64)
+    rr = np.asarray(rr, dtype=np.int64)
+    C = tag.shape[0]
+    S = C // W
+    pinned, miss, hits = set(), set(), 0
+    for h in np.asarray(idx, dtype=np.int64).reshape(-1):
+        if not (0 <= h < R):
+            continue
+        st = int(h % S)
+        ways = [st * W + w for w in range(W) if tag[st * W + w] == h]
+        if ways:
+            hits += 1
+            pinned.add(ways[0])
+        else:
+            miss.add(int(h))
+    by_set = {}
+    for h in sorted(miss):
+        by_set.setdefault(h % S, []).append(h)
+    placed, content, spills = {}, {}, 0
+    rr_next = rr.copy()
+    for st, rows in by_set.items():
+        free = [st * W + (int(rr[st]) + j) % W for j in range(W) if st * W + (int(rr[st]) + j) % W not in pinned]
+        m, u = len(rows), len(free)
+        placed[st] = free[:min(m, u)]
+        spills += max(0, m - u)
+        rr_next[st] = (rr[st] + min(m, W)) % W
+        if m <= u:
+            t = tag.copy()
+            t[placed[st]] = rows
+            content[st] = sorted(t[st * W:(st + 1) * W].tolist())
+    return {"hits": hits, "pinned": pinned, "misses": sorted(miss), "placed": placed, "spills": spills,
+            "rr_next": rr_next, "content": content}
