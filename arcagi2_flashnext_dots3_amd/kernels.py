@@ -226,8 +226,9 @@ def copy_rows(src, src_rows, dst, dst_rows, R_src=None):
 
 class RowCache:
     """Device state of a dynamic W-way HBM row cache (spmla_wcache_*): C lines in S = C / W sets plus `cap` spill rows,
-    both in one Row656 pool [C + cap, 656] that the attention reads; tags, round-robin pointers, pins and the
-    epoch-tagged miss table. Everything is zero-initialized once (tags -1); no buffer is cleared between steps."""
+    both in one Row656 pool [C + cap, 656] that the attention reads; tags, round-robin pointers, pins, and per host row
+    the epoch of its last miss and that miss's pool row. Everything is zero-initialized once (tags -1); no buffer is
+    cleared between steps."""
 
     def __init__(self, C, W, cap, device):
         _need(C > 0 and W > 0 and C % W == 0 and cap >= 0, "RowCache: C a positive multiple of W, cap >= 0")
@@ -241,16 +242,16 @@ class RowCache:
         self.state = torch.zeros(4, **i32)              # epoch, misses, spill rows used, hits (of the last step)
         self.pool = torch.zeros((self.C + self.cap, ROW656), dtype=torch.uint8, device=self.device)
         self.n = 0
+        self.R = 0
 
-    def _tables(self, n):
+    def _tables(self, n, R):
+        dev = self.device
+        if R > self.R:
+            self.claim = torch.zeros(R, dtype=torch.int32, device=dev)
+            self.rdst = torch.zeros(R, dtype=torch.int32, device=dev)
+            self.R = R
         if n > self.n:
-            log2 = max(10, int(n).bit_length() + 1)       # 2^log2 > 2n: the table stays at most half full
-            dev = self.device
-            self.ht = torch.zeros(1 << log2, dtype=torch.int64, device=dev)
-            self.ht_log2 = log2
-            self.htv = torch.zeros(1 << log2, dtype=torch.int32, device=dev)
             self.ml = torch.zeros(n, dtype=torch.int64, device=dev)
-            self.mslot = torch.zeros(n, dtype=torch.int32, device=dev)
             self.mdst = torch.zeros(n, dtype=torch.int64, device=dev)
             self.n = n
 
@@ -265,13 +266,34 @@ def wcache_step(cache, idx, R, res=None):
     entry (line or C + spill row), -2 for a row left on the host (spill area full), -1 invalid."""
     T, K = idx.shape
     _need(idx.dtype == torch.int32 and idx.stride(1) == 1, "idx int32 [T, K]")
-    cache._tables(T * K)
+    cache._tables(T * K, int(R))
     if res is None:
         res = torch.empty(T, K, dtype=torch.int32, device=idx.device)
-    _lib.call("spmla_wcache_step", idx.data_ptr(), idx.stride(0), T, K, int(R), cache.tag.data_ptr(), cache.C,
-              cache.W, cache.rr.data_ptr(), cache.cnt.data_ptr(), cache.pin.data_ptr(), cache.ht.data_ptr(),
-              cache.ht_log2, cache.htv.data_ptr(), cache.ml.data_ptr(), cache.mslot.data_ptr(), cache.mdst.data_ptr(),
-              cache.state.data_ptr(), cache.cap, res.data_ptr(), res.stride(0), _stream(idx))
+    _lib.call("spmla_wcache_step", *_wc_args(cache, idx, R), res.data_ptr(), res.stride(0), _stream(idx))
+    return res
+
+
+def _wc_args(cache, idx, R):
+    T, K = idx.shape
+    return (idx.data_ptr(), idx.stride(0), T, K, int(R), cache.tag.data_ptr(), cache.C, cache.W, cache.rr.data_ptr(),
+            cache.cnt.data_ptr(), cache.pin.data_ptr(), cache.claim.data_ptr(), cache.rdst.data_ptr(),
+            cache.ml.data_ptr(), cache.mdst.data_ptr(), cache.state.data_ptr(), cache.cap)
+
+
+def wcache_place(cache, idx, R):
+    """First half of wcache_step: lookup and placement (the miss list and tags are final; wcache_fill may follow)."""
+    T, K = idx.shape
+    _need(idx.dtype == torch.int32 and idx.stride(1) == 1, "idx int32 [T, K]")
+    cache._tables(T * K, int(R))
+    _lib.call("spmla_wcache_place", *_wc_args(cache, idx, R), _stream(idx))
+
+
+def wcache_resolve(cache, idx, R, res=None):
+    """Second half of wcache_step: res [T, K] and the round-robin advance."""
+    T, K = idx.shape
+    if res is None:
+        res = torch.empty(T, K, dtype=torch.int32, device=idx.device)
+    _lib.call("spmla_wcache_resolve", *_wc_args(cache, idx, R), res.data_ptr(), res.stride(0), _stream(idx))
     return res
 
 
@@ -299,6 +321,21 @@ def split_res(idx, res, hbm=None, hbm_cnt=None, host=None, host_cnt=None):
     _lib.call("spmla_split_res", idx.data_ptr(), idx.stride(0), res.data_ptr(), res.stride(0), T, K, hbm.data_ptr(),
               hbm.stride(0), hbm_cnt.data_ptr(), host.data_ptr(), host.stride(0), host_cnt.data_ptr(), _stream(idx))
     return hbm, hbm_cnt, host, host_cnt
+
+
+def wcache_split(cache, res, hit=None, hit_cnt=None, fresh=None, fresh_cnt=None):
+    """Entries of a cache step's res [T, K] split into this step's hits and the rows its fill brings in (pool rows,
+    compacted per token, -1 padded, counts per token)."""
+    T, K = res.shape
+    dev = res.device
+    hit = torch.empty(T, K, dtype=torch.int32, device=dev) if hit is None else hit
+    fresh = torch.empty(T, K, dtype=torch.int32, device=dev) if fresh is None else fresh
+    hit_cnt = torch.empty(T, dtype=torch.int32, device=dev) if hit_cnt is None else hit_cnt
+    fresh_cnt = torch.empty(T, dtype=torch.int32, device=dev) if fresh_cnt is None else fresh_cnt
+    _lib.call("spmla_wcache_split", res.data_ptr(), res.stride(0), T, K, cache.pin.data_ptr(), cache.C,
+              cache.state.data_ptr(), hit.data_ptr(), hit.stride(0), hit_cnt.data_ptr(), fresh.data_ptr(),
+              fresh.stride(0), fresh_cnt.data_ptr(), _stream(res))
+    return hit, hit_cnt, fresh, fresh_cnt
 
 
 def tier_split(idx, rowmap, R, hbm=None, hbm_cnt=None, host=None, host_cnt=None):

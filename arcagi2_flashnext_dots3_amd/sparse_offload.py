@@ -45,11 +45,13 @@ class LayerOffload:
     offload_rowfmt.py:1-22; values = code * kv_scale, so store and attend take the same kv_scale);
     cache_mode: "static" (set_hot_rows) or "ways" (dynamic W-way cache with `ways` lines per set, C % ways == 0, and
     `spill_rows` HBM rows for misses that find no free way; a step with more entries than spill rows can leave rows on
-    the host, which then take the host tier).
+    the host, which then take the host tier). overlap_fill (ways): attend over the step's hits on a second stream while
+    the misses are copied in, then over the fresh rows with the hits' partial merged in the epilogue; False: one
+    attention over the whole step after the copy (bit-identical to attending the gathered rows).
     """
 
     def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
-                 spill_rows=131072):
+                 spill_rows=131072, overlap_fill=True):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         if cache_mode not in ("static", "ways"):
@@ -66,6 +68,7 @@ class LayerOffload:
         self.rowmap = torch.full((max(self.R, 1),), -1, dtype=torch.int32, device=self.device)
         self._ws = {}
         self.mode = cache_mode
+        self.overlap_fill = bool(overlap_fill)
         self.wc = None
         if cache_mode == "ways":
             if self.C <= 0 or self.C % int(ways):
@@ -229,8 +232,32 @@ class LayerOffload:
         K = idx.shape[1]
         wc = self.wc
         res = self._buf("res", (T, K), torch.int32)
+        fmt = 2 if self.row_fmt == "e2m2" else 0
+        if T * K <= wc.cap and self.overlap_fill:
+            # placement, then the PCIe copy of the misses on the second stream while the resolution, the hit / fresh
+            # split and the attention over the hits run here; the fresh rows' attention merges the hits' partial
+            kernels.wcache_place(wc, idx, self.R)
+            main = torch.cuda.current_stream(q.device)
+            side, ev_place, ev_fill = self._side(q.device)
+            ev_place.record(main)
+            side.wait_event(ev_place)
+            with torch.cuda.stream(side):
+                kernels.wcache_fill(wc, self.host, self.R, fmt, T * K)
+                ev_fill.record(side)
+            kernels.wcache_resolve(wc, idx, self.R, res)
+            hit = self._buf("hbm", (T, K), torch.int32)
+            fresh = self._buf("host", (T, K), torch.int32)
+            hcnt = self._buf("hcnt", (T,), torch.int32)
+            fcnt = self._buf("mcnt", (T,), torch.int32)
+            kernels.wcache_split(wc, res, hit, hcnt, fresh, fcnt)
+            op = self._buf("opart", (1, T, H, kernels.D_LAT), torch.float32)
+            lp = self._buf("lpart", (1, T, H), torch.float32)
+            kernels.attend_partial(q, wc.pool, hit, sm_scale, kv_scale, op, lp, kcount=hcnt)
+            main.wait_event(ev_fill)
+            kernels.attend_merge(q, wc.pool, fresh, sm_scale, kv_scale, op[0], lp[0], out=out, lse=lse, kcount=fcnt)
+            return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
         kernels.wcache_step(wc, idx, self.R, res)
-        kernels.wcache_fill(wc, self.host, self.R, 2 if self.row_fmt == "e2m2" else 0, T * K)
+        kernels.wcache_fill(wc, self.host, self.R, fmt, T * K)
         if T * K <= wc.cap:                                  # every miss fits the spill area: one HBM tier
             kernels.attend(q, wc.pool, res, sm_scale, kv_scale, out=out, lse=lse)
         else:

@@ -12,7 +12,9 @@ GB/s = algorithmic bytes / step time, algorithmic bytes = 131072 rows x 656 B + 
 torch-CPU restatement (oracle/cpu_port.py) of the same step on this host's cores. Unless --no-variant, the line also
 carries `host_tier_variant`: BASELINE config 3 (same shapes, 2M-row pool in pinned host memory, 25% HBM hot set,
 Zipf(1.1) selections) measured in the same run, and `host_tier_compact_variant`: the same with the host pool in the
-reference's compact Row400 rows (decoded on the way in; 400 instead of 656 bytes per row over PCIe).
+reference's compact Row400 rows (decoded on the way in; 400 instead of 656 bytes per row over PCIe), and
+`host_tier_ways_variant`: compact host rows behind the dynamic 16-way row cache instead of the static hot set, on a
+stream of fresh Zipf draws (`--config 3 --cache ways`).
 
 Other configs print their own JSON line (same keys): 1 = B=1 / 16 heads / K=256 check + timing, 3 = offload split-K,
 4 = indexer logits + top-2048 at L = 32768 and 131072, 5 = chunked prefill (8192 queries) + cache write.
@@ -238,6 +240,61 @@ def run_config3(a, dev, steps=None, row_fmt="row656"):
     return res
 
 
+def run_config3_ways(a, dev, steps=None, row_fmt="e2m2", W=16):
+    """Config 3 shapes with the dynamic W-way cache in place of the static hot set: every step draws fresh Zipf(1.1)
+    selections (a decode stream); the cache is warmed over the 64 warm-up steps' draws, then each timed step looks
+    its rows up, places the misses, copies them in over PCIe (beside the attention over the hits) and attends."""
+    import torch
+    from arcagi2_flashnext_dots3_amd.sparse_offload import HOST_ROW, LayerOffload
+    steps = steps or a.steps
+    warm_n = max(2, a.warmup // 4)
+    C = R3 // 4
+    lo = LayerOffload(R3, dev, cache_rows=C, row_fmt=row_fmt, cache_mode="ways", ways=W, spill_rows=B * K)
+    _cache_fill(lo.host, R3, 1, dev, fmt=2 if row_fmt == "e2m2" else 0)
+    perm = torch.randperm(R3, generator=torch.Generator().manual_seed(3))
+    gq = torch.Generator().manual_seed(0)
+    q = torch.randn(B, H, D, generator=gq).to(torch.bfloat16).to(dev)
+    out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    warm = zipf_selections(64 * B, K, R3, seed=4, perm=perm, device=dev).to(torch.int32).view(64, B, K)
+    for s_ in range(64):
+        lo.attend(q, warm[s_], SM_SCALE, 1.0, H, out=out, lse=lse)
+    del warm
+    # stats pass over fresh steps (untimed): hits, misses, spills per step from the cache's counters
+    nstat = 8
+    stat = zipf_selections(nstat * B, K, R3, seed=6, perm=perm, device=dev).to(torch.int32).view(nstat, B, K)
+    hits = misses = spills = 0
+    for s_ in range(nstat):
+        lo.attend(q, stat[s_], SM_SCALE, 1.0, H, out=out, lse=lse)
+        st = lo.wc.state.cpu()
+        hits += int(st[3]); misses += int(st[1]); spills += int(st[2])
+    del stat
+    nsteps = warm_n + steps
+    seq = zipf_selections(nsteps * B, K, R3, seed=5, perm=perm, device=dev).to(torch.int32).view(nsteps, B, K)
+    it = iter(range(nsteps))
+    ms = _timed(lambda: lo.attend(q, seq[next(it)], SM_SCALE, 1.0, H, out=out, lse=lse), steps, warm_n)
+    hb = torch.empty(1 << 28, dtype=torch.uint8, pin_memory=True)      # host-tier roofline: pinned -> HBM copy
+    db = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+    h2d = (1 << 28) / (_timed(lambda: db.copy_(hb, non_blocking=True), 5, 2) * 1e-3) / 1e9
+    del hb, db
+    hit = hits / (nstat * B * K)
+    mb = misses / nstat * HOST_ROW[row_fmt]
+    res = {"value": round(ALG_BYTES / (ms * 1e-3) / 1e9, 3),
+           "unit": "GB/s (algorithmic bytes of the config-2 step / step time)", "ms_per_step": round(ms, 4),
+           "hit_rate": round(hit, 4), "misses_per_step": round(misses / nstat, 1),
+           "spill_rows_per_step": round(spills / nstat, 1), "pcie_bytes_per_step": int(mb),
+           "pcie_gbs_achieved": round(mb / (ms * 1e-3) / 1e9, 2), "h2d_copy_gbs": round(h2d, 2),
+           "host_row_format": row_fmt, "ways": W,
+           "workload": f"config 3 shapes with a dynamic {W}-way set-associative HBM cache of 524,288 lines (+ "
+                       f"131,072 spill rows) over a 2,097,152-row {'compact Row400' if row_fmt == 'e2m2' else 'Row656'}"
+                       " pinned host pool; each step a fresh Zipf(1.1) draw of B=64 x top-2048 rows; warmed over "
+                       "64 steps; per step: lookup / place / resolve, miss copy over PCIe beside the attention over "
+                       "the hits, attention over the fresh rows merged in its epilogue"}
+    del lo, seq
+    torch.cuda.empty_cache()
+    return res
+
+
 # ------------------------------------------------------------------------------------------------ config 4
 def run_config4(a, dev):
     import numpy as np
@@ -420,6 +477,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--host-rows", default="row656", choices=["row656", "e2m2"],
                     help="config 3: host pool row format (Row656, or the reference's compact Row400 e2m2b32 rows)")
+    ap.add_argument("--cache", default="static", choices=["static", "ways"],
+                    help="config 3: static frequency hot set (BASELINE's definition) or the dynamic W-way cache")
+    ap.add_argument("--ways", type=int, default=16, help="config 3 --cache ways: lines per set")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
                     help="only run 5 plain device-to-device copies of BYTES bytes (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -449,8 +509,13 @@ def main():
                     res[key] = run_config3(a, dev, steps=min(a.steps, 20), row_fmt=fmt)
                 except Exception as e:   # the primary line must still print
                     res[key] = {"error": repr(e)[:300]}
+            try:
+                res["host_tier_ways_variant"] = run_config3_ways(a, dev, steps=min(a.steps, 20), row_fmt="e2m2")
+            except Exception as e:
+                res["host_tier_ways_variant"] = {"error": repr(e)[:300]}
     elif a.config == 3:
-        r = run_config3(a, dev, row_fmt=a.host_rows)
+        r = run_config3_ways(a, dev, row_fmt=a.host_rows, W=a.ways) if a.cache == "ways" else \
+            run_config3(a, dev, row_fmt=a.host_rows)
         res = _line("offload split-K decode step us (host tier + HBM hot rows), B=64 top2048", r["ms_per_step"] * 1e3,
                     "us", a, r["ms_per_step"], "bf16 / f16 MFMA, fp32 accumulate", {"workload": r["workload"]},
                     {"bound": "pcie", "achieved": r["pcie_gbs_achieved"], "peak": r["h2d_copy_gbs"], "unit": "GB/s",

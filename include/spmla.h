@@ -155,17 +155,26 @@ int spmla_row400_gather_tiers(const void* src, long long R, const int* rows, lon
  * in its set and the ticket-th unpinned way counted round-robin from rr[set] (its tag is set to the row), or, with no
  * unpinned way left, spill row C + k (k < cap) or the host (-2); rr[set] advances by min(tickets, W). res [T][K]
  * (stride res_st) = the pool row holding each entry's row (line or C + k), -2 host, -1 invalid. The miss list
- * (miss_rows, miss_slots, miss_dst: >= T * K entries) and state (int[4]: epoch, misses, spill rows used, hits)
- * feed spmla_wcache_fill. Caller-owned state, zero-initialized once: tag -1, rr / cnt / pin / state / ht 0; ht
- * (2^ht_log2 > T * K entries of 8 bytes) and htv (int per entry) are the step's miss table, tagged with the epoch so
- * that no buffer is cleared between steps. Which ways the misses of a set take, and which misses of an overfull set
- * spill, follow the order of the device atomics. Replaces the reference's W-way cache step (_sa_prefill and
+ * (miss_rows, miss_dst: >= T * K entries) and state (int[4]: epoch, misses, spill rows used, hits) feed
+ * spmla_wcache_fill. Caller-owned state, zero-initialized once: tag -1, rr / cnt / pin / state / claim 0; claim and
+ * rdst hold one int per host row (the epoch of the row's last miss, the pool row it got), so no buffer is cleared
+ * between steps. Which ways the misses of a set take, and which misses of an overfull set spill, follow the order of
+ * the device atomics. Replaces the reference's W-way cache step (_sa_prefill and
  * _sa_scan / _sa_fill / _sa_advance / _sa_resolve kernels, dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:
  * 677-770, :1595-1622; epoch-tagged miss table offload_fill.py:1-45). */
 int spmla_wcache_step(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
-                      int* cnt, int* pin, unsigned long long* ht, int ht_log2, int* htv, long long* miss_rows,
-                      int* miss_slots, long long* miss_dst, int* state, int cap, int* res, long long res_st,
-                      void* stream);
+                      int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst, int* state,
+                      int cap, int* res, long long res_st, void* stream);
+
+/* spmla_wcache_step in two launches groups, so that the row copies can start before the resolution: _place runs the
+ * step's lookup and placement (the miss list and the tags are final after it; spmla_wcache_fill may follow on
+ * another stream), _resolve writes res and advances the round-robin pointers. Same arguments and results. */
+int spmla_wcache_place(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
+                       int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst, int* state,
+                       int cap, void* stream);
+int spmla_wcache_resolve(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
+                         int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst,
+                         int* state, int cap, int* res, long long res_st, void* stream);
 
 /* The step's row copies: for each miss m < state[1] with miss_dst[m] >= 0, pool row miss_dst[m] (Row656) = host row
  * miss_rows[m] (host_fmt 0: Row656 bytes; 2: a compact Row400 row decoded to Row656). n_max bounds the miss count
@@ -184,6 +193,16 @@ int spmla_wcache_invalidate(const long long* slots, int n, long long R, int* tag
  * csrc/offload_attn2.cu:1610-1995). */
 int spmla_split_res(const int* idx, long long idx_st, const int* res, long long res_st, int T, int K, int* hbm_idx,
                     long long hbm_st, int* hbm_cnt, int* host_idx, long long host_st, int* host_cnt, void* stream);
+
+/* Split of a cache step's resolutions by hit: per token, entries whose line was a hit of the step (pin[line] equals
+ * the step's epoch, state[0]) -> hit_idx, the other entries with res >= 0 (rows the step's fill brings in) ->
+ * fresh_idx; both as pool rows, compacted in order, padded with -1, with counts per token. The attention over the
+ * hits can then run while spmla_wcache_fill copies the misses in, and the attention over the fresh rows merges it
+ * (spmla_attn_merge). Replaces the reference's overlapped fill, where the attention waits on per-row pending marks
+ * (offload_fill.py:33-38, ARC_OFFLOAD_OVERLAP). */
+int spmla_wcache_split(const int* res, long long res_st, int T, int K, const int* pin, int C, const int* state,
+                       int* hit_idx, long long hit_st, int* hit_cnt, int* fresh_idx, long long fresh_st, int* fresh_cnt,
+                       void* stream);
 
 /* Row copy: dst row dst_rows[i] = src row src_rows[i] (pairs with an out-of-range side skipped); fills the HBM hot-row
  * cache from the host pool. Replaces the row-cache fill copies (offload_fill.py:311-333, csrc/offload_attn.cu:522-584). */

@@ -75,9 +75,20 @@ def test_wcache_steps(dev, W, host_fmt):
         tag0, rr0 = wc.tag.cpu().numpy().astype(np.int64), wc.rr.cpu().numpy()
         print(f"[wcache] W={W} fmt={host_fmt} step={step}", flush=True)
         res = kernels.wcache_step(wc, torch.from_numpy(idx).to(dev), R)
+        hit, hc, fresh, fc = kernels.wcache_split(wc, res)
         kernels.wcache_fill(wc, host, R, host_fmt, T * K)
         torch.cuda.synchronize()
         _check_step(wc, host_rows, idx, res, tag0, rr0, R)
+        # hits: entries whose row was in its set before the step, in order; fresh: the other valid entries
+        r = res.cpu().numpy()
+        S = wc.S
+        was = np.array([[0 <= h < R and h in set(tag0[(h % S) * W:(h % S + 1) * W].tolist()) for h in row]
+                        for row in idx])
+        valid = (idx >= 0) & (idx < R)
+        hit, hc, fresh, fc = [x.cpu().numpy() for x in (hit, hc, fresh, fc)]
+        for t in range(T):
+            assert np.array_equal(hit[t, :hc[t]], r[t][was[t]]) and np.all(hit[t, hc[t]:] == -1)
+            assert np.array_equal(fresh[t, :fc[t]], r[t][valid[t] & ~was[t]]) and np.all(fresh[t, fc[t]:] == -1)
     assert int(wc.state[3]) > 0                            # later steps hit the hot range
 
 
@@ -116,19 +127,19 @@ def test_wcache_overflow_and_invalidate(dev):
     assert not np.isin(wc.tag.cpu().numpy(), cached).any()
 
 
-@pytest.mark.parametrize("cap", [4096, 64])
-def test_layer_offload_ways_matches_single_tier(dev, cap):
-    """LayerOffload(cache_mode='ways') over several steps: with a spill area covering the step, the attention over
-    the cache pool equals the single-tier attention over the gathered rows bit for bit (same row bytes, same order);
-    with a small spill area some rows take the host tier and the merged result matches within the tier-merge
-    tolerance."""
+@pytest.mark.parametrize("cap,overlap", [(4096, False), (4096, True), (64, True)])
+def test_layer_offload_ways_matches_single_tier(dev, cap, overlap):
+    """LayerOffload(cache_mode='ways') over several steps: with a spill area covering the step and no overlap, the
+    attention over the cache pool equals the single-tier attention over the gathered rows bit for bit (same row bytes,
+    same order); with the hits attended beside the copy, or a small spill area that leaves rows on the host, the
+    merged result matches within the tier-merge tolerance."""
     from arcagi2_flashnext_dots3_amd import kernels
     from arcagi2_flashnext_dots3_amd.sparse_offload import LayerOffload
     R, T, H, K = 6000, 4, 64, 1024
     g = torch.Generator().manual_seed(5)
     kv = (torch.randn(R, 512, generator=g)).to(torch.bfloat16)
     pe = torch.randn(R, 64, generator=g).to(torch.bfloat16)
-    lo = LayerOffload(R, dev, cache_rows=512, cache_mode="ways", ways=8, spill_rows=cap)
+    lo = LayerOffload(R, dev, cache_rows=512, cache_mode="ways", ways=8, spill_rows=cap, overlap_fill=overlap)
     lo.store(kv.to(dev), pe.to(dev), torch.arange(R, dtype=torch.int64, device=dev))
     q = make_q(T, H, seed=6).to(dev)
     sm = 192 ** -0.5
@@ -141,7 +152,7 @@ def test_layer_offload_ways_matches_single_tier(dev, cap):
                            torch.full_like(idx, -1))
         o1, l1 = kernels.attend(q, staged, sidx, sm)
         torch.cuda.synchronize()
-        if cap >= T * K:
+        if cap >= T * K and not overlap:
             assert torch.equal(out, o1) and torch.equal(lse, l1)
         else:
             assert float((out.float() - o1.float()).abs().max()) <= 1e-2
