@@ -458,3 +458,39 @@ def lse_merge(parts, lses, out=None, out_f32=None, lse=None):
               _ptr(out), ref.stride(0), ref.stride(1), _ptr(out_f32), lse.data_ptr(), lse.stride(0),
               _stream(parts))
     return (out if out is not None else out_f32), lse
+
+
+# ---------------------------------------------------------------------------------------------- MLA absorbed matmuls
+def bmm_fp8(a, codes, scales, scale_k, out):
+    """out[n, b, j] = sum_k a[n, b, k] * bf16(codes[n, j, k] (e4m3) * S), S = scales[n, j, k // 128] (scale_k) else
+    scales[n, k, j // 128]; a bf16 [N, B, K] (any strides), out bf16 or fp32 [N, B, J] (any strides)."""
+    N, B, K = a.shape
+    J = codes.shape[1]
+    _need(a.dtype == torch.bfloat16, "a must be bf16")
+    _need(codes.dtype in (torch.uint8, torch.float8_e4m3fn) and codes.shape[0] == N and codes.shape[2] == K,
+          "codes [N, J, K] e4m3")
+    _need(scales.dtype == torch.float32, "scales fp32")
+    _need(out.dtype in (torch.bfloat16, torch.float32) and tuple(out.shape) == (N, B, J), "out [N, B, J]")
+    _lib.call("spmla_bmm_fp8", a.data_ptr(), a.stride(0), a.stride(1), a.stride(2), codes.data_ptr(), codes.stride(0),
+              codes.stride(1), codes.stride(2), scales.data_ptr(), scales.stride(0), scales.stride(1),
+              scales.stride(2), int(bool(scale_k)), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+              int(out.dtype == torch.float32), N, B, J, K, _stream(a))
+    return out
+
+
+def mla_query(q_nope, q_pe, codes_uk, scales_uk, out=None):
+    """The decode query of the sparse attention in one launch: out[t, h, :512] = q_nope[t, h] @ W_UK_T[h] (FP8
+    weights, codes [H, 512, 128], scales [H, 128, 4]), out[t, h, 512:] = q_pe[t, h]."""
+    T, H, _ = q_nope.shape
+    _need(q_nope.dtype == torch.bfloat16 and q_nope.shape[2] == 128 and q_nope.stride(2) == 1, "q_nope [T, H, 128]")
+    _need(q_pe.dtype == torch.bfloat16 and tuple(q_pe.shape) == (T, H, 64) and q_pe.stride(2) == 1, "q_pe [T, H, 64]")
+    _need(tuple(codes_uk.shape) == (H, 512, 128) and codes_uk.is_contiguous(), "codes_uk [H, 512, 128]")
+    _need(tuple(scales_uk.shape) == (H, 128, 4) and scales_uk.is_contiguous() and scales_uk.dtype == torch.float32,
+          "scales_uk [H, 128, 4] fp32")
+    if out is None:
+        out = torch.empty(T, H, D_QK, dtype=torch.bfloat16, device=q_nope.device)
+    _need(out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H, D_QK) and out.stride(2) == 1, "out [T, H, 576]")
+    _lib.call("spmla_mla_query", q_nope.data_ptr(), q_nope.stride(0), q_nope.stride(1), q_pe.data_ptr(),
+              q_pe.stride(0), q_pe.stride(1), codes_uk.data_ptr(), scales_uk.data_ptr(), T, H, out.data_ptr(),
+              out.stride(0), out.stride(1), _stream(q_nope))
+    return out

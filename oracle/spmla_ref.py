@@ -35,6 +35,8 @@ PINS = {
                       "in e4m3's normal range; round trip |dequant(quant(x)) - x| <= half a grid step",
     "cache_write_400": "row400_quant + row400_pack of the scaled, clamped input; rope as cache_write_576",
     "row400_gather": "decode of every row equals the Row576 row a direct Row576 write of the dequantized values gives",
+    "bmm_fp8": "torch statement of the reference's dequantization ((float8 -> float32) * scale -> bfloat16, all "
+               "library conversions) and torch.matmul in float64; a python triple loop on a tiny case",
     "wcache_step": "hand-worked W = 2 examples (hit, pin, round-robin replacement, overflow to spill); a sequential "
                    "simulation of ticketed placement under random miss orders reproduces every order-independent output",
     "attention": "torch.nn.functional.scaled_dot_product_attention (float64) on dequantized rows + torch.logsumexp;"
@@ -563,3 +565,25 @@ def wcache_step(tag, rr, idx, R, W):
             content[st] = sorted(t[st * W:(st + 1) * W].tolist())
     return {"hits": hits, "pinned": pinned, "misses": sorted(miss), "placed": placed, "spills": spills,
             "rr_next": rr_next, "content": content}
+
+
+# ------------------------------------------------------------------------------------------------ MLA absorbed matmuls
+def bmm_fp8_weights(codes, scales, scale_k):
+    """bf16 values (as float64) of block-scaled FP8 weights W[n][j][k] = bf16(fp32(e4m3(code) * S)), S =
+    scales[n][j][k // 128] (scale_k) else scales[n][k][j // 128] (dotsnote/engine/arcstats_pkg/arcstats/mla_fp8.py:
+    46-52: (w.to(float32) * s).to(bfloat16))."""
+    c = np.asarray(codes, dtype=np.uint8)
+    N, J, K = c.shape
+    s = np.asarray(scales, dtype=np.float32)
+    if scale_k:
+        S = np.repeat(s, 128, axis=2)[:, :, :K]
+    else:
+        S = np.repeat(s, 128, axis=2)[:, :, :J].transpose(0, 2, 1)
+    prod = (e4m3_decode(c).astype(np.float32) * S.astype(np.float32)).astype(np.float32)
+    return bf16_bits_to_f32(f32_to_bf16_bits(prod)).astype(np.float64)
+
+
+def bmm_fp8(a, codes, scales, scale_k):
+    """C[n][b][j] = sum_k A[n][b][k] * W[n][j][k] (mla_fp8.py:20-57), A the bf16 values, float64 result."""
+    W = bmm_fp8_weights(codes, scales, scale_k)
+    return np.einsum("nbk,njk->nbj", np.asarray(a, dtype=np.float64), W)
