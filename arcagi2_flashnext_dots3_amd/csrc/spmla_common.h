@@ -33,10 +33,9 @@ __host__ __device__ inline float bf2f(uint16_t b) { return u2f((uint32_t)b << 16
 
 // fp32 -> bf16, round to nearest even (NaN kept quiet).
 __host__ __device__ inline uint16_t f2bf_rne(float f) {
-  uint32_t u = f2u(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = f2u(f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : r);   // a select, not a branch
 }
 
 // OCP e4m3fn encoder, round to nearest even, from the format definition: bias 7, 3 mantissa bits,

@@ -17,7 +17,8 @@ reference's compact Row400 rows (decoded on the way in; 400 instead of 656 bytes
 stream of fresh Zipf draws (`--config 3 --cache ways`).
 
 Other configs print their own JSON line (same keys): 1 = B=1 / 16 heads / K=256 check + timing, 3 = offload split-K,
-4 = indexer logits + top-2048 at L = 32768 and 131072, 5 = chunked prefill (8192 queries) + cache write.
+4 = indexer logits + top-2048 at L = 32768 and 131072, 5 = chunked prefill (8192 queries) + cache write, 6 = the
+absorbed FP8 matmuls either side of the decode attention (query build + output).
 """
 import argparse
 import json
@@ -437,6 +438,111 @@ def run_config5(a, dev):
 
 
 # ------------------------------------------------------------------------------------------------ config 1
+def _graphed(fn, reps):
+    """`reps` calls of fn captured into one HIP graph (torch.cuda.CUDAGraph; the library's entry points launch on
+    torch's current stream, which is the capture stream inside torch.cuda.graph). Returns the graph's replay. One
+    graph launch costs about as much as a few-microsecond kernel, so a decode loop's graph holds many launches."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    torch.cuda.synchronize()
+    return g.replay
+
+
+def _graph_ms(fn, steps, warmup, reps=50):
+    """Average ms of one fn() call replayed from graphs of `reps` calls (at least `steps` calls timed)."""
+    replay = _graphed(fn, reps)
+    n = max(1, (steps + reps - 1) // reps)
+    return _timed(replay, n, max(1, warmup // reps)) / reps
+
+
+def run_config6(a, dev):
+    """The steps either side of the decode attention at config-2 shapes (B = 64 tokens, H = 128 heads): the fused
+    query build q[t, h] = (q_nope @ W_UK_T[h], q_pe) and the output matmul attn_out @ W_UV[h], both on FP8
+    block-scaled weights (128 x 512 per head and direction). Beside it: torch.bmm on the bf16 weights they replace.
+    A decode loop replays its launches from a HIP graph; each side is timed that way (the host-side dispatch of a
+    few-microsecond launch from Python would otherwise be what is measured) and eagerly for reference."""
+    import torch
+    from arcagi2_flashnext_dots3_amd import kernels
+    N, T, P, L, V = H, B, 128, 512, 128
+    g = torch.Generator().manual_seed(9)
+    cu = (torch.randn(N, L, P, generator=g) * 60).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).to(dev)
+    su = (torch.exp(torch.randn(N, P, L // 128, generator=g)) * 1e-3).to(dev)
+    cv = (torch.randn(N, V, L, generator=g) * 60).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).to(dev)
+    sv = (torch.exp(torch.randn(N, V, L // 128, generator=g)) * 1e-3).to(dev)
+    q_nope = torch.randn(T, N, P, generator=g).to(torch.bfloat16).to(dev)
+    q_pe = torch.randn(T, N, 64, generator=g).to(torch.bfloat16).to(dev)
+    x = torch.randn(T, N, L, generator=g).to(torch.bfloat16).to(dev)
+    q = torch.empty(T, N, D, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(T, N, V, dtype=torch.bfloat16, device=dev)
+
+    def query():
+        kernels.mla_query(q_nope, q_pe, cu, su, out=q)
+
+    def output():
+        kernels.bmm_fp8(x.transpose(0, 1), cv, sv, True, y.transpose(0, 1))
+
+    def step():
+        query()
+        output()
+
+    step()
+    torch.cuda.synchronize()
+    q_e, y_e = q.clone(), y.clone()
+    eager_ms = _timed(step, a.steps, a.warmup)
+    replay = _graphed(step, 1)
+    q.zero_()
+    y.zero_()
+    for _ in range(3):                                  # every replay reproduces the eager result
+        replay()
+        torch.cuda.synchronize()
+        if not (torch.equal(q, q_e) and torch.equal(y, y_e)):
+            raise SystemExit("config 6: graph replay differs from the eager step")
+    ms = _graph_ms(step, a.steps, a.warmup)
+    q_us = _graph_ms(query, a.steps, a.warmup) * 1e3
+    v_us = _graph_ms(output, a.steps, a.warmup) * 1e3
+    # bytes: FP8 codes + fp32 block scales + activations in and out
+    qb = N * L * P + su.numel() * 4 + T * N * P * 2 + T * N * 64 * 2 + T * N * D * 2
+    vb = N * V * L + sv.numel() * 4 + T * N * L * 2 + T * N * V * 2
+    flops = 2 * T * N * L * P * 2
+    # the bf16 path they replace: torch.bmm on dequantized bf16 weights (twice the weight bytes), also graphed
+    wu = (cu.view(torch.float8_e4m3fn).float() * su.repeat_interleave(128, 2).transpose(1, 2)).to(torch.bfloat16)
+    wv = (cv.view(torch.float8_e4m3fn).float() * sv.repeat_interleave(128, 2)).to(torch.bfloat16)
+    wu_t = wu.transpose(1, 2).contiguous()                  # [N, P, L]
+    wv_t = wv.transpose(1, 2).contiguous()                  # [N, L, V]
+    qn_h = q_nope.transpose(0, 1).contiguous()
+    x_h = x.transpose(0, 1).contiguous()
+
+    def step_bf16():
+        torch.cat([torch.bmm(qn_h, wu_t).transpose(0, 1), q_pe], dim=2)
+        torch.bmm(x_h, wv_t)
+
+    ms_bf16 = _graph_ms(step_bf16, a.steps, a.warmup)
+    ms_bf16_eager = _timed(step_bf16, a.steps, a.warmup)
+    gbs = (qb + vb) / (ms * 1e-3) / 1e9
+    return _line("MLA absorbed matmuls (query build + output), FP8 weights, B=64 H=128, us per decode step", ms * 1e3,
+                 "us", a, ms, "e4m3 weights dequantized to bf16, bf16 MFMA, fp32 accumulate",
+                 {"workload": "q[t,h] = (q_nope @ W_UK_T[h], q_pe) into the [64, 128, 576] attention query + "
+                              "attn_out @ W_UV[h] -> [64, 128, 128]; per head 128 x 512 FP8 weights each way, "
+                              "128 x 128 block scales; steps replayed from HIP graphs of 50"},
+                 {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                  "kernel": "spmla::mla::bmm_fp8_staged_kernel"},
+                 hib=False, query_build_us=round(q_us, 2), output_bmm_us=round(v_us, 2),
+                 eager_us=round(eager_ms * 1e3, 2), alg_bytes=qb + vb,
+                 tflops=round(flops / (ms * 1e-3) / 1e12, 2), torch_bf16_bmm_us=round(ms_bf16 * 1e3, 2),
+                 torch_bf16_bmm_eager_us=round(ms_bf16_eager * 1e3, 2))
+
+
 def run_config1(a, dev):
     import numpy as np
     import torch
@@ -474,7 +580,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-variant", action="store_true", help="config 2 only: skip the host-tier (config 3) variant")
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6])
     ap.add_argument("--host-rows", default="row656", choices=["row656", "e2m2"],
                     help="config 3: host pool row format (Row656, or the reference's compact Row400 e2m2b32 rows)")
     ap.add_argument("--cache", default="static", choices=["static", "ways"],
@@ -525,6 +631,8 @@ def main():
         res = run_config4(a, dev)
     elif a.config == 5:
         res = run_config5(a, dev)
+    elif a.config == 6:
+        res = run_config6(a, dev)
     else:
         res = run_config1(a, dev)
     print(json.dumps(res), flush=True)

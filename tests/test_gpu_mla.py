@@ -62,3 +62,50 @@ def test_mla_query(dev):
     assert np.all(np.abs(got - want) <= bound + 1e-30)
     assert torch.equal(q[:, :, 512:].cpu(), q_pe)
     assert bool((buf[:, :, 576:] == 7).all())
+
+
+@pytest.mark.parametrize("scale_k", [True, False])
+def test_bmm_fp8_dequant_exact(dev, scale_k):
+    """A = identity rows: C[n][b][j] = W[n][j][b] with nothing else added, so the fp32 output shows every dequantized
+    weight bit for bit: all 254 non-NaN codes at scales that land on bf16 rounding ties and near the fp32 subnormal
+    range."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    N, J, K = 2, 256, 256
+    c = np.arange(J * K, dtype=np.int64).reshape(1, J, K) * 7 % 256
+    c = np.where((c & 0x7f) == 0x7f, 0, c).astype(np.uint8).repeat(N, 0)                 # no NaN codes
+    g = np.random.default_rng(3)
+    sshape = (N, J, 2) if scale_k else (N, K, 2)
+    # 1 + 2^-8 + 2^-9 style scales give products with exact halfway bits; some tiny, some plain random
+    ties = (1.0 + g.integers(0, 256, sshape) / 256.0 + 2.0 ** -9) * 2.0 ** g.integers(-20, 4, sshape)
+    scales = np.where(g.random(sshape) < 0.5, ties, np.exp(g.standard_normal(sshape)) * 1e-3).astype(np.float32)
+    scales[0, 0, 0] = 2.0 ** -110                      # tiny products, still normal (MFMA may flush subnormal inputs)
+    a = torch.eye(K, dtype=torch.bfloat16).expand(N, K, K).contiguous()
+    out = torch.empty(N, K, J, dtype=torch.float32, device=dev)
+    kernels.bmm_fp8(a.to(dev), torch.from_numpy(c).to(dev), torch.from_numpy(scales).to(dev), scale_k, out)
+    torch.cuda.synchronize()
+    want = ref.bmm_fp8_weights(c, scales, scale_k).transpose(0, 2, 1)
+    assert np.array_equal(out.cpu().numpy().astype(np.float64), want)
+
+
+@pytest.mark.parametrize("out_f32", [True, False])
+def test_bmm_fp8_strided_operands(dev, out_f32):
+    """Operands the staged (LDS) kernel does not take — A strided along k, codes strided along k, an output strided
+    along j — run on the register kernel; both kernels meet the same bound, and the staged one serves the same
+    values with contiguous copies of the operands."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    N, B, J, K = 3, 50, 96, 256
+    codes, scales = _weights(N, J, K, True, 21)
+    g = torch.Generator().manual_seed(22)
+    a_nkb = torch.randn(N, K, B, generator=g).to(torch.bfloat16)
+    a = a_nkb.transpose(1, 2)                                          # [N, B, K], stride along k = B
+    codes_t = codes.transpose(1, 2).contiguous().transpose(1, 2)       # [N, J, K], stride along k = J
+    dt = torch.float32 if out_f32 else torch.bfloat16
+    out_s = torch.empty(N, J, B, dtype=dt, device=dev).transpose(1, 2)  # stride along j = B
+    kernels.bmm_fp8(a_nkb.to(dev).transpose(1, 2), codes_t.to(dev), scales.to(dev), True, out_s)
+    out_c = torch.empty(N, B, J, dtype=dt, device=dev)
+    kernels.bmm_fp8(a.contiguous().to(dev), codes.to(dev), scales.to(dev), True, out_c)
+    torch.cuda.synchronize()
+    want = ref.bmm_fp8(a.float().numpy(), codes.numpy(), scales.numpy(), True)
+    bound = 2.0 ** -18 * _bound(a, codes, scales, True) + (0.0 if out_f32 else 2.0 ** -8 * np.abs(want))
+    for got in (out_s, out_c):
+        assert np.all(np.abs(got.float().cpu().numpy().astype(np.float64) - want) <= bound + 1e-30)
