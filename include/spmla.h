@@ -260,6 +260,26 @@ int spmla_lse_merge(const void* parts, int parts_bf16, long long o_ps, long long
                     long long out_st, long long out_sh, float* out_f32, float* lse_out, long long lo_st,
                     void* stream);
 
+/* Per-head matmul on FP8 block-scaled weights: C[n][b][j] = sum_k A[n][b][k] * bf16(fp32(e4m3(W[n][j][k]) * S)),
+ * S = s[n][j][k / 128] (scale_k = 1) or s[n][k][j / 128] (scale_k = 0), fp32 accumulation. A bf16 (strides sa_*),
+ * W e4m3 codes (strides sw_*), s fp32 (strides ss_n, ss_0, ss_1 over its three dimensions), C bf16 or fp32 (out_f32)
+ * with strides sc_*. K % 8 == 0. Contiguous, 16-byte aligned operands with K % 16 == 0 take the LDS-staged kernel.
+ * Replaces _bmm_fp8_kernel / bmm_fp8 (dotsnote/engine/arcstats_pkg/arcstats/mla_fp8.py:22-67), which serves MLA's
+ * absorbed W_UK_T and W_UV products (its _TorchProxy.bmm, :121-132). */
+int spmla_bmm_fp8(const void* a, long long sa_n, long long sa_b, long long sa_k, const void* w, long long sw_n,
+                  long long sw_j, long long sw_k, const float* s, long long ss_n, long long ss_0, long long ss_1,
+                  int scale_k, void* c, long long sc_n, long long sc_b, long long sc_j, int out_f32, int N, int B,
+                  int J, int K, void* stream);
+
+/* The decode query of the sparse attention in one launch: q[t][h][0:512] = q_nope[t][h][0:128] @ W_UK_T[h] on the
+ * FP8 form (codes [H][512][128] contiguous, scales [H][128][4] fp32, scale over k), q[t][h][512:576] = q_pe[t][h]
+ * copied bit for bit. q rows 16-byte aligned (strides q_st, q_sh, in elements, multiples of 8).
+ * Replaces the qcat patch's bmm into the first columns of the concatenated query plus the q_pe copy
+ * (dotsnote/engine/arcstats_pkg/arcstats/qcat.py:20-28), with mla_fp8's FP8 weights (mla_fp8.py:77-109). */
+int spmla_mla_query(const void* q_nope, long long qn_st, long long qn_sh, const void* q_pe, long long qp_st,
+                    long long qp_sh, const void* w_uk, const float* s_uk, int T, int H, void* q, long long q_st,
+                    long long q_sh, void* stream);
+
 /* Build identification string (static storage). */
 const char* spmla_version(void);
 

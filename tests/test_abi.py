@@ -23,6 +23,21 @@ def test_exports_every_declared_symbol():
     assert set(declared) <= set(_lib.SIGNATURES), "ctypes signatures must cover every declared entry point"
 
 
+def test_every_export_is_declared():
+    """The other direction: no spmla_ entry point leaves the library without a declaration (and its citation) in
+    include/spmla.h. Read from the dynamic symbol table with nm."""
+    import shutil
+    import subprocess
+    from arcagi2_flashnext_dots3_amd import _lib
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--defined-only", _lib.lib()._name], capture_output=True, text=True, check=True)
+    exported = sorted({f[2] for f in (ln.split() for ln in out.stdout.splitlines())
+                       if len(f) == 3 and f[1] == "T" and f[2].startswith("spmla_")})
+    assert exported and sorted(set(exported) - set(_declared())) == []
+
+
 def test_version():
     from arcagi2_flashnext_dots3_amd import _lib
     assert _lib.lib().spmla_version().startswith(b"spmla-gfx950")
