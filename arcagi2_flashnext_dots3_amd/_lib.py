@@ -47,6 +47,7 @@ SIGNATURES = {
     "spmla_lse_merge": [P, I, LL, LL, LL, P, LL, LL, I, I, I, P, LL, LL, P, P, LL, P],
     "spmla_bmm_fp8": [P, LL, LL, LL, P, LL, LL, LL, P, LL, LL, LL, I, P, LL, LL, LL, I, I, I, I, I, P],
     "spmla_mla_query": [P, LL, LL, P, LL, LL, P, P, I, I, P, LL, LL, P],
+    "spmla_topk_overlap": [P, LL, LL, I, I, I, P, P, P],
     "spmla_version": [],
     "spmla_host_e4m3_encode": [P, P, LL],
 }

@@ -494,3 +494,15 @@ def mla_query(q_nope, q_pe, codes_uk, scales_uk, out=None):
               q_pe.stride(0), q_pe.stride(1), codes_uk.data_ptr(), scales_uk.data_ptr(), T, H, out.data_ptr(),
               out.stride(0), out.stride(1), _stream(q_nope))
     return out
+
+
+def topk_overlap(sets):
+    """sets: int32 [L, n, K] top-k rows of L layers (-1 = none) -> (hits [L, L, n] int32: valid entries of layer b
+    also in layer a, diagonal 0; nvalid [L, n] int32)."""
+    _need(sets.dtype == torch.int32 and sets.dim() == 3 and sets.stride(2) == 1, "topk_overlap: int32 [L, n, K]")
+    L, n, K = sets.shape
+    hits = torch.zeros(L, L, n, dtype=torch.int32, device=sets.device)
+    nvalid = torch.empty(L, n, dtype=torch.int32, device=sets.device)
+    _lib.call("spmla_topk_overlap", sets.data_ptr(), sets.stride(0), sets.stride(1), L, n, K, hits.data_ptr(),
+              nvalid.data_ptr(), _stream(sets))
+    return hits, nvalid

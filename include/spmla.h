@@ -280,6 +280,15 @@ int spmla_mla_query(const void* q_nope, long long qn_st, long long qn_sh, const 
                     long long qp_sh, const void* w_uk, const float* s_uk, int T, int H, void* q, long long q_st,
                     long long q_sh, void* stream);
 
+/* Top-k overlap of L layers' selections for n query rows: for layers a != b, hits[(a L + b) n + i] = number of valid
+ * entries (>= 0) of layer b's row i that also occur in layer a's row i (symmetric for duplicate-free rows; the
+ * diagonal is not written); nvalid[a n + i] = valid entries of layer a's row i. Entry k of layer l, row i at
+ * sets[l s_l + i s_r + k]. K <= 2048.
+ * Replaces TopkOverlap._accumulate's sort / searchsorted intersection (dotsnote/engine/arcstats_pkg/arcstats/
+ * index_share.py:109-130), the statistic behind cross-layer top-k sharing (ARC_INDEX_SHARE). */
+int spmla_topk_overlap(const int* sets, long long s_l, long long s_r, int L, int n, int K, int* hits, int* nvalid,
+                       void* stream);
+
 /* Build identification string (static storage). */
 const char* spmla_version(void);
 

@@ -50,6 +50,9 @@ PINS = {
     "compact_stage": "torch.unique(sorted=True, return_inverse=True) (library)",
     "gather": "numpy fancy indexing",
     "tier_split": "python loop with stable order",
+    "topk_overlap": "the reference's own statement (sort, searchsorted, gather-compare, torch) on random rows with "
+                    "-1 padding; python set arithmetic on tiny rows; symmetry, hits <= min(|a|, |b|), identical rows "
+                    "give |a|, disjoint rows give 0",
 }
 
 
@@ -587,3 +590,22 @@ def bmm_fp8(a, codes, scales, scale_k):
     """C[n][b][j] = sum_k A[n][b][k] * W[n][j][k] (mla_fp8.py:20-57), A the bf16 values, float64 result."""
     W = bmm_fp8_weights(codes, scales, scale_k)
     return np.einsum("nbk,njk->nbj", np.asarray(a, dtype=np.float64), W)
+
+
+def topk_overlap(sets):
+    """Top-k overlap of L layers' selections (dotsnote/engine/arcstats_pkg/arcstats/index_share.py:109-130): sets
+    int [L, n, K] (-1 = none) -> hits [L, L, n] (hits[a, b, i] = number of entries x >= 0 of sets[b, i] with x in
+    sets[a, i], counted with multiplicity in b; diagonal 0) and nvalid [L, n] (entries >= 0)."""
+    s = np.asarray(sets, dtype=np.int64)
+    L, n, K = s.shape
+    hits = np.zeros((L, L, n), dtype=np.int64)
+    nvalid = (s >= 0).sum(axis=2)
+    for i in range(n):
+        for a in range(L):
+            A = s[a, i][s[a, i] >= 0]
+            for b in range(L):
+                if a == b:
+                    continue
+                B = s[b, i][s[b, i] >= 0]
+                hits[a, b, i] = int(np.isin(B, A).sum())
+    return hits, nvalid
