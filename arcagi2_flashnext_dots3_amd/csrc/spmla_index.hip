@@ -39,6 +39,7 @@ struct LogitParams {
   float* out; long long out_st;
   int bs_sh, rpb_sh, p_sh;                   // log2 of bs, rpb, P when a power of two, else -1
   long long lim;                             // R_local * P (< 2^31): valid block-table positions lie below
+  int clamp;                                 // 1: logits clamped at 60000 (shard kernels); 0: unclamped (paged)
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -63,7 +64,10 @@ constexpr int LG_OFF_BT = LG_OFF_SC + LG_NBUF * 128;
 constexpr int LG_WAVE = LG_OFF_BT + LG_NBT * 128;   // LDS bytes per wave
 constexpr int LG_WAVES = 4;
 
-template <bool POW2>
+// SHUF: the keys live in vLLM's paged SHUFFLE layout (P = 1, rpb = keys per block): key t of a block has its
+// 16-byte chunk c at (t / 16) * 2048 + (t % 16) * 16 + 256 c and its scale at rpb * 128 + 4 t
+// (dotsnote/engine/arcstats_pkg/arcstats/dsa_sm89.py:63-66); otherwise 132-byte rows [128 codes | scale].
+template <bool POW2, bool SHUF>
 __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LG_WAVES * LG_WAVE];
   const int row = blockIdx.x;
@@ -110,8 +114,10 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
     const long long tt = (long long)blk * p.bs + md(pos, (uint32_t)p.bs, p.bs_sh);
     ok = ok && tt < p.lim;
     const uint32_t lrow = ok ? dv((uint32_t)tt, (uint32_t)p.P, p.p_sh) : 0u;   // p.lim > 0: row 0 exists
-    const uint8_t* rp = p.store + (long long)dv(lrow, (uint32_t)p.rpb, p.rpb_sh) * p.blk_stride +
-                        md(lrow, (uint32_t)p.rpb, p.rpb_sh) * 132u;
+    const uint8_t* kblk = p.store + (long long)dv(lrow, (uint32_t)p.rpb, p.rpb_sh) * p.blk_stride;
+    const uint32_t kt = md(lrow, (uint32_t)p.rpb, p.rpb_sh);
+    const uint8_t* rp = SHUF ? kblk + (kt >> 4) * 2048u + (kt & 15u) * 16u : kblk + kt * 132u;   // chunk 0
+    const uint8_t* sp = SHUF ? kblk + (uint32_t)p.rpb * 128u + 4u * kt : rp + 128;               // scale
     const long long ra = (long long)(uintptr_t)rp;
     SPMLA_LDS uint8_t* cb = lds + (t % LG_NBUF) * LG_CODES;
 #pragma unroll
@@ -119,9 +125,9 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
       const int r = 8 * i + (lane >> 3);
       const int c = (lane & 7) ^ (r & 7);               // chunk that lands in 16-byte slot lane & 7 of row r
       const long long a = __shfl(ra, r, 64);
-      dma16((const uint8_t*)(uintptr_t)a + 16 * c, cb + 8 * i * 128);
+      dma16((const uint8_t*)(uintptr_t)a + (SHUF ? 256 : 16) * c, cb + 8 * i * 128);
     }
-    if (lane < 32) dma4(rp + 128, lds + LG_OFF_SC + (t % LG_NBUF) * 128);
+    if (lane < 32) dma4(sp, lds + LG_OFF_SC + (t % LG_NBUF) * 128);
     return ok;
   };
 
@@ -199,7 +205,7 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
     part += __shfl_xor(part, 32, 64);
     const int j = j_wv + 32 * t + l32;
     if (half == 0 && j < p.Lc) {
-      const float lg = fminf(part * sc, 60000.f);
+      const float lg = p.clamp ? fminf(part * sc, 60000.f) : part * sc;
       if (ok0) orow[j] = lg;
       else if (!p.noinf) orow[j] = -__builtin_inff();
     }
@@ -982,11 +988,41 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
   auto log2_or = [](long long v) { return (v & (v - 1)) == 0 ? __builtin_ctzll((unsigned long long)v) : -1; };
   p.bs_sh = log2_or(block_size); p.rpb_sh = log2_or(rows_per_block); p.p_sh = log2_or(P);
   p.lim = R_local * P;
+  p.clamp = 1;
   dim3 grid(rows, (Lc + idx::LG_KPB - 1) / idx::LG_KPB);
   if (p.bs_sh >= 0 && p.rpb_sh >= 0 && p.p_sh >= 0)
-    hipLaunchKernelGGL(idx::logits_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((idx::logits_kernel<true, false>), grid, dim3(256), 0, (hipStream_t)stream, p);
   else
-    hipLaunchKernelGGL(idx::logits_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((idx::logits_kernel<false, false>), grid, dim3(256), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}
+
+int spmla_paged_mqa_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
+                           const void* cache, long long num_blocks, int block_size, long long block_stride,
+                           const int* block_table, long long bt_st, const int* req, const int* ctx, int rows, int H,
+                           int D, int Lc, int noinf, float* out, long long out_st, void* stream) {
+  if (rows < 0 || Lc < 0 || block_size <= 0 || (block_size & 15) || num_blocks < 0) return SPMLA_EARG;
+  if (rows == 0 || Lc == 0) return SPMLA_OK;
+  if (H != 64 || D != 128) return SPMLA_ELIMIT;
+  if (num_blocks > (long long)INT_MAX / block_size) return SPMLA_ELIMIT;
+  if (!q || !w || !cache || !block_table || !req || !ctx || !out) return SPMLA_EARG;
+  if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)cache & 3) || (block_stride & 3) ||
+      block_stride < (long long)block_size * 132)
+    return SPMLA_EALIGN;
+  idx::LogitParams p;
+  p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh; p.w = w; p.w_st = w_st;
+  p.store = (const uint8_t*)cache; p.R_local = num_blocks * block_size; p.rpb = block_size;
+  p.blk_stride = block_stride; p.bt = block_table; p.bt_st = bt_st; p.bs = block_size; p.req = req; p.ctx = ctx;
+  p.rows = rows; p.Lc = Lc; p.P = 1; p.rank = 0; p.noinf = noinf; p.out = out; p.out_st = out_st;
+  auto log2_or = [](long long v) { return (v & (v - 1)) == 0 ? __builtin_ctzll((unsigned long long)v) : -1; };
+  p.bs_sh = log2_or(block_size); p.rpb_sh = p.bs_sh; p.p_sh = 0;
+  p.lim = p.R_local;
+  p.clamp = 0;
+  dim3 grid(rows, (Lc + idx::LG_KPB - 1) / idx::LG_KPB);
+  if (p.bs_sh >= 0)
+    hipLaunchKernelGGL((idx::logits_kernel<true, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL((idx::logits_kernel<false, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 

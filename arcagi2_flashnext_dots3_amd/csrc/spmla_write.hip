@@ -135,6 +135,9 @@ struct KeyParams {
   uint8_t* store; long long R_local;       // local rows
   int P, rank, rpb; long long blk_stride;  // row r at (r / rpb) * blk_stride + (r % rpb) * 132
   int ue8m0;
+  int shuf;                                // vLLM's paged SHUFFLE layout (P = 1): key t of a block of rpb keys has
+                                           // its 16-byte chunk c at (t / 16) * 2048 + (t % 16) * 16 + 256 c and its
+                                           // scale at rpb * 128 + 4 t
 };
 
 __global__ void __launch_bounds__(256) key_write_kernel(KeyParams p) {
@@ -145,7 +148,12 @@ __global__ void __launch_bounds__(256) key_write_kernel(KeyParams p) {
   if (slot < 0 || slot % p.P != p.rank) return;
   const long long r = slot / p.P;
   if (r >= p.R_local) return;
-  uint8_t* row = p.store + (r / p.rpb) * p.blk_stride + (r % p.rpb) * 132;
+  uint8_t* blk = p.store + (r / p.rpb) * p.blk_stride;
+  const int t = (int)(r % p.rpb);
+  uint8_t* row = blk + t * 132;                                        // 132-byte rows
+  uint8_t* code = p.shuf ? blk + (t >> 4) * 2048 + (t & 15) * 16 + (lane >> 3) * 256 + (lane & 7) * 2
+                         : row + lane * 2;
+  float* scale = (float*)(p.shuf ? blk + p.rpb * 128 + 4 * t : row + 128);
   const uint32_t raw = *(const uint32_t*)(p.k + (long long)tok * p.k_st + lane * 2);
   const float x0 = u2f(raw << 16), x1 = u2f(raw & 0xffff0000u);
   float am = fmaxf(fabsf(x0), fabsf(x1));
@@ -159,8 +167,8 @@ __global__ void __launch_bounds__(256) key_write_kernel(KeyParams p) {
     s = u2f(u);
   }
   const uint32_t c = (uint32_t)e4m3_rne(x0 / s) | ((uint32_t)e4m3_rne(x1 / s) << 8);
-  *(uint16_t*)(row + lane * 2) = (uint16_t)c;
-  if (lane == 0) *(float*)(row + 128) = s;
+  *(uint16_t*)code = (uint16_t)c;
+  if (lane == 0) *scale = s;
 }
 
 }  // namespace wr
@@ -200,6 +208,24 @@ int spmla_index_key_write(const void* k, long long k_st, const long long* slots,
   wr::KeyParams p;
   p.k = (const uint16_t*)k; p.k_st = k_st; p.slots = slots; p.n = n; p.store = (uint8_t*)store;
   p.R_local = R_local; p.P = P; p.rank = rank; p.rpb = rows_per_block; p.blk_stride = block_stride; p.ue8m0 = ue8m0;
+  p.shuf = 0;
+  hipLaunchKernelGGL(wr::key_write_kernel, dim3((n + 3) / 4), dim3(256), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}
+
+int spmla_index_key_write_shuffle(const void* k, long long k_st, const long long* slots, int n, void* cache,
+                                  long long num_blocks, int block_size, long long block_stride, int ue8m0,
+                                  void* stream) {
+  if (n < 0 || num_blocks < 0 || block_size <= 0 || (block_size & 15)) return SPMLA_EARG;
+  if (n == 0) return SPMLA_OK;
+  if (!k || !slots || !cache) return SPMLA_EARG;
+  if (((uintptr_t)k & 3) || (k_st & 1) || ((uintptr_t)cache & 3) || (block_stride & 3) ||
+      block_stride < (long long)block_size * 132)
+    return SPMLA_EALIGN;
+  wr::KeyParams p;
+  p.k = (const uint16_t*)k; p.k_st = k_st; p.slots = slots; p.n = n; p.store = (uint8_t*)cache;
+  p.R_local = num_blocks * block_size; p.P = 1; p.rank = 0; p.rpb = block_size; p.blk_stride = block_stride;
+  p.ue8m0 = ue8m0; p.shuf = 1;
   hipLaunchKernelGGL(wr::key_write_kernel, dim3((n + 3) / 4), dim3(256), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }

@@ -66,6 +66,65 @@ def index_key_write(k, slots, store, P=1, rank=0, ue8m0=False):
               rpb, bstride, int(bool(ue8m0)), _stream(k))
 
 
+def _shuffle_cache(kv_cache):
+    """vLLM's indexer key cache [blocks, bs, 1, 132] / [blocks, bs, 132] / [blocks, bs * 132] uint8 -> (blocks, bs,
+    block stride in bytes)."""
+    _need(kv_cache.dtype == torch.uint8, "indexer key cache must be uint8")
+    if kv_cache.dim() >= 3:
+        nb, bs = kv_cache.shape[0], kv_cache.shape[1]
+        _need(kv_cache[0].numel() == bs * KEYROW, "indexer key cache rows of 132 bytes")
+    else:
+        nb, bs = kv_cache.shape[0], kv_cache.shape[1] // KEYROW
+    _need(bs % 16 == 0, "SHUFFLE layout needs a block size that is a multiple of 16")
+    return nb, bs, kv_cache.stride(0)
+
+
+def index_key_write_shuffle(k, slots, kv_cache, ue8m0=False):
+    """k [n, 128] bf16 -> vLLM's paged indexer key cache in the SHUFFLE layout (dsa_sm89.py:63-66): the same
+    per-key quantization as index_key_write, slot = block * bs + offset."""
+    n = min(k.shape[0], slots.shape[0])
+    _need(k.dtype == torch.bfloat16 and k.shape[1] == 128 and k.stride(1) == 1, "k [n, 128] bf16")
+    nb, bs, bstride = _shuffle_cache(kv_cache)
+    _lib.call("spmla_index_key_write_shuffle", k.data_ptr(), k.stride(0), slots.data_ptr(), n, kv_cache.data_ptr(),
+              nb, bs, bstride, int(bool(ue8m0)), _stream(k))
+
+
+def paged_ctx(seq_lens, next_n):
+    """Per logits row b * next_n + j: (request b, visible keys): seq_lens[b] - (next_n - 1 - j), or seq_lens[b, j]
+    for 2-D seq_lens (dsa_sm89.py:46-53). int32 tensors on seq_lens' device."""
+    B = seq_lens.shape[0]
+    dev = seq_lens.device
+    req = torch.arange(B * next_n, device=dev, dtype=torch.int32) // next_n
+    if seq_lens.dim() == 2:
+        ctx = seq_lens.reshape(-1).to(torch.int32)
+    else:
+        j = torch.arange(next_n, device=dev, dtype=torch.int32).repeat(B)
+        ctx = (seq_lens.to(torch.int32)[req.long()] - (next_n - 1 - j)).to(torch.int32)
+    return req.contiguous(), ctx.contiguous()
+
+
+def paged_mqa_logits(q, kv_cache, weights, seq_lens, block_table, max_model_len, out=None):
+    """paged_mqa_logits_triton (dsa_sm89.py:75-94): q [B, next_n, 64, 128] (bf16, or float8_e4m3fn widened exactly
+    to bf16), kv_cache vLLM's SHUFFLE indexer cache, weights [B * next_n, 64] fp32, seq_lens [B] or [B, next_n],
+    block_table [B, cols] int32 -> logits [B * next_n, max_model_len] fp32, -inf outside each row's context."""
+    B, nn, H, D = q.shape
+    if q.dtype == torch.float8_e4m3fn:
+        q = q.to(torch.bfloat16)
+    _need(q.dtype == torch.bfloat16 and q.stride(3) == 1, "q bf16 / e4m3 with contiguous head dim")
+    qr = q.reshape(B * nn, H, D)
+    _need(weights.dtype == torch.float32 and weights.stride(1) == 1, "weights fp32")
+    _need(block_table.dtype == torch.int32, "int32 block table")
+    nb, bs, bstride = _shuffle_cache(kv_cache)
+    req, ctx = paged_ctx(seq_lens, nn)
+    rows = B * nn
+    if out is None:
+        out = torch.empty(rows, max(max_model_len, 1), dtype=torch.float32, device=q.device)
+    _lib.call("spmla_paged_mqa_logits", qr.data_ptr(), qr.stride(0), qr.stride(1), weights.data_ptr(),
+              weights.stride(0), kv_cache.data_ptr(), nb, bs, bstride, block_table.data_ptr(), block_table.stride(0),
+              req.data_ptr(), ctx.data_ptr(), rows, H, D, max_model_len, 0, out.data_ptr(), out.stride(0), _stream(q))
+    return out
+
+
 # ---------------------------------------------------------------------------------------------- indexer
 def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P=1, rank=0, noinf=False):
     """q [rows, 64, 128] bf16, w [rows, 64] fp32, store [blocks, rpb, 132] uint8, block_table [nreq, cols] int32,

@@ -280,6 +280,26 @@ int spmla_mla_query(const void* q_nope, long long qn_st, long long qn_sh, const 
                     long long qp_sh, const void* w_uk, const float* s_uk, int T, int H, void* q, long long q_st,
                     long long q_sh, void* stream);
 
+/* Indexer key write into vLLM's paged indexer key cache in its SHUFFLE layout: key at slot = block * block_size + t
+ * (block_size % 16 == 0, block b at cache + b * block_stride bytes): its 128 e4m3 codes in 16-token x 16-byte tiles,
+ * code d at (t / 16) * 2048 + (t % 16) * 16 + (d / 16) * 256 + d % 16, its fp32 scale at block_size * 128 + 4 t; the
+ * quantization of spmla_index_key_write (s = max(amax, 1e-4) / 448, UE8M0 option). Slots < 0 or beyond the cache are
+ * skipped. The layout is the one the reference's paged reader addresses (dotsnote/engine/arcstats_pkg/arcstats/
+ * dsa_sm89.py:63-66); the writer it pairs with is vLLM's indexer cache insert (compiled, not in the tree). */
+int spmla_index_key_write_shuffle(const void* k, long long k_st, const long long* slots, int n, void* cache,
+                                  long long num_blocks, int block_size, long long block_stride, int ue8m0,
+                                  void* stream);
+
+/* spmla_index_logits over the SHUFFLE cache (P = 1, no 60000 clamp): out[row][j] = sum_h w[row][h] *
+ * relu(q[row][h] . kcode) * kscale for positions j < ctx[row] (key block block_table[req[row]][j / block_size]),
+ * -inf beyond (noinf: left unwritten). H = 64, D = 128, q bf16.
+ * Replaces paged_mqa_logits_triton / _paged_logits_kernel (dotsnote/engine/arcstats_pkg/arcstats/dsa_sm89.py:41-94),
+ * the decode logits of the reference's default indexer path; the host wrapper builds req / ctx for next_n > 1. */
+int spmla_paged_mqa_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
+                           const void* cache, long long num_blocks, int block_size, long long block_stride,
+                           const int* block_table, long long bt_st, const int* req, const int* ctx, int rows, int H,
+                           int D, int Lc, int noinf, float* out, long long out_st, void* stream);
+
 /* Top-k overlap of L layers' selections for n query rows: for layers a != b, hits[(a L + b) n + i] = number of valid
  * entries (>= 0) of layer b's row i that also occur in layer a's row i (symmetric for duplicate-free rows; the
  * diagonal is not written); nvalid[a n + i] = valid entries of layer a's row i. Entry k of layer l, row i at

@@ -50,6 +50,10 @@ PINS = {
     "compact_stage": "torch.unique(sorted=True, return_inverse=True) (library)",
     "gather": "numpy fancy indexing",
     "tier_split": "python loop with stable order",
+    "shuffle_layout": "the reference reader's byte offsets (16-token x 16-byte tiles, scales after the codes) written "
+                      "out element by element; shuffle_rows(shuffle_layout(x)) == x",
+    "paged_mqa_logits": "index_logits (pinned above) on the unshuffled rows with the reader's context rule "
+                        "(seq_len - (next_n - 1 - j), or the 2-D seq_lens entry) checked by hand; no clamp",
     "topk_overlap": "the reference's own statement (sort, searchsorted, gather-compare, torch) on random rows with "
                     "-1 padding; python set arithmetic on tiny rows; symmetry, hits <= min(|a|, |b|), identical rows "
                     "give |a|, disjoint rows give 0",
@@ -609,3 +613,64 @@ def topk_overlap(sets):
                 B = s[b, i][s[b, i] >= 0]
                 hits[a, b, i] = int(np.isin(B, A).sum())
     return hits, nvalid
+
+
+def shuffle_layout(rows, bs):
+    """132-byte key rows [R, 132] (R a multiple of bs) -> vLLM's paged SHUFFLE cache [R / bs, bs * 132]: in block b,
+    code d of key t at (t // 16) * 16 * 128 + (t % 16) * 16 + (d // 16) * 256 + d % 16, its fp32 scale at
+    bs * 128 + 4 t (dotsnote/engine/arcstats_pkg/arcstats/dsa_sm89.py:63-66)."""
+    rows = np.asarray(rows, dtype=np.uint8)
+    nb = rows.shape[0] // bs
+    out = np.zeros((nb, bs * KEYROW), dtype=np.uint8)
+    t = np.arange(bs)[:, None]
+    d = np.arange(128)[None, :]
+    off = (t // 16) * 2048 + (t % 16) * 16 + (d // 16) * 256 + d % 16
+    for b in range(nb):
+        blk = rows[b * bs:(b + 1) * bs]
+        out[b, off] = blk[:, :128]
+        out[b, bs * 128:] = blk[:, 128:132].reshape(-1)
+    return out
+
+
+def shuffle_rows(cache, bs):
+    """Inverse of shuffle_layout: [nb, bs * 132] -> [nb * bs, 132]."""
+    cache = np.asarray(cache, dtype=np.uint8).reshape(-1, bs * KEYROW)
+    nb = cache.shape[0]
+    rows = np.zeros((nb * bs, KEYROW), dtype=np.uint8)
+    t = np.arange(bs)[:, None]
+    d = np.arange(128)[None, :]
+    off = (t // 16) * 2048 + (t % 16) * 16 + (d // 16) * 256 + d % 16
+    for b in range(nb):
+        rows[b * bs:(b + 1) * bs, :128] = cache[b, off]
+        rows[b * bs:(b + 1) * bs, 128:132] = cache[b, bs * 128:].reshape(bs, 4)
+    return rows
+
+
+def index_key_write_shuffle(k_bits, slots, cache, bs, ue8m0=False):
+    """The indexer key write into the SHUFFLE cache: the same per-key quantization as index_key_write (P = 1),
+    stored at slot = block * bs + t in the layout of shuffle_layout."""
+    rows = shuffle_rows(cache, bs)
+    index_key_write(k_bits, slots, rows, P=1, rank=0, ue8m0=ue8m0)
+    cache[...] = shuffle_layout(rows, bs).reshape(cache.shape)
+    return cache
+
+
+def paged_ctx(seq_lens, next_n):
+    """Per logits row r = b * next_n + j: (request b, visible keys) as paged_mqa_logits_triton reads them
+    (dsa_sm89.py:46-53): seq_lens[b] - (next_n - 1 - j), or seq_lens[b, j] when seq_lens is 2-D."""
+    sl = np.asarray(seq_lens, dtype=np.int64)
+    B = sl.shape[0]
+    req = np.repeat(np.arange(B), next_n)
+    j = np.tile(np.arange(next_n), B)
+    ctx = sl.reshape(-1) if sl.ndim == 2 else sl[req] - (next_n - 1 - j)
+    return req, ctx
+
+
+def paged_mqa_logits(q, cache, w, seq_lens, block_table, bs, max_model_len):
+    """paged_mqa_logits_triton (dsa_sm89.py:41-94): q [B, next_n, H, D] values, cache [nb, bs * 132] SHUFFLE bytes,
+    w [B * next_n, H] -> [B * next_n, max_model_len] float64, -inf outside each row's context (no clamp)."""
+    q = np.asarray(q, dtype=np.float64)
+    B, nn, H, D = q.shape
+    req, ctx = paged_ctx(seq_lens, nn)
+    return index_logits(q.reshape(B * nn, H, D), w, shuffle_rows(cache, bs), block_table, bs, req, ctx,
+                        max_model_len, clamp=np.inf)
