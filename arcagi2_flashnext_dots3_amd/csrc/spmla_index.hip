@@ -40,6 +40,8 @@ struct LogitParams {
   int bs_sh, rpb_sh, p_sh;                   // log2 of bs, rpb, P when a power of two, else -1
   long long lim;                             // R_local * P (< 2^31): valid block-table positions lie below
   int clamp;                                 // 1: logits clamped at 60000 (shard kernels); 0: unclamped (paged)
+  const int* lo;                             // optional per-row first valid position (flat layout: cu_seqlen_ks)
+  const float* kscale; long long k_st;       // flat layout: key j codes at store + j * k_st, scale kscale[j]
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -64,11 +66,15 @@ constexpr int LG_OFF_BT = LG_OFF_SC + LG_NBUF * 128;
 constexpr int LG_WAVE = LG_OFF_BT + LG_NBT * 128;   // LDS bytes per wave
 constexpr int LG_WAVES = 4;
 
-// SHUF: the keys live in vLLM's paged SHUFFLE layout (P = 1, rpb = keys per block): key t of a block has its
-// 16-byte chunk c at (t / 16) * 2048 + (t % 16) * 16 + 256 c and its scale at rpb * 128 + 4 t
-// (dotsnote/engine/arcstats_pkg/arcstats/dsa_sm89.py:63-66); otherwise 132-byte rows [128 codes | scale].
-template <bool POW2, bool SHUF>
+// Key layouts: LY_ROW 132-byte rows [128 codes | scale] (the rank-sharded store); LY_SHUF vLLM's paged SHUFFLE
+// layout (P = 1, rpb = keys per block): key t of a block has its 16-byte chunk c at (t / 16) * 2048 + (t % 16) * 16
+// + 256 c and its scale at rpb * 128 + 4 t (dotsnote/engine/arcstats_pkg/arcstats/dsa_sm89.py:63-66); LY_FLAT the
+// prefill gather: key j (column j) at store + j * k_st, scale kscale[j], valid for lo[row] <= j < ctx[row], no
+// block table (dsa_sm89.py:97-118).
+enum { LY_ROW = 0, LY_SHUF = 1, LY_FLAT = 2 };
+template <bool POW2, int LY>
 __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
+  constexpr bool SHUF = LY == LY_SHUF, FLAT = LY == LY_FLAT;
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LG_WAVES * LG_WAVE];
   const int row = blockIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -85,21 +91,22 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
       for (int j = j_wv + lane; j < j_wv + 32 * nt && j < p.Lc; j += 64) orow[j] = -__builtin_inff();
     return;
   }
-  const int* btr = p.bt + (long long)p.req[row] * p.bt_st;
+  const int* btr = FLAT ? nullptr : p.bt + (long long)p.req[row] * p.bt_st;
+  const int lo = p.lo ? p.lo[row] : 0;
   // n / d, n % d: shifts when every divisor is a power of two (POW2), else 32-bit division
   auto dv = [&](uint32_t n, uint32_t d, int sh) -> uint32_t { return POW2 ? n >> sh : n / d; };
   auto md = [&](uint32_t n, uint32_t d, int sh) -> uint32_t { return POW2 ? n & (d - 1u) : n % d; };
   // positions without a block-table entry read the wave's first entry (in range)
-  const int* bt_dummy = btr + dv((uint32_t)(j_wv * p.P + p.rank), (uint32_t)p.bs, p.bs_sh);
+  const int* bt_dummy = FLAT ? nullptr : btr + dv((uint32_t)(j_wv * p.P + p.rank), (uint32_t)p.bs, p.bs_sh);
   auto key_pos = [&](int t, int r, uint32_t& pos) -> bool {
     const int j = j_wv + 32 * t + r;
     const long long ps = (long long)j * p.P + p.rank;
     pos = (uint32_t)ps;
-    return t < nt && j < p.Lc && ps < ctx;
+    return t < nt && j < p.Lc && ps < ctx && ps >= lo;
   };
   // LDS DMA of the block-table entries of tile t (lanes 0..31: key l32)
   auto issue_bt = [&](int t) {
-    if (lane < 32) {
+    if (!FLAT && lane < 32) {
       uint32_t pos;
       const bool in = key_pos(t, l32, pos);
       dma4(in ? btr + dv(pos, (uint32_t)p.bs, p.bs_sh) : bt_dummy, lds + LG_OFF_BT + (t & (LG_NBT - 1)) * 128);
@@ -108,16 +115,24 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
   // LDS DMA of the codes and scales of tile t (its block-table entries already in LDS). Lane l32 maps key l32 to
   // its row; the copying lanes take the row addresses from those lanes. Returns the lane's key-valid flag.
   auto issue_codes = [&](int t) -> bool {
-    const int blk = ((const SPMLA_LDS int*)(lds + LG_OFF_BT + (t & (LG_NBT - 1)) * 128))[l32];
     uint32_t pos;
-    bool ok = key_pos(t, l32, pos) && blk >= 0;
-    const long long tt = (long long)blk * p.bs + md(pos, (uint32_t)p.bs, p.bs_sh);
-    ok = ok && tt < p.lim;
-    const uint32_t lrow = ok ? dv((uint32_t)tt, (uint32_t)p.P, p.p_sh) : 0u;   // p.lim > 0: row 0 exists
-    const uint8_t* kblk = p.store + (long long)dv(lrow, (uint32_t)p.rpb, p.rpb_sh) * p.blk_stride;
-    const uint32_t kt = md(lrow, (uint32_t)p.rpb, p.rpb_sh);
-    const uint8_t* rp = SHUF ? kblk + (kt >> 4) * 2048u + (kt & 15u) * 16u : kblk + kt * 132u;   // chunk 0
-    const uint8_t* sp = SHUF ? kblk + (uint32_t)p.rpb * 128u + 4u * kt : rp + 128;               // scale
+    bool ok = key_pos(t, l32, pos);
+    const uint8_t* rp;
+    const void* sp;
+    if (FLAT) {                                        // key pos itself (pos < Lc = number of keys)
+      rp = p.store + (long long)(ok ? pos : 0u) * p.k_st;
+      sp = p.kscale + (ok ? pos : 0u);
+    } else {
+      const int blk = ((const SPMLA_LDS int*)(lds + LG_OFF_BT + (t & (LG_NBT - 1)) * 128))[l32];
+      ok = ok && blk >= 0;
+      const long long tt = (long long)blk * p.bs + md(pos, (uint32_t)p.bs, p.bs_sh);
+      ok = ok && tt < p.lim;
+      const uint32_t lrow = ok ? dv((uint32_t)tt, (uint32_t)p.P, p.p_sh) : 0u;   // p.lim > 0: row 0 exists
+      const uint8_t* kblk = p.store + (long long)dv(lrow, (uint32_t)p.rpb, p.rpb_sh) * p.blk_stride;
+      const uint32_t kt = md(lrow, (uint32_t)p.rpb, p.rpb_sh);
+      rp = SHUF ? kblk + (kt >> 4) * 2048u + (kt & 15u) * 16u : kblk + kt * 132u;   // chunk 0
+      sp = SHUF ? kblk + (uint32_t)p.rpb * 128u + 4u * kt : rp + 128;               // scale
+    }
     const long long ra = (long long)(uintptr_t)rp;
     SPMLA_LDS uint8_t* cb = lds + (t % LG_NBUF) * LG_CODES;
 #pragma unroll
@@ -169,7 +184,7 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
     bool ok2 = false;
     nprev = 0;
     if (t + 2 < nt) { ok2 = issue_codes(t + 2); nprev = 5; }
-    if (t + 4 < nt) { issue_bt(t + 4); nprev += 1; }
+    if (!FLAT && t + 4 < nt) { issue_bt(t + 4); nprev += 1; }
     // tile t
     const SPMLA_LDS uint8_t* cb = lds + (t % LG_NBUF) * LG_CODES + l32 * 128;
     bf16x8 kb[8];
@@ -989,11 +1004,12 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
   p.bs_sh = log2_or(block_size); p.rpb_sh = log2_or(rows_per_block); p.p_sh = log2_or(P);
   p.lim = R_local * P;
   p.clamp = 1;
+  p.lo = nullptr; p.kscale = nullptr; p.k_st = 0;
   dim3 grid(rows, (Lc + idx::LG_KPB - 1) / idx::LG_KPB);
   if (p.bs_sh >= 0 && p.rpb_sh >= 0 && p.p_sh >= 0)
-    hipLaunchKernelGGL((idx::logits_kernel<true, false>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_ROW>), grid, dim3(256), 0, (hipStream_t)stream, p);
   else
-    hipLaunchKernelGGL((idx::logits_kernel<false, false>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_ROW>), grid, dim3(256), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 
@@ -1018,11 +1034,36 @@ int spmla_paged_mqa_logits(const void* q, long long q_st, long long q_sh, const 
   p.bs_sh = log2_or(block_size); p.rpb_sh = p.bs_sh; p.p_sh = 0;
   p.lim = p.R_local;
   p.clamp = 0;
+  p.lo = nullptr; p.kscale = nullptr; p.k_st = 0;
   dim3 grid(rows, (Lc + idx::LG_KPB - 1) / idx::LG_KPB);
   if (p.bs_sh >= 0)
-    hipLaunchKernelGGL((idx::logits_kernel<true, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_SHUF>), grid, dim3(256), 0, (hipStream_t)stream, p);
   else
-    hipLaunchKernelGGL((idx::logits_kernel<false, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_SHUF>), grid, dim3(256), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}
+
+int spmla_mqa_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st, const void* k,
+                     long long k_st, const float* kscale, int N, const int* ks, const int* ke, int M, int H, int D,
+                     float* out, long long out_st, void* stream) {
+  if (M < 0 || N < 0) return SPMLA_EARG;
+  if (M == 0 || N == 0) return SPMLA_OK;
+  if (H != 64 || D != 128) return SPMLA_ELIMIT;
+  if (!q || !w || !k || !kscale || !ks || !ke || !out) return SPMLA_EARG;
+  if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)k & 3) || (k_st & 3) || k_st < 128 ||
+      ((uintptr_t)kscale & 3))
+    return SPMLA_EALIGN;
+  idx::LogitParams p;
+  p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh; p.w = w; p.w_st = w_st;
+  p.store = (const uint8_t*)k; p.R_local = N; p.rpb = 1; p.blk_stride = 0;
+  p.bt = nullptr; p.bt_st = 0; p.bs = 1; p.req = nullptr; p.ctx = ke;
+  p.rows = M; p.Lc = N; p.P = 1; p.rank = 0; p.noinf = 0; p.out = out; p.out_st = out_st;
+  p.bs_sh = p.rpb_sh = p.p_sh = 0;
+  p.lim = N;
+  p.clamp = 0;
+  p.lo = ks; p.kscale = kscale; p.k_st = k_st;
+  dim3 grid(M, (N + idx::LG_KPB - 1) / idx::LG_KPB);
+  hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_FLAT>), grid, dim3(256), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 

@@ -125,6 +125,29 @@ def paged_mqa_logits(q, kv_cache, weights, seq_lens, block_table, max_model_len,
     return out
 
 
+def mqa_logits(q, kv, weights, cu_seqlen_ks, cu_seqlen_ke):
+    """mqa_logits_triton (dsa_sm89.py:121-133), the prefill logits over gathered keys: q [M, 64, 128] (bf16, or
+    float8_e4m3fn widened exactly), kv = (codes [N, 128] e4m3 / uint8, scales [N] or [N, 1] fp32), weights [M, 64]
+    fp32, key range [ks[m], ke[m]) per row (int32) -> [M, N] fp32, -inf outside the range."""
+    codes, scales = kv
+    M, H, D = q.shape
+    N = codes.shape[0]
+    if q.dtype == torch.float8_e4m3fn:
+        q = q.to(torch.bfloat16)
+    _need(q.dtype == torch.bfloat16 and q.stride(2) == 1, "q bf16 / e4m3 with contiguous head dim")
+    codes = codes.view(torch.uint8) if codes.dtype != torch.uint8 else codes
+    _need(codes.dim() == 2 and codes.shape[1] == 128 and codes.stride(1) == 1, "codes [N, 128]")
+    sc = scales.reshape(-1).contiguous()
+    _need(sc.dtype == torch.float32 and sc.numel() == N, "scales [N] fp32")
+    ks = cu_seqlen_ks.to(torch.int32).contiguous()
+    ke = cu_seqlen_ke.to(torch.int32).contiguous()
+    out = torch.empty(M, N, dtype=torch.float32, device=q.device)
+    _lib.call("spmla_mqa_logits", q.data_ptr(), q.stride(0), q.stride(1), weights.data_ptr(), weights.stride(0),
+              codes.data_ptr(), codes.stride(0), sc.data_ptr(), N, ks.data_ptr(), ke.data_ptr(), M, H, D,
+              out.data_ptr(), out.stride(0), _stream(q))
+    return out
+
+
 # ---------------------------------------------------------------------------------------------- indexer
 def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P=1, rank=0, noinf=False):
     """q [rows, 64, 128] bf16, w [rows, 64] fp32, store [blocks, rpb, 132] uint8, block_table [nreq, cols] int32,

@@ -300,6 +300,14 @@ int spmla_paged_mqa_logits(const void* q, long long q_st, long long q_sh, const 
                            const int* block_table, long long bt_st, const int* req, const int* ctx, int rows, int H,
                            int D, int Lc, int noinf, float* out, long long out_st, void* stream);
 
+/* Prefill indexer logits over gathered keys: out[m][n] = sum_h w[m][h] * relu(q[m][h] . kcode[n]) * kscale[n] for
+ * ks[m] <= n < ke[m], -inf for the other n < N (no clamp). Key n's 128 e4m3 codes at k + n * k_st bytes, its fp32
+ * scale kscale[n]. H = 64, D = 128, q bf16.
+ * Replaces mqa_logits_triton / _mqa_logits_kernel (dotsnote/engine/arcstats_pkg/arcstats/dsa_sm89.py:96-133). */
+int spmla_mqa_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st, const void* k,
+                     long long k_st, const float* kscale, int N, const int* ks, const int* ke, int M, int H, int D,
+                     float* out, long long out_st, void* stream);
+
 /* Top-k overlap of L layers' selections for n query rows: for layers a != b, hits[(a L + b) n + i] = number of valid
  * entries (>= 0) of layer b's row i that also occur in layer a's row i (symmetric for duplicate-free rows; the
  * diagonal is not written); nvalid[a n + i] = valid entries of layer a's row i. Entry k of layer l, row i at

@@ -54,6 +54,8 @@ PINS = {
                       "out element by element; shuffle_rows(shuffle_layout(x)) == x",
     "paged_mqa_logits": "index_logits (pinned above) on the unshuffled rows with the reader's context rule "
                         "(seq_len - (next_n - 1 - j), or the 2-D seq_lens entry) checked by hand; no clamp",
+    "mqa_logits": "index_logits (pinned above) on 132-byte rows built from the flat codes and scales, block size 1 and "
+                  "an identity block table, with positions below ks masked",
     "topk_overlap": "the reference's own statement (sort, searchsorted, gather-compare, torch) on random rows with "
                     "-1 padding; python set arithmetic on tiny rows; symmetry, hits <= min(|a|, |b|), identical rows "
                     "give |a|, disjoint rows give 0",
@@ -674,3 +676,19 @@ def paged_mqa_logits(q, cache, w, seq_lens, block_table, bs, max_model_len):
     req, ctx = paged_ctx(seq_lens, nn)
     return index_logits(q.reshape(B * nn, H, D), w, shuffle_rows(cache, bs), block_table, bs, req, ctx,
                         max_model_len, clamp=np.inf)
+
+
+def mqa_logits(q, codes, scales, w, ks, ke):
+    """mqa_logits_triton (dsa_sm89.py:97-133): q [M, H, D] values, codes [N, 128] e4m3, scales [N] fp32, w [M, H],
+    valid keys ks[m] <= n < ke[m] -> [M, N] float64, -inf elsewhere (no clamp)."""
+    q = np.asarray(q, dtype=np.float64)
+    w = np.asarray(w, dtype=np.float64)
+    M, N = q.shape[0], codes.shape[0]
+    kc = e4m3_decode(np.asarray(codes, dtype=np.uint8)).astype(np.float64)
+    sc = np.asarray(scales, dtype=np.float32).astype(np.float64)
+    out = np.full((M, N), -np.inf)
+    for m in range(M):
+        n = np.arange(max(0, int(ks[m])), min(N, int(ke[m])))
+        if n.size:
+            out[m, n] = (w[m] @ np.maximum(q[m] @ kc[n].T, 0.0)) * sc[n]
+    return out

@@ -83,3 +83,31 @@ def test_paged_logits_fp8_query(dev):
     b = kernels.paged_mqa_logits(q8.to(torch.bfloat16), cache, w, sl, bt, L)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_mqa_logits_flat(dev):
+    """Prefill logits over a flat key gather [N, 128] + scales [N] with per-row [ks, ke) ranges vs the oracle."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    N, M = 3000, 9
+    g = torch.Generator().manual_seed(6)
+    k = torch.randn(N, 128, generator=g).to(torch.bfloat16)
+    rows = np.zeros((N, 132), dtype=np.uint8)
+    ref.index_key_write(bf16_bits(k), np.arange(N), rows)
+    codes = torch.from_numpy(rows[:, :128].copy())
+    scales = torch.from_numpy(rows[:, 128:].copy().view(np.float32)[:, 0].copy())
+    q = torch.randn(M, 64, 128, generator=g).to(torch.bfloat16)
+    w = torch.rand(M, 64, generator=g)
+    ks = torch.tensor([0, 0, 100, 2999, 500, 1000, 0, 64, 2048], dtype=torch.int32)
+    ke = torch.tensor([3000, 1, 2100, 3000, 500, 2999, 257, 96, 3000], dtype=torch.int32)
+    print("[mqa logits] flat", flush=True)
+    out = kernels.mqa_logits(q.to(dev), (codes.to(dev).view(torch.float8_e4m3fn), scales.to(dev).view(N, 1)),
+                             w.to(dev), ks.to(dev), ke.to(dev))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    exp = ref.mqa_logits(q.float().numpy(), rows[:, :128], rows[:, 128:].copy().view(np.float32)[:, 0], w.numpy(),
+                         ks.numpy(), ke.numpy())
+    assert np.array_equal(np.isinf(got), np.isinf(exp))
+    fin = np.isfinite(exp)
+    err = np.abs(got[fin] - exp[fin]) / np.maximum(1.0, np.abs(exp[fin]))
+    print(f"[mqa logits] max rel err {err.max():.3e}", flush=True)
+    assert err.max() <= 2e-5

@@ -60,3 +60,27 @@ def test_paged_logits_unclamped_and_matches_row_store():
     assert np.array_equal(got, want)
     assert np.isinf(got[0, 49:]).all() and np.isfinite(got[0, :49]).all()      # row (b 0, j 0): ctx 49
     assert got[np.isfinite(got)].max() > 60000                                  # no clamp on this path
+
+
+def test_mqa_logits_oracle_vs_row_store():
+    """The flat prefill statement equals index_logits on 132-byte rows built from the same codes and scales (block
+    size 1, identity block table) with positions below ks masked."""
+    g = torch.Generator().manual_seed(4)
+    N, M = 50, 5
+    k = bf16_bits(torch.randn(N, 128, generator=g) * 2)
+    rows = np.zeros((N, 132), dtype=np.uint8)
+    ref.index_key_write(k, np.arange(N), rows)
+    codes, scales = rows[:, :128], rows[:, 128:].copy().view(np.float32)[:, 0]
+    q = torch.randn(M, 64, 128, generator=g).float().numpy()
+    w = torch.rand(M, 64, generator=g).numpy()
+    ks = np.array([0, 3, 10, 49, 20])
+    ke = np.array([50, 4, 30, 50, 20])
+    got = ref.mqa_logits(q, codes, scales, w, ks, ke)
+    want = ref.index_logits(q, w, rows, np.arange(N, dtype=np.int32)[None, :], 1, np.zeros(M, dtype=np.int64), ke, N,
+                            clamp=np.inf)
+    for m in range(M):
+        want[m, :ks[m]] = -np.inf
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+    fin = np.isfinite(want)                            # float64, summation order of different matrix shapes
+    assert np.allclose(got[fin], want[fin], rtol=1e-12, atol=0)
+    assert np.isinf(got[4]).all()                      # empty range
