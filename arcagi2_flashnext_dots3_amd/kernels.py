@@ -588,3 +588,28 @@ def topk_overlap(sets):
     _lib.call("spmla_topk_overlap", sets.data_ptr(), sets.stride(0), sets.stride(1), L, n, K, hits.data_ptr(),
               nvalid.data_ptr(), _stream(sets))
     return hits, nvalid
+
+
+def mtp_union(idx, ql=None, cu=None, R=None, nmax=None):
+    """The union of each request's MTP top-k rows with token masks: idx [T, topk] int32 rows, requests of ql tokens
+    (or boundaries cu [nreq + 1]) -> (u [nreq, nmax] int32 (-1 padded), mk [nreq, nmax] uint8, cnt [nreq] int32),
+    rows ordered by mask descending then first occurrence (the request-packed decode's row list)."""
+    T, topk = idx.shape
+    _need(idx.dtype == torch.int32 and idx.stride(1) == 1, "idx int32 [T, topk]")
+    _need(R is not None, "mtp_union: R (rows of the pool) is required")
+    if cu is not None:
+        cu = cu.to(torch.int32).contiguous()
+        nreq, ql_ = cu.shape[0] - 1, 0
+        gmax = 6
+    else:
+        _need(ql is not None and ql > 0, "mtp_union: ql or cu")
+        nreq, ql_ = (T + ql - 1) // ql, int(ql)
+        gmax = min(ql, 6)
+    if nmax is None:
+        nmax = max(1, gmax * topk)
+    u = torch.empty(nreq, nmax, dtype=torch.int32, device=idx.device)
+    mk = torch.zeros(nreq, nmax, dtype=torch.uint8, device=idx.device)
+    cnt = torch.empty(nreq, dtype=torch.int32, device=idx.device)
+    _lib.call("spmla_mtp_union", idx.data_ptr(), idx.stride(0), T, ql_, _ptr(cu), nreq, int(R), topk, nmax,
+              u.data_ptr(), mk.data_ptr(), cnt.data_ptr(), _stream(idx))
+    return u, mk, cnt

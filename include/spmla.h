@@ -308,6 +308,15 @@ int spmla_mqa_logits(const void* q, long long q_st, long long q_sh, const float*
                      long long k_st, const float* kscale, int N, const int* ks, const int* ke, int M, int H, int D,
                      float* out, long long out_st, void* stream);
 
+/* Request-packed MTP decode, the row list: for request r (tokens cu[r] .. cu[r + 1], or r * ql .. + ql clipped to
+ * T; at most the first 6 used), u[r][0 .. cnt[r]) = the distinct rows 0 <= row < R of those tokens' top-k lists
+ * (idx [T][topk], row stride idx_st), mk[r][i] = bit j set when token j selected row u[r][i]; ordered by mask
+ * descending, then by the position j * topk + k of the row's first occurrence; u[r][cnt .. nmax) = -1.
+ * nmax >= (tokens used) * topk, R < 2^26 - 1, topk <= 2048.
+ * Replaces pk_union_kernel (dotsnote/engine/arcstats_pkg/arcstats/csrc/offload_attn.cu:586-698, ARC_OFFLOAD_CUDA_PK). */
+int spmla_mtp_union(const int* idx, long long idx_st, int T, int ql, const int* cu, int nreq, long long R, int topk,
+                    int nmax, int* u, unsigned char* mk, int* cnt, void* stream);
+
 /* Top-k overlap of L layers' selections for n query rows: for layers a != b, hits[(a L + b) n + i] = number of valid
  * entries (>= 0) of layer b's row i that also occur in layer a's row i (symmetric for duplicate-free rows; the
  * diagonal is not written); nvalid[a n + i] = valid entries of layer a's row i. Entry k of layer l, row i at

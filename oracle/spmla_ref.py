@@ -56,6 +56,8 @@ PINS = {
                         "(seq_len - (next_n - 1 - j), or the 2-D seq_lens entry) checked by hand; no clamp",
     "mqa_logits": "index_logits (pinned above) on 132-byte rows built from the flat codes and scales, block size 1 and "
                   "an identity block table, with positions below ks masked",
+    "mtp_union": "python sets on tiny requests (every selected valid row exactly once, its mask = the tokens whose "
+                 "list holds it); the order checked by its definition (mask descending, then first position)",
     "topk_overlap": "the reference's own statement (sort, searchsorted, gather-compare, torch) on random rows with "
                     "-1 padding; python set arithmetic on tiny rows; symmetry, hits <= min(|a|, |b|), identical rows "
                     "give |a|, disjoint rows give 0",
@@ -692,3 +694,32 @@ def mqa_logits(q, codes, scales, w, ks, ke):
         if n.size:
             out[m, n] = (w[m] @ np.maximum(q[m] @ kc[n].T, 0.0)) * sc[n]
     return out
+
+
+def mtp_union(idx, T, ql, cu, nreq, R, nmax, gmax=6):
+    """The request's union of MTP top-k rows (dotsnote/engine/arcstats_pkg/arcstats/csrc/offload_attn.cu:586-698):
+    for request r, tokens t0 .. t0 + G - 1 (G = min(t1 - t0, 6)), entries at position j * topk + k; each valid row
+    (0 <= row < R) once, with mask = OR of 1 << j over the tokens j that selected it, ordered by mask descending
+    then by the position of its first occurrence. Returns (u [nreq, nmax] int (-1 padded), mk [nreq, nmax] uint8
+    (0 where padded), cnt [nreq])."""
+    idx = np.asarray(idx)
+    topk = idx.shape[1]
+    u = np.full((nreq, nmax), -1, dtype=np.int64)
+    mk = np.zeros((nreq, nmax), dtype=np.uint8)
+    cnt = np.zeros(nreq, dtype=np.int64)
+    for r in range(nreq):
+        t0 = int(cu[r]) if cu is not None else min(r * ql, T)
+        t1 = int(cu[r + 1]) if cu is not None else min(t0 + ql, T)
+        G = min(max(t1 - t0, 0), gmax)
+        mask, first = {}, {}
+        for j in range(G):
+            for k in range(topk):
+                h = int(idx[t0 + j, k])
+                if 0 <= h < R:
+                    mask[h] = mask.get(h, 0) | (1 << j)
+                    first.setdefault(h, j * topk + k)
+        order = sorted(mask, key=lambda h: (-mask[h], first[h]))
+        cnt[r] = len(order)
+        u[r, :len(order)] = order
+        mk[r, :len(order)] = [mask[h] for h in order]
+    return u, mk, cnt
