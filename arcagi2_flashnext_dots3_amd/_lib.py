@@ -49,6 +49,7 @@ SIGNATURES = {
     "spmla_mla_query": [P, LL, LL, P, LL, LL, P, P, I, I, P, LL, LL, P],
     "spmla_topk_overlap": [P, LL, LL, I, I, I, P, P, P],
     "spmla_mtp_union": [P, LL, I, I, P, I, LL, I, I, P, P, P, P],
+    "spmla_attn_packed": [P, LL, LL, P, LL, P, P, P, I, P, I, I, I, I, I, F, F, I, P, LL, LL, P, LL, P, P, P],
     "spmla_index_key_write_shuffle": [P, LL, P, I, P, LL, I, LL, I, P],
     "spmla_mqa_logits": [P, LL, LL, P, LL, P, LL, P, I, P, P, I, I, I, P, LL, P],
     "spmla_paged_mqa_logits": [P, LL, LL, P, LL, P, LL, I, LL, P, LL, P, P, I, I, I, I, I, P, LL, P],

@@ -132,6 +132,11 @@ struct Params {
   // optional prior partial merged into the bf16 output (S == 1): normalized fp32 o and natural-log lse
   const float* prior_o; long long po_st, po_sh;
   const float* prior_lse; long long pl_st;
+  // request-packed MTP decode (attn_kernel<true>): work item t is a request; its rows are its union list (idx = u,
+  // idx_st = nmax, kcount = union sizes) and mk[t * idx_st + i] is row i's token mask. Column c of a workgroup is
+  // token t0 + (c >> (5 - tsh)) (t0 = cu[t] or t * ql) and head hg * (32 >> tsh) + c % (32 >> tsh); a column's
+  // softmax keeps the rows its token selected. T = total tokens (output rows), NR = requests.
+  const uint8_t* mk; const int* cu; int ql, tsh, NR;
 };
 
 // Copy one tile (32 rows: codes + scales) into the wave's buffer and load the rows' rope into VGPRs.
@@ -152,17 +157,29 @@ __device__ inline void issue_tile(const uint8_t* __restrict__ pool, const SPMLA_
   for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(src + ROPE_OFF + ks * 32 + h * 16);
 }
 
+template <bool PK>
 __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_generic[];
   SPMLA_LDS uint8_t* lds = (SPMLA_LDS uint8_t*)smem_generic;
 
-  const int nwork = p.T * p.S * p.HGN;
+  const int nwork = (PK ? p.NR : p.T) * p.S * p.HGN;
   const int f = remap_xcd(blockIdx.x, nwork);
   if (f < 0) return;
   const int hg = f % p.HGN;
   const int ts = f / p.HGN;
   const int s = ts % p.S;
   const int t = ts / p.S;
+  // columns -> (token, head): 32 heads of token t, or (packed) 2^tsh tokens of request t x (32 >> tsh) heads
+  int t0 = t, ntok = 1;
+  if (PK) {
+    t0 = p.cu ? p.cu[t] : min(t * p.ql, p.T);
+    const int t1 = p.cu ? p.cu[t + 1] : min(t0 + p.ql, p.T);
+    ntok = min(max(t1 - t0, 0), min(1 << p.tsh, 6));
+  }
+  const int csh = PK ? 5 - p.tsh : 5;          // log2 heads per token in a workgroup
+  auto col_tok = [&](int c) -> int { return PK ? t0 + (c >> csh) : t; };
+  auto col_head = [&](int c) -> int { return PK ? (hg << csh) + (c & ((1 << csh) - 1)) : hg * HG + c; };
+  auto col_ok = [&](int c) -> bool { return (!PK || (c >> csh) < ntok) && col_head(c) < p.H; };
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control flow
@@ -182,8 +199,15 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   // that go to LDS; (2) the first tile's copy, its rope and the latent query fragments (in flight while the query
   // staging is written). Row ids of later tiles are loaded one tile ahead, into registers.
   const int* idxrow = p.idx + (long long)t * p.idx_st + kb;
-  const int h = hg * HG + l32;
-  const bool hval = h < p.H;
+  const int h = col_head(l32);
+  const bool hval = col_ok(l32);
+  const uint8_t* mkrow = PK ? p.mk + (long long)t * p.idx_st + kb : nullptr;
+  auto mk_raw = [&](int tile) -> uint32_t {   // token mask of this lane's row in `tile` (packed decode)
+    const int i = tile * TR + l32;
+    uint32_t m = 0u;
+    if (PK && i < nrow) m = mkrow[i];
+    return m;
+  };
   auto row_raw = [&](int tile) -> int {       // index entry of this lane's row in `tile` (-1: past the end)
     const int i = tile * TR + l32;
     int x = -1;
@@ -193,13 +217,14 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   auto row_ok = [&](int x) -> int { return (x >= 0 && (long long)x < p.R) ? x : -1; };   // -1: none / invalid
   int rcur = row_ok(row_raw(w)), rnxt = row_ok(row_raw(w + NW));
   int rnn = -1;                        // raw entry two tiles ahead: loaded in one iteration, checked in the next
+  uint32_t mcur = mk_raw(w), mnxt = mk_raw(w + NW), mnn = 0u;
   {
     u32x4 qv[HG * QPIECES / 256];
 #pragma unroll
     for (int k = 0; k < HG * QPIECES / 256; ++k) {          // 32 heads x 40 pieces (rope, latent groups 2, 3)
       const int i = tid + 256 * k, qh = i / QPIECES, part = i % QPIECES;
-      const bool ok = hg * HG + qh < p.H;
-      const uint16_t* qsrc = p.q + (long long)t * p.q_st + (long long)(ok ? hg * HG + qh : 0) * p.q_sh;
+      const bool ok = col_ok(qh);
+      const uint16_t* qsrc = p.q + (long long)(ok ? col_tok(qh) : 0) * p.q_st + (long long)(ok ? col_head(qh) : 0) * p.q_sh;
       const uint16_t* src = part < 8 ? qsrc + D_LAT + part * 8 : qsrc + 2 * QGROUP + (part - 8) * 8;
       qv[k] = *(const u32x4*)src & (ok ? 0xffffffffu : 0u);
     }
@@ -225,7 +250,7 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   // latent query fragments of groups 0, 1 (bf16 B operands), k-pair kp (32 dims = chunks 2kp, 2kp + 1): lane half
   // h holds the dims of chunk 2kp + h; MFMA 2kp + e uses its bytes 8e .. 8e + 7 (the K operand is read the same
   // way). They are waited for with the first tile.
-  const uint16_t* qrow = p.q + (long long)t * p.q_st + (long long)(hval ? h : 0) * p.q_sh;
+  const uint16_t* qrow = p.q + (long long)(hval ? col_tok(l32) : 0) * p.q_st + (long long)(hval ? h : 0) * p.q_sh;
   bf16x8 qf[16];
   const uint32_t qmask = hval ? 0xffffffffu : 0u;       // heads past H: zero query (row 0 is read instead)
 #pragma unroll
@@ -268,8 +293,9 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     const bool more = j + 1 < ntw;
     // the entries loaded one iteration ago are checked only now, after the wait above: checking them where they
     // are loaded would stall every tile on a global-memory round trip
-    if (j > 0) rnxt = row_ok(rnn);
+    if (j > 0) { rnxt = row_ok(rnn); mnxt = mnn; }
     rnn = j + 2 < ntw ? row_raw(tix + 2 * NW) : -1;
+    if (PK) mnn = j + 2 < ntw ? mk_raw(tix + 2 * NW) : 0u;
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- rope part of S^T (operands in VGPRs / LDS)
@@ -348,9 +374,18 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- rows that do not exist: -inf (C-layout row of value i: 8 (i / 4) + 4 half + i % 4)
-    if (__builtin_expect(vmask != 0xffffffffu, 0)) {     // rare: keep it a branch, not 48 selects per tile
+    unsigned rm = vmask;                                 // rows of the tile this lane's column may use
+    if (PK) {                                            // its token's rows (padding tokens: every row)
+      const int ct = l32 >> csh;
+      for (int jt = 0; jt < ntok; ++jt) {
+        const unsigned bj = (unsigned)__ballot(rcur >= 0 && ((mcur >> jt) & 1u));
+        if (ct == jt) rm = bj;
+      }
+    }
+    const bool anymask = PK ? __ballot(rm != 0xffffffffu) != 0ull : vmask != 0xffffffffu;
+    if (__builtin_expect(anymask, 0)) {                  // rare: keep it a branch, not 48 selects per tile
       asm volatile("" ::: "memory");
-      const unsigned lm = vmask >> (4 * half);
+      const unsigned lm = rm >> (4 * half);
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         if (!((lm >> (8 * (i >> 2) + (i & 3))) & 1u)) S[i] = -__builtin_inff();
@@ -421,6 +456,7 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
       }
     }
     rcur = rnxt;
+    mcur = mnxt;
   }
 
   // ---- merge the 4 waves: per head M = max m_w, L = sum l_w 2^(m_w - M), O = sum O_w 2^(m_w - M) / L
@@ -463,8 +499,9 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
 
   SPMLA_LDS f32x4* xo = (SPMLA_LDS f32x4*)(lds + L_TILES);   // [wave][tile 0..7][qd][lane]
   // output head of this lane, recomputed from the lane id (cheaper than keeping it live across the loop)
-  const int ho = hg * HG + (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31);
-  const bool hoval = ho < p.H;
+  const int oc = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31);
+  const int ho = col_head(oc), to = col_tok(oc);
+  const bool hoval = col_ok(oc);
 #pragma unroll
   for (int rnd = 0; rnd < 2; ++rnd) {
 #pragma unroll
@@ -497,10 +534,10 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
             for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(x[e], wp, acc[e]);
           }
           if (p.opart == nullptr) {
-            uint16_t* orow = p.out + (long long)t * p.o_st + (long long)ho * p.o_sh;
+            uint16_t* orow = p.out + (long long)to * p.o_st + (long long)ho * p.o_sh;
             *(uint2*)(orow + col) = make_uint2(pk_bf16(acc[0], acc[1]), pk_bf16(acc[2], acc[3]));
           } else {
-            float* orow = p.opart + (((long long)s * p.T + t) * p.H + ho) * D_LAT;
+            float* orow = p.opart + (((long long)s * p.T + to) * p.H + ho) * D_LAT;
             *(f32x4*)(orow + col) = acc;
           }
         }
@@ -509,8 +546,8 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     lds_barrier();
   }
   if (w == 0 && half == 0 && hoval) {
-    if (p.opart == nullptr) p.lse[(long long)t * p.lse_st + ho] = lse_v;
-    else p.lsepart[((long long)s * p.T + t) * p.H + ho] = lse_v;
+    if (p.opart == nullptr) p.lse[(long long)to * p.lse_st + ho] = lse_v;
+    else p.lsepart[((long long)s * p.T + to) * p.H + ho] = lse_v;
   }
 }
 
@@ -605,17 +642,57 @@ static int attn_launch(const void* q, long long q_st, long long q_sh, const void
   p.out = (uint16_t*)out; p.o_st = o_st; p.o_sh = o_sh; p.lse = lse; p.lse_st = lse_st;
   p.opart = f32part ? opart : nullptr; p.lsepart = lsepart;
   p.prior_o = prior_o; p.po_st = po_st; p.po_sh = po_sh; p.prior_lse = prior_lse; p.pl_st = pl_st;
+  p.mk = nullptr; p.cu = nullptr; p.ql = 1; p.tsh = 0; p.NR = T;
   const long long nwork = (long long)T * S * p.HGN;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)attn::attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       attn::L_TOTAL);
+    hipError_t e = hipFuncSetAttribute((const void*)attn::attn_kernel<false>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, attn::L_TOTAL);
     if (e != hipSuccess) return (int)e;
     attr = true;
   }
-  hipLaunchKernelGGL(attn::attn_kernel, dim3(grid), dim3(256), attn::L_TOTAL, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(attn::attn_kernel<false>, dim3(grid), dim3(256), attn::L_TOTAL, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}
+
+int spmla_attn_packed(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* u,
+                      const unsigned char* mk, const int* cnt, int nmax, const int* cu, int ql, int nreq, int T,
+                      int H, int tpg, float sm_scale, float kv_scale, int S, void* out, long long o_st,
+                      long long o_sh, float* lse, long long lse_st, float* opart, float* lsepart, void* stream) {
+  if (T < 0 || nreq < 0 || H <= 0 || nmax < 0 || S <= 0 || R < 0 || (!cu && ql <= 0)) return SPMLA_EARG;
+  if (tpg != 1 && tpg != 2 && tpg != 4 && tpg != 8) return SPMLA_EARG;
+  if (T == 0 || nreq == 0) return SPMLA_OK;
+  if (!q || !u || !mk || !cnt || (R > 0 && !pool)) return SPMLA_EARG;
+  const bool f32part = opart != nullptr;
+  if (f32part ? !lsepart : (S != 1 || !out || !lse)) return SPMLA_EARG;
+  if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)pool & 15)) return SPMLA_EALIGN;
+  if (out && (((uintptr_t)out & 7) || (o_st & 3) || (o_sh & 3))) return SPMLA_EALIGN;
+  attn::Params p;
+  p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh;
+  p.pool = (const uint8_t*)pool; p.R = R;
+  p.idx = u; p.idx_st = nmax; p.K = nmax; p.kcount = cnt;
+  p.T = T; p.H = H; p.S = S;
+  p.tsh = tpg == 1 ? 0 : (tpg == 2 ? 1 : (tpg == 4 ? 2 : 3));
+  p.HGN = (H + (attn::HG >> p.tsh) - 1) / (attn::HG >> p.tsh);
+  p.c = sm_scale * kv_scale * 1.4426950408889634f;
+  p.kv_scale = kv_scale;
+  p.out = (uint16_t*)out; p.o_st = o_st; p.o_sh = o_sh; p.lse = lse; p.lse_st = lse_st;
+  p.opart = f32part ? opart : nullptr; p.lsepart = lsepart;
+  p.prior_o = nullptr; p.po_st = p.po_sh = 0; p.prior_lse = nullptr; p.pl_st = 0;
+  p.mk = (const uint8_t*)mk; p.cu = cu; p.ql = ql; p.NR = nreq;
+  const long long nwork = (long long)nreq * S * p.HGN;
+  if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
+  const int grid = (int)((nwork + 7) / 8 * 8);
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)attn::attn_kernel<true>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, attn::L_TOTAL);
+    if (e != hipSuccess) return (int)e;
+    attr = true;
+  }
+  hipLaunchKernelGGL(attn::attn_kernel<true>, dim3(grid), dim3(256), attn::L_TOTAL, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 

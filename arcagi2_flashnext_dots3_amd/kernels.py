@@ -613,3 +613,38 @@ def mtp_union(idx, ql=None, cu=None, R=None, nmax=None):
     _lib.call("spmla_mtp_union", idx.data_ptr(), idx.stride(0), T, ql_, _ptr(cu), nreq, int(R), topk, nmax,
               u.data_ptr(), mk.data_ptr(), cnt.data_ptr(), _stream(idx))
     return u, mk, cnt
+
+
+def attend_packed(q, pool, idx, sm_scale, kv_scale=1.0, ql=None, cu=None, out=None, lse=None, split=1, tpg=None,
+                  union=None):
+    """Request-packed MTP decode (the reference's ARC_OFFLOAD_CUDA_PK path): the tokens of a request (ql tokens each,
+    or boundaries cu) attend over the union of their top-k rows (mtp_union), each union row loaded and converted once
+    per request and head group, each token's softmax kept to its own rows. Same result as attend per token up to the
+    fp32 summation order. q [T, H, 576] bf16, pool Row656 rows, idx [T, K] int32 -> (out [T, H, 512] bf16, lse)."""
+    T, H, _ = q.shape
+    _need(attention_ok(q, idx), "attend_packed: q must be bf16 [T, H, 576] with 16-byte aligned rows, idx int32")
+    R = int(pool.shape[0])
+    u, mk, cnt = union if union is not None else mtp_union(idx, ql=ql, cu=cu, R=R)
+    nreq, nmax = u.shape
+    if tpg is None:
+        g = min(int(ql), 6) if cu is None else 6
+        tpg = 1 if g <= 1 else (2 if g <= 2 else (4 if g <= 4 else 8))
+    if out is None:
+        out = torch.empty(T, H, D_LAT, dtype=torch.bfloat16, device=q.device)
+    if lse is None:
+        lse = torch.empty(T, H, dtype=torch.float32, device=q.device)
+    cu_t = cu.to(torch.int32).contiguous() if cu is not None else None
+    st = _stream(q)
+    if split == 1:
+        _lib.call("spmla_attn_packed", q.data_ptr(), q.stride(0), q.stride(1), pool.data_ptr(), R, u.data_ptr(),
+                  mk.data_ptr(), cnt.data_ptr(), nmax, _ptr(cu_t), int(ql or 0), nreq, T, H, tpg, float(sm_scale),
+                  float(kv_scale), 1, out.data_ptr(), out.stride(0), out.stride(1), lse.data_ptr(), lse.stride(0),
+                  None, None, st)
+        return out, lse
+    opart = torch.empty(split, T, H, D_LAT, dtype=torch.float32, device=q.device)
+    lpart = torch.empty(split, T, H, dtype=torch.float32, device=q.device)
+    _lib.call("spmla_attn_packed", q.data_ptr(), q.stride(0), q.stride(1), pool.data_ptr(), R, u.data_ptr(),
+              mk.data_ptr(), cnt.data_ptr(), nmax, _ptr(cu_t), int(ql or 0), nreq, T, H, tpg, float(sm_scale),
+              float(kv_scale), split, None, 0, 0, None, 0, opart.data_ptr(), lpart.data_ptr(), st)
+    lse_merge(opart, lpart, out=out, lse=lse)
+    return out, lse

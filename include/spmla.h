@@ -317,6 +317,18 @@ int spmla_mqa_logits(const void* q, long long q_st, long long q_sh, const float*
 int spmla_mtp_union(const int* idx, long long idx_st, int T, int ql, const int* cu, int nreq, long long R, int topk,
                     int nmax, int* u, unsigned char* mk, int* cnt, void* stream);
 
+/* Request-packed MTP decode attention over the union rows of spmla_mtp_union (u, mk, cnt; row capacity nmax): a
+ * workgroup's 32 query columns are tpg (1, 2, 4, 8) tokens of one request x 32 / tpg heads, so each union row is
+ * loaded and converted once for all of them; a column's softmax uses only the rows its token's mask holds. Request
+ * r = tokens cu[r] .. cu[r + 1] (or r * ql .. + ql clipped to T), the first min(tpg, 6) of them computed. Results
+ * and outputs as spmla_attn_splitk for each token (S splits of the union with fp32 partials, or S = 1 with the
+ * bf16 out + lse), up to the fp32 summation order of the rows.
+ * Replaces pk_attn_kernel (dotsnote/engine/arcstats_pkg/arcstats/csrc/offload_attn.cu:700-1153). */
+int spmla_attn_packed(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* u,
+                      const unsigned char* mk, const int* cnt, int nmax, const int* cu, int ql, int nreq, int T,
+                      int H, int tpg, float sm_scale, float kv_scale, int S, void* out, long long o_st,
+                      long long o_sh, float* lse, long long lse_st, float* opart, float* lsepart, void* stream);
+
 /* Top-k overlap of L layers' selections for n query rows: for layers a != b, hits[(a L + b) n + i] = number of valid
  * entries (>= 0) of layer b's row i that also occur in layer a's row i (symmetric for duplicate-free rows; the
  * diagonal is not written); nvalid[a n + i] = valid entries of layer a's row i. Entry k of layer l, row i at

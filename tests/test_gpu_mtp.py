@@ -46,3 +46,66 @@ def test_mtp_union_boundaries(dev):
     torch.cuda.synchronize()
     eu, emk, ecnt = ref.mtp_union(idx, T, None, cu, 3, R, nmax=u.shape[1])
     assert np.array_equal(cnt.cpu().numpy(), ecnt) and np.array_equal(u.cpu().numpy(), eu)
+
+
+def _mtp_inputs(B, ql, H, R, K, shared, seed):
+    from tests.helpers import make_pool_656, make_q
+    g = np.random.default_rng(seed)
+    T = B * ql
+    idx = np.empty((T, K), dtype=np.int32)
+    for b in range(B):
+        base = g.choice(R, K, replace=False)
+        for t in range(b * ql, (b + 1) * ql):
+            own = g.choice(R, K, replace=False)
+            row = np.where(g.random(K) < shared, base, own)
+            _, first = np.unique(row, return_index=True)
+            keep = np.zeros(K, bool)
+            keep[first] = True
+            idx[t] = np.where(keep, row, -1)
+    pool, _, _ = make_pool_656(R, seed=seed + 1)
+    return torch.from_numpy(idx), pool, make_q(T, H, seed=seed + 2)
+
+
+@pytest.mark.parametrize("B,ql,H,K,shared,split", [(4, 4, 128, 1024, 0.8, 1), (3, 3, 64, 512, 0.5, 1),
+                                                   (2, 2, 128, 2048, 0.9, 2), (5, 1, 32, 256, 0.0, 1)])
+def test_attend_packed_vs_oracle_and_per_token(dev, B, ql, H, K, shared, split):
+    from arcagi2_flashnext_dots3_amd import kernels
+    R = 8192
+    idx, pool, q = _mtp_inputs(B, ql, H, R, K, shared, seed=K + ql)
+    idx[0, :7] = R + 3                                                  # invalid rows
+    sm = 192 ** -0.5
+    print(f"[packed] B={B} ql={ql} H={H} K={K} split={split}", flush=True)
+    pd = torch.from_numpy(pool).to(dev)
+    out, lse = kernels.attend_packed(q.to(dev), pd, idx.to(dev), sm, ql=ql, split=split)
+    o1, l1 = kernels.attend(q.to(dev), pd, idx.to(dev), sm)
+    torch.cuda.synchronize()
+    o_ref, l_ref = ref.attention(q.float().numpy(), pool, idx.numpy(), sm)
+    o = out.float().cpu().numpy()
+    l = lse.cpu().numpy()
+    err_o = (np.abs(o - o_ref) / np.maximum(1.0, np.abs(o_ref))).max()
+    err_l = np.abs(l - l_ref).max()
+    print(f"[packed] vs oracle {err_o:.3e} {err_l:.3e}", flush=True)
+    assert err_o <= 1e-2 and err_l <= 1e-3
+    d = ((out.float() - o1.float()).abs() / o1.float().abs().clamp_min(1.0)).max()
+    assert float(d) <= 1e-2 and float((lse - l1).abs().max()) <= 1e-4
+
+
+def test_attend_packed_variable_requests(dev):
+    """cu boundaries: requests of 3, 1, 0 and 7 tokens (the first 6 of the last computed, the 7th left untouched)."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    H, R, K = 64, 4096, 512
+    idx, pool, q = _mtp_inputs(1, 11, H, R, K, 0.7, seed=5)
+    cu = torch.tensor([0, 3, 4, 4, 11], dtype=torch.int32)
+    sm = 192 ** -0.5
+    pd = torch.from_numpy(pool).to(dev)
+    out = torch.full((11, H, 512), 7.0, dtype=torch.bfloat16, device=dev)
+    lse = torch.full((11, H), 7.0, dtype=torch.float32, device=dev)
+    kernels.attend_packed(q.to(dev), pd, idx.to(dev), sm, cu=cu.to(dev), out=out, lse=lse)
+    torch.cuda.synchronize()
+    o_ref, l_ref = ref.attention(q.float().numpy(), pool, idx.numpy(), sm)
+    o = out.float().cpu().numpy()
+    l = lse.cpu().numpy()
+    done = [0, 1, 2, 3, 4, 5, 6, 7, 8, 9]
+    assert (np.abs(o[done] - o_ref[done]) / np.maximum(1.0, np.abs(o_ref[done]))).max() <= 1e-2
+    assert np.abs(l[done] - l_ref[done]).max() <= 1e-3
+    assert bool((out[10] == 7.0).all()) and bool((lse[10] == 7.0).all())
