@@ -78,6 +78,17 @@ def test_version():
     (("spmla_index_logits", None, 0, 0, None, 0, None, 0, 64, 0, None, 0, 64, None, None, 1, 32, 128, 10, 1, 0, 0,
       None, 0, None), -5),
     (("spmla_lse_merge", None, 0, 0, 0, 0, None, 0, 0, 0, 1, 1, None, 0, 0, None, None, 0, None), -2),
+    # (pointer 256 below: a placeholder that the argument checks reject before anything is launched)
+    (("spmla_topk_overlap", 256, 0, 0, 1, 1, 4096, 256, 256, None), -5),
+    (("spmla_topk_overlap", 256, 0, 0, 0, 1, 8, 256, 256, None), -2),
+    (("spmla_index_key_write_shuffle", None, 0, None, 1, None, 4, 24, 0, 0, None), -2),
+    (("spmla_paged_mqa_logits", None, 0, 0, None, 0, None, 4, 64, 8448, None, 0, None, None, 1, 32, 128, 10, 0, None,
+      0, None), -5),
+    (("spmla_mqa_logits", 256, 8, 8, 256, 64, 256, 64, 256, 5, 256, 256, 1, 64, 128, 256, 5, None), -3),
+    (("spmla_mtp_union", 256, 8, 4, 4, None, 1, 100, 8, 16, 256, 256, 256, None), -2),
+    (("spmla_mtp_union", 256, 8, 4, 4, None, 1, 1 << 26, 8, 32, 256, 256, 256, None), -5),
+    (("spmla_attn_packed", None, 0, 0, None, 0, None, None, None, 0, None, 4, 1, 4, 128, 3, 1.0, 1.0, 1, None, 0, 0,
+      None, 0, None, None, None), -2),
 ])
 def test_argument_rejection(call, code):
     from arcagi2_flashnext_dots3_amd import _lib
