@@ -12,6 +12,12 @@
 //     rr[set]; misses beyond the set's unpinned ways go to spill rows (C + k, k < cap), past cap to the host (-2);
 //   * advance (in the resolve launch): rr[set] += min(tickets, W) (mod W);
 //   * resolve: res[t][k] = the line (tag hit) or the miss's spill row / -2; invalid entries -1.
+//   * two-choice placement (option `two`; offload_fill.py:16-23, _set2 :136-138, P2 paths :158-165 and :269-279,
+//     _invalidate2_kernel :296-303): row h may also live in a second set ((h * 2654435761) >> 12) % S. Lookups check
+//     it for entries that miss the first set (a hit there pins that line); a miss that finds no unpinned way for its
+//     ticket in the first set takes a ticket in the second before it spills; invalidation clears both sets. Tickets of
+//     both kinds share the set's counter, so the ways one step hands out in a set stay distinct and rr advances by
+//     min(tickets, W) as before. A row is cached in at most one of its sets (only a miss in both places it).
 // Which ways the misses of one set take, and which misses of an overfull set spill, follow the order of the atomics;
 // the rows an entry resolves to always hold that entry's host row.
 //
@@ -35,7 +41,13 @@ struct Cache {
   int* claim; int* rdst;                              // per host row: last epoch it missed, its pool row then
   long long* ml; long long* mdst;                     // miss list: row, its destination row
   int* state; int cap;
+  int two;                                            // two-choice placement
 };
+
+// the second candidate set of host row h (0 <= h < 2^31, so the product fits 63 bits)
+__device__ inline int set2_of(long long h, int S) {
+  return (int)((((unsigned long long)h * 2654435761ull) >> 12) % (unsigned long long)S);
+}
 
 __global__ void begin_kernel(int* state) {
   state[ST_EPOCH] = state[ST_EPOCH] + 1;
@@ -68,6 +80,7 @@ __global__ void __launch_bounds__(SCAN_TPB) scan_kernel(const int* __restrict__ 
   int line = -1;
   if (valid) {
     line = find_way(c, h, (int)(h % c.S));
+    if (line < 0 && c.two) line = find_way(c, h, set2_of(h, c.S));
     if (line >= 0) c.pin[line] = epoch;
   }
   // distinct misses: the entry that raises claim[h] to this epoch owns the row's miss
@@ -90,24 +103,29 @@ __global__ void __launch_bounds__(SCAN_TPB) scan_kernel(const int* __restrict__ 
   if (claimed) c.ml[mbase + wm[wv] + (int)__popcll(cb & ((1ull << lane) - 1ull))] = h;
 }
 
+// a ticket in set st: the ticket-th unpinned way counted round-robin from rr[st], or -2 past the set's unpinned ways
+__device__ inline long long take_way(const Cache& c, int st, int epoch) {
+  int ticket = atomicAdd(c.cnt + st, 1);
+  const int r0 = c.rr[st];
+  for (int j = 0; j < c.W; ++j) {
+    const int w = r0 + j < c.W ? r0 + j : r0 + j - c.W;
+    const int line = st * c.W + w;
+    if (c.pin[line] != epoch) {
+      if (ticket == 0) return line;
+      --ticket;
+    }
+  }
+  return -2;
+}
+
 // one thread per miss m < state[ST_MISS] (the launch covers every entry of the step)
 __global__ void __launch_bounds__(256) alloc_kernel(long long n, Cache c) {
   const long long m = (long long)blockIdx.x * 256 + threadIdx.x;
   if (m >= n || m >= c.state[ST_MISS]) return;
   const int epoch = c.state[ST_EPOCH];
   const long long h = c.ml[m];
-  const int st = (int)(h % c.S);
-  int ticket = atomicAdd(c.cnt + st, 1);
-  const int r0 = c.rr[st];
-  long long dst = -2;
-  for (int j = 0; j < c.W; ++j) {
-    const int w = r0 + j < c.W ? r0 + j : r0 + j - c.W;
-    const int line = st * c.W + w;
-    if (c.pin[line] != epoch) {
-      if (ticket == 0) { dst = line; break; }
-      --ticket;
-    }
-  }
+  long long dst = take_way(c, (int)(h % c.S), epoch);
+  if (dst < 0 && c.two) dst = take_way(c, set2_of(h, c.S), epoch);
   if (dst >= 0) {
     c.tag[dst] = (int)h;
   } else {
@@ -133,6 +151,7 @@ __global__ void __launch_bounds__(256) resolve_kernel(const int* __restrict__ id
   int r = -1;
   if (h >= 0 && h < R) {
     r = find_way(c, h, (int)(h % c.S));
+    if (r < 0 && c.two) r = find_way(c, h, set2_of(h, c.S));
     if (r < 0) r = c.rdst[h];                        // this step's miss: its line (tag found above) or spill / host
   }
   res[(long long)t * res_st + k] = r;
@@ -140,7 +159,7 @@ __global__ void __launch_bounds__(256) resolve_kernel(const int* __restrict__ id
 
 // a rewritten host row must not be served from a stale line (sparse_offload.py:782-789)
 __global__ void __launch_bounds__(256) invalidate_kernel(const long long* __restrict__ slots, int n, long long R,
-                                                         int* tag, int W, int S) {
+                                                         int* tag, int W, int S, int two) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   const long long h = slots[i];
@@ -148,6 +167,11 @@ __global__ void __launch_bounds__(256) invalidate_kernel(const long long* __rest
   int* tg = tag + (h % S) * W;
   for (int w = 0; w < W; ++w)
     if (tg[w] == (int)h) tg[w] = -1;
+  if (two) {
+    tg = tag + (long long)set2_of(h, S) * W;
+    for (int w = 0; w < W; ++w)
+      if (tg[w] == (int)h) tg[w] = -1;
+  }
 }
 
 // per token, two lists compacted in order and padded with -1, with counts per token:
@@ -227,23 +251,24 @@ extern "C" {
 
 static int wcache_setup(wc::Cache& c, const int* idx, int T, int K, long long R, int* tag, int C, int W, int* rr,
                         int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst,
-                        int* state, int cap) {
-  if (T < 0 || K < 0 || R < 0 || C <= 0 || W <= 0 || C % W || cap < 0) return SPMLA_EARG;
+                        int* state, int cap, int two) {
+  if (T < 0 || K < 0 || R < 0 || C <= 0 || W <= 0 || C % W || cap < 0 || (two != 0 && two != 1)) return SPMLA_EARG;
   if (R > 0x7fffffffll) return SPMLA_ELIMIT;
   const long long n = (long long)T * K;
   if (!tag || !rr || !cnt || !pin || !claim || !rdst || !miss_rows || !miss_dst || !state || (n > 0 && !idx))
     return SPMLA_EARG;
   c.tag = tag; c.C = C; c.W = W; c.S = C / W; c.rr = rr; c.cnt = cnt; c.pin = pin;
   c.claim = claim; c.rdst = rdst; c.ml = miss_rows; c.mdst = miss_dst;
-  c.state = state; c.cap = cap;
+  c.state = state; c.cap = cap; c.two = two;
   return SPMLA_OK;
 }
 
 int spmla_wcache_place(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
                        int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst, int* state,
-                       int cap, void* stream) {
+                       int cap, int two, void* stream) {
   wc::Cache c;
-  const int e = wcache_setup(c, idx, T, K, R, tag, C, W, rr, cnt, pin, claim, rdst, miss_rows, miss_dst, state, cap);
+  const int e =
+      wcache_setup(c, idx, T, K, R, tag, C, W, rr, cnt, pin, claim, rdst, miss_rows, miss_dst, state, cap, two);
   if (e) return e;
   hipStream_t s = (hipStream_t)stream;
   const long long n = (long long)T * K;
@@ -258,9 +283,10 @@ int spmla_wcache_place(const int* idx, long long idx_st, int T, int K, long long
 
 int spmla_wcache_resolve(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
                          int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst,
-                         int* state, int cap, int* res, long long res_st, void* stream) {
+                         int* state, int cap, int two, int* res, long long res_st, void* stream) {
   wc::Cache c;
-  const int e = wcache_setup(c, idx, T, K, R, tag, C, W, rr, cnt, pin, claim, rdst, miss_rows, miss_dst, state, cap);
+  const int e =
+      wcache_setup(c, idx, T, K, R, tag, C, W, rr, cnt, pin, claim, rdst, miss_rows, miss_dst, state, cap, two);
   if (e) return e;
   if (!res) return SPMLA_EARG;
   const long long n = (long long)T * K;
@@ -272,24 +298,26 @@ int spmla_wcache_resolve(const int* idx, long long idx_st, int T, int K, long lo
 
 int spmla_wcache_step(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
                       int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst, int* state,
-                      int cap, int* res, long long res_st, void* stream) {
+                      int cap, int two, int* res, long long res_st, void* stream) {
   wc::Cache c;                                        // validate everything before anything is launched
-  int e = wcache_setup(c, idx, T, K, R, tag, C, W, rr, cnt, pin, claim, rdst, miss_rows, miss_dst, state, cap);
+  int e =
+      wcache_setup(c, idx, T, K, R, tag, C, W, rr, cnt, pin, claim, rdst, miss_rows, miss_dst, state, cap, two);
   if (e) return e;
   if (!res) return SPMLA_EARG;
-  e = spmla_wcache_place(idx, idx_st, T, K, R, tag, C, W, rr, cnt, pin, claim, rdst, miss_rows, miss_dst,
-                                   state, cap, stream);
+  e = spmla_wcache_place(idx, idx_st, T, K, R, tag, C, W, rr, cnt, pin, claim, rdst, miss_rows, miss_dst, state,
+                         cap, two, stream);
   if (e) return e;
   return spmla_wcache_resolve(idx, idx_st, T, K, R, tag, C, W, rr, cnt, pin, claim, rdst, miss_rows, miss_dst, state,
-                              cap, res, res_st, stream);
+                              cap, two, res, res_st, stream);
 }
 
-int spmla_wcache_invalidate(const long long* slots, int n, long long R, int* tag, int C, int W, void* stream) {
-  if (n < 0 || R < 0 || C <= 0 || W <= 0 || C % W) return SPMLA_EARG;
+int spmla_wcache_invalidate(const long long* slots, int n, long long R, int* tag, int C, int W, int two,
+                            void* stream) {
+  if (n < 0 || R < 0 || C <= 0 || W <= 0 || C % W || (two != 0 && two != 1)) return SPMLA_EARG;
   if (n == 0) return SPMLA_OK;
   if (!slots || !tag) return SPMLA_EARG;
   hipLaunchKernelGGL(wc::invalidate_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, slots, n, R,
-                     tag, W, C / W);
+                     tag, W, C / W, two);
   return (int)hipGetLastError();
 }
 

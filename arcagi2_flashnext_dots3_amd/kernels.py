@@ -310,11 +310,13 @@ class RowCache:
     """Device state of a dynamic W-way HBM row cache (spmla_wcache_*): C lines in S = C / W sets plus `cap` spill rows,
     both in one Row656 pool [C + cap, 656] that the attention reads; tags, round-robin pointers, pins, and per host row
     the epoch of its last miss and that miss's pool row. Everything is zero-initialized once (tags -1); no buffer is
-    cleared between steps."""
+    cleared between steps. two=True: two-choice placement (a row may also live in a second, hashed set; every step
+    and invalidation of this cache then uses both sets)."""
 
-    def __init__(self, C, W, cap, device):
+    def __init__(self, C, W, cap, device, two=False):
         _need(C > 0 and W > 0 and C % W == 0 and cap >= 0, "RowCache: C a positive multiple of W, cap >= 0")
         self.C, self.W, self.S, self.cap = int(C), int(W), int(C) // int(W), int(cap)
+        self.two = bool(two)
         self.device = torch.device(device)
         i32 = dict(dtype=torch.int32, device=self.device)
         self.tag = torch.full((self.C,), -1, **i32)
@@ -337,10 +339,18 @@ class RowCache:
             self.mdst = torch.zeros(n, dtype=torch.int64, device=dev)
             self.n = n
 
+    def set2(self, rows):
+        """The second candidate set of each row (int64 tensor of rows >= 0) under two-choice placement."""
+        return ((rows.long() * 2654435761) >> 12) % self.S
+
     def lookup(self, rows):
         """bool per row id (int64 tensor): currently in a cache line (diagnostics; no kernel of its own)."""
-        st = (rows % self.S).long()
-        return (self.tag.view(self.S, self.W)[st] == rows[:, None].to(torch.int32)).any(1) & (rows >= 0)
+        tg = self.tag.view(self.S, self.W)
+        r32 = rows[:, None].to(torch.int32)
+        hit = (tg[(rows % self.S).long()] == r32).any(1)
+        if self.two:
+            hit |= (tg[self.set2(rows)] == r32).any(1)
+        return hit & (rows >= 0)
 
 
 def wcache_step(cache, idx, R, res=None):
@@ -359,7 +369,7 @@ def _wc_args(cache, idx, R):
     T, K = idx.shape
     return (idx.data_ptr(), idx.stride(0), T, K, int(R), cache.tag.data_ptr(), cache.C, cache.W, cache.rr.data_ptr(),
             cache.cnt.data_ptr(), cache.pin.data_ptr(), cache.claim.data_ptr(), cache.rdst.data_ptr(),
-            cache.ml.data_ptr(), cache.mdst.data_ptr(), cache.state.data_ptr(), cache.cap)
+            cache.ml.data_ptr(), cache.mdst.data_ptr(), cache.state.data_ptr(), cache.cap, int(cache.two))
 
 
 def wcache_place(cache, idx, R):
@@ -390,7 +400,7 @@ def wcache_fill(cache, host, R, host_fmt, n):
 def wcache_invalidate(cache, slots, R):
     _need(slots.dtype == torch.int64, "slots int64")
     _lib.call("spmla_wcache_invalidate", slots.data_ptr(), slots.shape[0], int(R), cache.tag.data_ptr(), cache.C,
-              cache.W, _stream(slots))
+              cache.W, int(cache.two), _stream(slots))
 
 
 def split_res(idx, res, hbm=None, hbm_cnt=None, host=None, host_cnt=None):

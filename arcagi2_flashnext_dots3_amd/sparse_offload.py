@@ -47,11 +47,13 @@ class LayerOffload:
     `spill_rows` HBM rows for misses that find no free way; a step with more entries than spill rows can leave rows on
     the host, which then take the host tier). overlap_fill (ways): attend over the step's hits on a second stream while
     the misses are copied in, then over the fresh rows with the hits' partial merged in the epilogue; False: one
-    attention over the whole step after the copy (bit-identical to attending the gathered rows).
+    attention over the whole step after the copy (bit-identical to attending the gathered rows). two_choice (ways):
+    the reference's two-choice set placement (ARC_OFFLOAD_TWO_CHOICE, offload_fill.py:16-23): a missing row whose set
+    has no free way takes one in a second, hashed set before it spills; lookups and invalidations cover both sets.
     """
 
     def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
-                 spill_rows=131072, overlap_fill=True):
+                 spill_rows=131072, overlap_fill=True, two_choice=False):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         if cache_mode not in ("static", "ways"):
@@ -73,7 +75,7 @@ class LayerOffload:
         if cache_mode == "ways":
             if self.C <= 0 or self.C % int(ways):
                 raise ValueError("cache_mode='ways' needs cache_rows a positive multiple of ways")
-            self.wc = kernels.RowCache(self.C, int(ways), int(spill_rows), self.device)
+            self.wc = kernels.RowCache(self.C, int(ways), int(spill_rows), self.device, two=two_choice)
 
     # ------------------------------------------------------------------------------------------------ rows in
     def store(self, kv_c_normed, k_pe, slots, kv_scale=1.0):

@@ -14,7 +14,8 @@ carries `host_tier_variant`: BASELINE config 3 (same shapes, 2M-row pool in pinn
 Zipf(1.1) selections) measured in the same run, and `host_tier_compact_variant`: the same with the host pool in the
 reference's compact Row400 rows (decoded on the way in; 400 instead of 656 bytes per row over PCIe), and
 `host_tier_ways_variant`: compact host rows behind the dynamic 16-way row cache instead of the static hot set, on a
-stream of fresh Zipf draws (`--config 3 --cache ways`).
+stream of fresh Zipf draws (`--config 3 --cache ways`); `host_tier_ways_two_choice_variant` the same with two-choice
+set placement (`--two-choice`).
 
 Other configs print their own JSON line (same keys): 1 = B=1 / 16 heads / K=256 check + timing, 3 = offload split-K,
 4 = indexer logits + top-2048 at L = 32768 and 131072, 5 = chunked prefill (8192 queries) + cache write, 6 = the
@@ -251,16 +252,18 @@ def run_config3(a, dev, steps=None, row_fmt="row656"):
     return res
 
 
-def run_config3_ways(a, dev, steps=None, row_fmt="e2m2", W=16):
+def run_config3_ways(a, dev, steps=None, row_fmt="e2m2", W=16, two=False):
     """Config 3 shapes with the dynamic W-way cache in place of the static hot set: every step draws fresh Zipf(1.1)
     selections (a decode stream); the cache is warmed over the 64 warm-up steps' draws, then each timed step looks
-    its rows up, places the misses, copies them in over PCIe (beside the attention over the hits) and attends."""
+    its rows up, places the misses, copies them in over PCIe (beside the attention over the hits) and attends.
+    two: two-choice set placement (a miss whose set is full takes a way in a second, hashed set)."""
     import torch
     from arcagi2_flashnext_dots3_amd.sparse_offload import HOST_ROW, LayerOffload
     steps = steps or a.steps
     warm_n = max(2, a.warmup // 4)
     C = R3 // 4
-    lo = LayerOffload(R3, dev, cache_rows=C, row_fmt=row_fmt, cache_mode="ways", ways=W, spill_rows=B * K)
+    lo = LayerOffload(R3, dev, cache_rows=C, row_fmt=row_fmt, cache_mode="ways", ways=W, spill_rows=B * K,
+                      two_choice=two)
     _cache_fill(lo.host, R3, 1, dev, fmt=2 if row_fmt == "e2m2" else 0)
     perm = torch.randperm(R3, generator=torch.Generator().manual_seed(3))
     gq = torch.Generator().manual_seed(0)
@@ -295,9 +298,10 @@ def run_config3_ways(a, dev, steps=None, row_fmt="e2m2", W=16):
            "hit_rate": round(hit, 4), "misses_per_step": round(misses / nstat, 1),
            "spill_rows_per_step": round(spills / nstat, 1), "pcie_bytes_per_step": int(mb),
            "pcie_gbs_achieved": round(mb / (ms * 1e-3) / 1e9, 2), "h2d_copy_gbs": round(h2d, 2),
-           "host_row_format": row_fmt, "ways": W,
-           "workload": f"config 3 shapes with a dynamic {W}-way set-associative HBM cache of 524,288 lines (+ "
-                       f"131,072 spill rows) over a 2,097,152-row {'compact Row400' if row_fmt == 'e2m2' else 'Row656'}"
+           "host_row_format": row_fmt, "ways": W, "two_choice": bool(two),
+           "workload": f"config 3 shapes with a dynamic {W}-way set-associative{' two-choice' * two} HBM cache of "
+                       f"524,288 lines (+ 131,072 spill rows) over a 2,097,152-row "
+                       f"{'compact Row400' if row_fmt == 'e2m2' else 'Row656'}"
                        " pinned host pool; each step a fresh Zipf(1.1) draw of B=64 x top-2048 rows; warmed over "
                        "64 steps; per step: lookup / place / resolve, miss copy over PCIe beside the attention over "
                        "the hits, attention over the fresh rows merged in its epilogue"}
@@ -660,6 +664,7 @@ def main():
     ap.add_argument("--cache", default="static", choices=["static", "ways"],
                     help="config 3: static frequency hot set (BASELINE's definition) or the dynamic W-way cache")
     ap.add_argument("--ways", type=int, default=16, help="config 3 --cache ways: lines per set")
+    ap.add_argument("--two-choice", action="store_true", help="config 3 --cache ways: two-choice set placement")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
                     help="only run 5 plain device-to-device copies of BYTES bytes (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -689,12 +694,13 @@ def main():
                     res[key] = run_config3(a, dev, steps=min(a.steps, 20), row_fmt=fmt)
                 except Exception as e:   # the primary line must still print
                     res[key] = {"error": repr(e)[:300]}
-            try:
-                res["host_tier_ways_variant"] = run_config3_ways(a, dev, steps=min(a.steps, 20), row_fmt="e2m2")
-            except Exception as e:
-                res["host_tier_ways_variant"] = {"error": repr(e)[:300]}
+            for key, two in (("host_tier_ways_variant", False), ("host_tier_ways_two_choice_variant", True)):
+                try:
+                    res[key] = run_config3_ways(a, dev, steps=min(a.steps, 20), row_fmt="e2m2", two=two)
+                except Exception as e:
+                    res[key] = {"error": repr(e)[:300]}
     elif a.config == 3:
-        r = run_config3_ways(a, dev, row_fmt=a.host_rows, W=a.ways) if a.cache == "ways" else \
+        r = run_config3_ways(a, dev, row_fmt=a.host_rows, W=a.ways, two=a.two_choice) if a.cache == "ways" else \
             run_config3(a, dev, row_fmt=a.host_rows)
         res = _line("offload split-K decode step us (host tier + HBM hot rows), B=64 top2048", r["ms_per_step"] * 1e3,
                     "us", a, r["ms_per_step"], "bf16 / f16 MFMA, fp32 accumulate", {"workload": r["workload"]},

@@ -159,22 +159,26 @@ int spmla_row400_gather_tiers(const void* src, long long R, const int* rows, lon
  * spmla_wcache_fill. Caller-owned state, zero-initialized once: tag -1, rr / cnt / pin / state / claim 0; claim and
  * rdst hold one int per host row (the epoch of the row's last miss, the pool row it got), so no buffer is cleared
  * between steps. Which ways the misses of a set take, and which misses of an overfull set spill, follow the order of
- * the device atomics. Replaces the reference's W-way cache step (_sa_prefill and
- * _sa_scan / _sa_fill / _sa_advance / _sa_resolve kernels, dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:
- * 677-770, :1595-1622; epoch-tagged miss table offload_fill.py:1-45). */
+ * the device atomics. two = 1: two-choice placement (the reference's ARC_OFFLOAD_TWO_CHOICE, offload_fill.py:16-23,
+ * :136-165, :255-303): row h may also live in set ((h * 2654435761) >> 12) % S; entries that miss the first set look
+ * there (a hit pins it), and a miss with no unpinned way for its ticket in the first set takes a ticket in the second
+ * before it spills. The same `two` must be passed to every call on one cache (spmla_wcache_invalidate included).
+ * Replaces the reference's W-way cache step (_sa_prefill and _sa_scan / _sa_fill / _sa_advance / _sa_resolve
+ * kernels, dotsnote/engine/arcstats_pkg/arcstats/sparse_offload.py:677-770, :1595-1622; epoch-tagged miss table
+ * offload_fill.py:1-45). */
 int spmla_wcache_step(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
                       int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst, int* state,
-                      int cap, int* res, long long res_st, void* stream);
+                      int cap, int two, int* res, long long res_st, void* stream);
 
 /* spmla_wcache_step in two launches groups, so that the row copies can start before the resolution: _place runs the
  * step's lookup and placement (the miss list and the tags are final after it; spmla_wcache_fill may follow on
  * another stream), _resolve writes res and advances the round-robin pointers. Same arguments and results. */
 int spmla_wcache_place(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
                        int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst, int* state,
-                       int cap, void* stream);
+                       int cap, int two, void* stream);
 int spmla_wcache_resolve(const int* idx, long long idx_st, int T, int K, long long R, int* tag, int C, int W, int* rr,
                          int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst,
-                         int* state, int cap, int* res, long long res_st, void* stream);
+                         int* state, int cap, int two, int* res, long long res_st, void* stream);
 
 /* The step's row copies: for each miss m < state[1] with miss_dst[m] >= 0, pool row miss_dst[m] (Row656) = host row
  * miss_rows[m] (host_fmt 0: Row656 bytes; 2: a compact Row400 row decoded to Row656). n_max bounds the miss count
@@ -183,9 +187,10 @@ int spmla_wcache_resolve(const int* idx, long long idx_st, int T, int K, long lo
 int spmla_wcache_fill(const void* host, long long R, int host_fmt, const long long* miss_rows, const long long* miss_dst,
                       const int* state, int n_max, void* pool, long long R_pool, void* stream);
 
-/* Clear the lines that cache rows slots[i] (a rewritten host row must not be served stale). Replaces
- * _sa_invalidate_kernel (sparse_offload.py:782-789). */
-int spmla_wcache_invalidate(const long long* slots, int n, long long R, int* tag, int C, int W, void* stream);
+/* Clear the lines that cache rows slots[i] (a rewritten host row must not be served stale); two = 1 also clears
+ * the rows' second sets. Replaces _sa_invalidate_kernel (sparse_offload.py:782-789) and, for two-choice placement,
+ * _invalidate2_kernel (offload_fill.py:296-308). */
+int spmla_wcache_invalidate(const long long* slots, int n, long long R, int* tag, int C, int W, int two, void* stream);
 
 /* Tier split by resolution: per token, entries with res >= 0 -> hbm_idx (the pool row), res == -2 -> host_idx (the
  * entry's host row idx[t][k]); both compacted in order, padded with -1 to K, counts per token. The host tier of a

@@ -37,6 +37,13 @@ PINS = {
     "row400_gather": "decode of every row equals the Row576 row a direct Row576 write of the dequantized values gives",
     "bmm_fp8": "torch statement of the reference's dequantization ((float8 -> float32) * scale -> bfloat16, all "
                "library conversions) and torch.matmul in float64; a python triple loop on a tiny case",
+    "wcache_step2": "reduces to wcache_step when the second sets are the first ones' (identical hits / misses); a "
+                    "hand-worked W = 1 example; tests/test_oracle_wcache.py",
+    "wcache_verify2": "a sequential simulation of the two-choice ticket rule under random miss orders always passes; "
+                      "planted mistakes (no second-set ticket, a pinned line replaced, a row placed in a third set, "
+                      "a wrong rr advance, a miscounted spill) each fail; tests/test_oracle_wcache.py",
+    "wcache_set2": "hand values of ((h * 2654435761) >> 12) % S, including rows near 2^31 (64-bit product); "
+                   "tests/test_oracle_wcache.py",
     "wcache_step": "hand-worked W = 2 examples (hit, pin, round-robin replacement, overflow to spill); a sequential "
                    "simulation of ticketed placement under random miss orders reproduces every order-independent output",
     "attention": "torch.nn.functional.scaled_dot_product_attention (float64) on dequantized rows + torch.logsumexp;"
@@ -576,6 +583,95 @@ def wcache_step(tag, rr, idx, R, W):
             content[st] = sorted(t[st * W:(st + 1) * W].tolist())
     return {"hits": hits, "pinned": pinned, "misses": sorted(miss), "placed": placed, "spills": spills,
             "rr_next": rr_next, "content": content}
+
+
+def wcache_set2(h, S):
+    """Second candidate set of host row h under two-choice placement (dotsnote/engine/arcstats_pkg/arcstats/
+    offload_fill.py:136-138: ((h * 2654435761) >> 12) % S, in 64-bit integers)."""
+    return ((int(h) * 2654435761) >> 12) % S
+
+
+def wcache_step2(tag, rr, idx, R, W):
+    """The order-independent part of a step with two-choice placement (offload_fill.py:141-165 scan with P2: an
+    entry that misses its first set h % S looks in wcache_set2(h, S), a hit there pins that line): hits, pinned lines
+    and the distinct missing rows (ascending), as dicts like wcache_step's."""
+    tag = np.asarray(tag, dtype=np.int64)
+    C = tag.shape[0]
+    S = C // W
+    pinned, miss, hits = set(), set(), 0
+    for h in np.asarray(idx, dtype=np.int64).reshape(-1):
+        if not (0 <= h < R):
+            continue
+        line = -1
+        for st in (int(h % S), wcache_set2(h, S)):
+            ways = [st * W + w for w in range(W) if tag[st * W + w] == h]
+            if ways:
+                line = ways[0]
+                break
+        if line >= 0:
+            hits += 1
+            pinned.add(line)
+        else:
+            miss.add(int(h))
+    return {"hits": hits, "pinned": pinned, "misses": sorted(miss), "S": S, "W": W}
+
+
+def wcache_verify2(model, tag, rr, tag_after, rr_after, spills):
+    """Conditions every outcome of a two-choice step satisfies, whatever order the device's atomics serve the misses
+    in (offload_fill.py:255-293 alloc with P2, advance sparse_offload.py:747-752); returns the violated ones (empty =
+    consistent). Each miss takes ticket k = cnt[s]++ in its first set s and the k-th unpinned way counted from rr[s];
+    if k reaches the set's unpinned ways u_s it takes a ticket in its second set the same way, and past that it
+    spills. So, with p_s the lines of set s that changed and T_s its tickets (its own misses plus the misses not placed
+    in their first set whose second set is s): pinned lines keep their rows; a changed line holds a miss, in one of
+    that miss's two sets, each miss at most once; the changed lines of s are its first p_s unpinned ways from rr[s];
+    p_s = min(T_s, u_s); a miss outside its first set needs that set full (p = u), a spilled miss both sets full;
+    spills = misses - placed; rr_after[s] = rr[s] + min(T_s, W) mod W."""
+    S, W = model["S"], model["W"]
+    tag = np.asarray(tag, dtype=np.int64)
+    ta = np.asarray(tag_after, dtype=np.int64)
+    rr = np.asarray(rr, dtype=np.int64)
+    misses = set(model["misses"])
+    bad = []
+    if any(ta[l] != tag[l] for l in model["pinned"]):
+        bad.append("pinned line replaced")
+    changed = np.nonzero(ta != tag)[0].tolist()
+    where = {}
+    for l in changed:
+        h = int(ta[l])
+        if h not in misses:
+            bad.append(f"line {l} holds {h}, not a miss of the step")
+            continue
+        if l // W not in (h % S, wcache_set2(h, S)):
+            bad.append(f"row {h} placed outside its two sets")
+        if h in where:
+            bad.append(f"row {h} placed twice")
+        where[h] = l // W
+    if spills != len(misses) - len(where):
+        bad.append(f"spills {spills} != misses {len(misses)} - placed {len(where)}")
+    pin = model["pinned"]
+    unp = [[s * W + (int(rr[s]) + j) % W for j in range(W) if s * W + (int(rr[s]) + j) % W not in pin]
+           for s in range(S)]
+    p = np.zeros(S, dtype=np.int64)
+    for l in changed:
+        p[l // W] += 1
+    tickets = np.zeros(S, dtype=np.int64)
+    for h in misses:
+        s1 = h % S
+        tickets[s1] += 1
+        if where.get(h) != s1:                         # its first ticket failed
+            tickets[wcache_set2(h, S)] += 1
+            if p[s1] != len(unp[s1]):
+                bad.append(f"row {h} left its first set {s1} with a free way")
+            if h not in where and p[wcache_set2(h, S)] != len(unp[wcache_set2(h, S)]):
+                bad.append(f"row {h} spilled with a free way in its second set")
+    for s in range(S):
+        if sorted(l for l in changed if l // W == s) != sorted(unp[s][:p[s]]):
+            bad.append(f"set {s}: replaced lines are not its first {p[s]} unpinned ways from rr")
+        if p[s] != min(tickets[s], len(unp[s])):
+            bad.append(f"set {s}: {p[s]} lines placed for {tickets[s]} tickets and {len(unp[s])} free ways")
+        if int(rr_after[s]) != (int(rr[s]) + min(int(tickets[s]), W)) % W:
+            bad.append(f"set {s}: rr {int(rr_after[s])} after {tickets[s]} tickets from {int(rr[s])}")
+    return bad
 
 
 # ------------------------------------------------------------------------------------------------ MLA absorbed matmuls

@@ -62,14 +62,17 @@ def test_version():
     (("spmla_cache_write", None, 0, None, 0, None, 1, None, 10, 64, 0, 7, 1.0, None), -2),
     (("spmla_cache_write", None, 0, None, 0, None, 1, None, 10, 64, 0, 3, 1.0, None), -2),
     (("spmla_row400_gather", None, 0, None, 1, None, 656, 2, 0, None), -2),
-    (("spmla_wcache_step", None, 0, 1, 8, 100, None, 10, 4, None, None, None, None, None, None, None, None, 0, None,
+    (("spmla_wcache_step", None, 0, 1, 8, 100, None, 10, 4, None, None, None, None, None, None, None, None, 0, 0, None,
       0, None), -2),
-    (("spmla_wcache_step", None, 0, 1, 8, 1 << 32, None, 8, 4, None, None, None, None, None, None, None, None, 0, None,
-      0, None), -5),
+    (("spmla_wcache_step", None, 0, 1, 8, 1 << 32, None, 8, 4, None, None, None, None, None, None, None, None, 0, 0,
+      None, 0, None), -5),
+    (("spmla_wcache_step", None, 0, 1, 8, 100, None, 8, 4, None, None, None, None, None, None, None, None, 0, 2, None,
+      0, None), -2),
     (("spmla_wcache_fill", None, 0, 1, None, None, None, 4, None, 0, None), -2),
     (("spmla_bmm_fp8", None, 0, 0, 1, None, 0, 0, 1, None, 0, 0, 0, 0, None, 0, 0, 1, 0, 1, 1, 1, 12, None), -2),
     (("spmla_mla_query", None, 0, 0, None, 0, 0, None, None, 1, 0, None, 0, 0, None), -2),
-    (("spmla_wcache_invalidate", None, 1, 10, None, 6, 4, None), -2),
+    (("spmla_wcache_invalidate", None, 1, 10, None, 6, 4, 0, None), -2),
+    (("spmla_wcache_invalidate", None, 1, 10, None, 8, 4, 3, None), -2),
     (("spmla_attn_merge", None, 0, 0, None, 0, None, 0, 0, None, 1, 1, 1.0, 1.0, None, 0, 0, None, 0, None, 0, 0,
       None, 0, None), -2),
     (("spmla_row400_gather", None, 0, None, -1, None, 656, 0, 0, None), -2),

@@ -158,3 +158,74 @@ def test_layer_offload_ways_matches_single_tier(dev, cap, overlap):
             assert float((out.float() - o1.float()).abs().max()) <= 1e-2
             assert float((lse - l1).abs().max()) <= 1e-4
     assert lo.hit_rate(idx) > 0.0
+
+
+@pytest.mark.parametrize("W,cap", [(1, 4096), (4, 4096), (4, 48)])
+def test_wcache_two_choice_steps(dev, W, cap):
+    """Two-choice placement over several steps of a cache much smaller than the working set (sets overflow): hits,
+    distinct misses and every outcome condition of the oracle's verifier (pinned lines kept, rows only in their two
+    sets and at most once, first-p unpinned ways per set, p = min(tickets, free), full sets before a second-set or
+    spill placement, rr advance); every entry's pool row holds its host row; invalidation clears both sets."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    R, C, T, K = 6000, 256, 4, 256
+    host_np, _, _ = make_pool_656(R, seed=8)
+    host = torch.from_numpy(host_np).pin_memory()
+    wc = kernels.RowCache(C, W, cap, dev, two=True)
+    S = wc.S
+    second = 0
+    for step in range(5):
+        idx = _selections(T, K, R, step, hot=400)
+        tag0, rr0 = wc.tag.cpu().numpy().astype(np.int64), wc.rr.cpu().numpy()
+        print(f"[wcache two] W={W} cap={cap} step={step}", flush=True)
+        res = kernels.wcache_step(wc, torch.from_numpy(idx).to(dev), R)
+        kernels.wcache_fill(wc, host, R, 0, T * K)
+        torch.cuda.synchronize()
+        m = ref.wcache_step2(tag0, rr0, idx, R, W)
+        st = wc.state.cpu().numpy()
+        assert st[3] == m["hits"] and st[1] == len(m["misses"]), (st, m["hits"], len(m["misses"]))
+        tag = wc.tag.cpu().numpy().astype(np.int64)
+        bad = ref.wcache_verify2(m, tag0, rr0, tag, wc.rr.cpu().numpy(), int(st[2]))
+        assert bad == [], bad[:5]
+        second += sum(1 for l in np.nonzero(tag != tag0)[0] if l // W != tag[l] % S)
+        r = res.cpu().numpy()
+        valid = (idx >= 0) & (idx < R)
+        assert np.all(r[~valid] == -1) and np.all(r[valid] >= -2)
+        ok = r >= 0
+        pool = wc.pool.cpu().numpy()
+        assert np.array_equal(pool[r[ok]], host_np[idx[ok]])
+        line = ok & (r < C)
+        assert np.all(tag[r[line]] == idx[line])
+        if cap >= T * K:
+            assert np.all(r[valid] >= 0)
+    assert second > 0                                      # some misses took their second set
+    cached = np.unique(tag[tag >= 0])
+    kernels.wcache_invalidate(wc, torch.from_numpy(cached.astype(np.int64)).to(dev), R)
+    torch.cuda.synchronize()
+    assert np.all(wc.tag.cpu().numpy() == -1)
+
+
+def test_layer_offload_two_choice_matches_single_tier(dev):
+    """LayerOffload(cache_mode='ways', two_choice=True) with a spill area covering the step and no overlap: the
+    attention over the cache pool equals the single-tier attention over the gathered rows bit for bit."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    from arcagi2_flashnext_dots3_amd.sparse_offload import LayerOffload
+    R, T, H, K = 6000, 4, 64, 1024
+    g = torch.Generator().manual_seed(9)
+    kv = (torch.randn(R, 512, generator=g)).to(torch.bfloat16)
+    pe = torch.randn(R, 64, generator=g).to(torch.bfloat16)
+    lo = LayerOffload(R, dev, cache_rows=512, cache_mode="ways", ways=8, spill_rows=T * K, overlap_fill=False,
+                      two_choice=True)
+    lo.store(kv.to(dev), pe.to(dev), torch.arange(R, dtype=torch.int64, device=dev))
+    q = make_q(T, H, seed=10).to(dev)
+    sm = 192 ** -0.5
+    for step in range(3):
+        idx = torch.from_numpy(_selections(T, K, R, step, hot=300)).to(dev)
+        out, lse = lo.attend(q, idx, sm, return_lse=True)
+        staged = torch.empty(T * K, 656, dtype=torch.uint8, device=dev)
+        kernels.gather(lo.host, idx.reshape(-1).to(torch.int64), staged)
+        sidx = torch.where((idx >= 0) & (idx < R), torch.arange(T * K, device=dev, dtype=torch.int32).view(T, K),
+                           torch.full_like(idx, -1))
+        o1, l1 = kernels.attend(q, staged, sidx, sm)
+        torch.cuda.synchronize()
+        assert torch.equal(out, o1) and torch.equal(lse, l1)
+    assert lo.hit_rate(idx) > 0.0
