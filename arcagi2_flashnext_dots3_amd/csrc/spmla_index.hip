@@ -26,7 +26,10 @@ namespace spmla {
 namespace idx {
 
 // ------------------------------------------------------------------------------------------------ logits
-constexpr int LG_TPW = 8;                 // 32-key tiles per wave
+#ifndef SPMLA_LG_TPW
+#define SPMLA_LG_TPW 8
+#endif
+constexpr int LG_TPW = SPMLA_LG_TPW;      // 32-key tiles per wave (any value >= 1; 8 measured best, build-time knob)
 constexpr int LG_KPB = 4 * LG_TPW * 32;   // keys per 4-wave workgroup
 
 struct LogitParams {
