@@ -413,7 +413,24 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     }
     started = true;
 
-    // ---- PV: output columns of group g use P' = P * scale(row, g) (fp16); group g + 1's operands read meanwhile
+    // ---- PV: output columns of group g use P' = P * scale(row, g) (fp16). Group g + 1's scales and V^T codes are
+    // read at the start of group g and its P' is formed between group g's MFMAs, so that VALU work overlaps the
+    // matrix core instead of preceding each group's first MFMA.
+    auto p_scaled = [&](const f32x4* sc, f16x8* pb) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const f32x4 s0 = sc[2 * ks], s1 = sc[2 * ks + 1];
+        const float* pp = P + 8 * ks;
+        i32x4 o;
+        o[0] = (int)pk_f16(pp[0] * s0[0], pp[1] * s0[1]);
+        o[1] = (int)pk_f16(pp[2] * s0[2], pp[3] * s0[3]);
+        o[2] = (int)pk_f16(pp[4] * s1[0], pp[5] * s1[1]);
+        o[3] = (int)pk_f16(pp[6] * s1[2], pp[7] * s1[3]);
+        pb[ks] = __builtin_bit_cast(f16x8, o);
+      }
+    };
+    f16x8 pb[2];
+    p_scaled(ps, pb);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       f32x4 pn[4];
@@ -427,18 +444,7 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
               (SPMLA_LDS i32x2*)(tb + (4 * (g + 1) + (f8 >> 1)) * 1024 + (f8 & 1) * 256 + tr_off));
       }
       __builtin_amdgcn_sched_barrier(0);
-      f16x8 pb[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const f32x4 s0 = ps[2 * ks], s1 = ps[2 * ks + 1];
-        const float* pp = P + 8 * ks;
-        i32x4 o;
-        o[0] = (int)pk_f16(pp[0] * s0[0], pp[1] * s0[1]);
-        o[1] = (int)pk_f16(pp[2] * s0[2], pp[3] * s0[3]);
-        o[2] = (int)pk_f16(pp[4] * s1[0], pp[5] * s1[1]);
-        o[3] = (int)pk_f16(pp[6] * s1[2], pp[7] * s1[3]);
-        pb[ks] = __builtin_bit_cast(f16x8, o);
-      }
+      f16x8 pbn[2];
 #pragma unroll
       for (int f8 = 0; f8 < 8; ++f8) {
         const int mt = 4 * g + (f8 >> 1), ks = f8 & 1;     // output columns 32 mt .. 32 mt + 31, rows 16 ks ..
@@ -447,10 +453,11 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
         a[0] = (int)fp8lo_f16x2((uint32_t)raw[0]); a[1] = (int)fp8hi_f16x2((uint32_t)raw[0]);
         a[2] = (int)fp8lo_f16x2((uint32_t)raw[1]); a[3] = (int)fp8hi_f16x2((uint32_t)raw[1]);
         O[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), pb[ks], O[mt], 0, 0, 0);
+        if (f8 == 3 && g < 3) p_scaled(pn, pbn);          // next group's P', behind four MFMAs
       }
       if (g < 3) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) ps[q4] = pn[q4];
+        pb[0] = pbn[0];
+        pb[1] = pbn[1];
 #pragma unroll
         for (int f8 = 0; f8 < 8; ++f8) tv[f8] = vn[f8];
       }
