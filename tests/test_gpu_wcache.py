@@ -155,7 +155,9 @@ def test_layer_offload_ways_matches_single_tier(dev, cap, overlap):
         if cap >= T * K and not overlap:
             assert torch.equal(out, o1) and torch.equal(lse, l1)
         else:
-            assert float((out.float() - o1.float()).abs().max()) <= 1e-2
+            # the parity bar 1e-2 * max(1, |ref|): one bf16 ulp of an output in [2, 4) is 2^-6 > 1e-2
+            err = (out.float() - o1.float()).abs() / o1.float().abs().clamp_min(1.0)
+            assert float(err.max()) <= 1e-2
             assert float((lse - l1).abs().max()) <= 1e-4
     assert lo.hit_rate(idx) > 0.0
 
