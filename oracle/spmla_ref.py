@@ -22,6 +22,25 @@ PINS = {
     "e4m3_decode": "torch float8_e4m3fn -> float32 on all 256 codes",
     "e4m3_to_bf16_bits": "torch float8_e4m3fn -> bfloat16 on all 256 codes",
     "bf16": "torch bfloat16 conversions",
+    "f32_to_bf16_bits": "torch float32 -> bfloat16 on 65K random fp32 over the full exponent range, 4096 exact ties "
+                        "and the specials (NaN stays NaN); tests/test_oracle_helpers.py",
+    "bf16_bits_to_f32": "torch bfloat16 -> float32 on the same values; tests/test_oracle_helpers.py",
+    "okey": "sorting by the key orders finite fp32 as numpy does, -0 below +0, NaN largest; "
+            "tests/test_oracle_helpers.py",
+    "dequant_656": "torch float8_e4m3fn decode times the row's fp32 scales, rope via torch bfloat16; "
+                   "tests/test_oracle_helpers.py",
+    "dequant_576": "torch float8_e4m3fn decode of all 576 bytes; tests/test_oracle_helpers.py",
+    "row400_unpack": "unpack(pack(x)) == x and the element-by-element byte layout (row400_pack's checks); "
+                     "tests/test_oracle_row400.py",
+    "row400_dequant": "the 16-value e2m2 grid x 2^k by hand; every value exact in e4m3 / bf16; "
+                      "tests/test_oracle_row400.py",
+    "bmm_fp8_weights": "torch (float8 -> float32) * scale -> bfloat16 on random codes and scales; "
+                       "tests/test_oracle_mla.py",
+    "shuffle_rows": "shuffle_rows(shuffle_layout(rows)) == rows; tests/test_oracle_shuffle.py",
+    "index_key_write_shuffle": "equals index_key_write into 132-byte rows followed by shuffle_layout; "
+                               "tests/test_oracle_shuffle.py",
+    "paged_ctx": "hand values of (request, visible keys) per token for decode and MTP (next_n) batches; "
+                 "tests/test_oracle_shuffle.py",
     "cache_write_656": "dequantized row within half an e4m3 ulp of x / s; per-group max code == 448 (0x7e); "
                        "zero groups; rope bit copy; slot skipping",
     "cache_write_576": "e4m3 of the clamped value (library encoder) ; rope codes",
