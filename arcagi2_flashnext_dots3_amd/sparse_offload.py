@@ -47,13 +47,17 @@ class LayerOffload:
     `spill_rows` HBM rows for misses that find no free way; a step with more entries than spill rows can leave rows on
     the host, which then take the host tier). overlap_fill (ways): attend over the step's hits on a second stream while
     the misses are copied in, then over the fresh rows with the hits' partial merged in the epilogue; False: one
-    attention over the whole step after the copy (bit-identical to attending the gathered rows). two_choice (ways):
+    attention over the whole step after the copy (bit-identical to attending the gathered rows). cache_fmt (static,
+    row_fmt="e2m2"): "row656" lines decoded once when filled, or "e2m2": the reference's compact GPU row cache
+    (offload_rowfmt.py:1-22 with its compact cache lines, csrc/offload_attn2.cu:210-256), Row400 lines in HBM (39%
+    fewer bytes per line) whose selected lines are decoded into Row656 staging each step before the HBM-tier
+    attention (same values, bit-identical results). two_choice (ways):
     the reference's two-choice set placement (ARC_OFFLOAD_TWO_CHOICE, offload_fill.py:16-23): a missing row whose set
     has no free way takes one in a second, hashed set before it spills; lookups and invalidations cover both sets.
     """
 
     def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
-                 spill_rows=131072, overlap_fill=True, two_choice=False):
+                 spill_rows=131072, overlap_fill=True, two_choice=False, cache_fmt="row656"):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         if cache_mode not in ("static", "ways"):
@@ -64,8 +68,11 @@ class LayerOffload:
         self.row_fmt = row_fmt
         self.host = torch.zeros((self.R, HOST_ROW[row_fmt]), dtype=torch.uint8, pin_memory=True)
         self.C = min(int(cache_rows), self.R)
-        self.cache = torch.zeros((max(self.C, 1) if cache_mode == "static" else 1, ROW), dtype=torch.uint8,
-                                 device=self.device)
+        if cache_fmt not in HOST_ROW or (cache_fmt == "e2m2" and (row_fmt != "e2m2" or cache_mode != "static")):
+            raise ValueError("cache_fmt 'e2m2' needs row_fmt='e2m2' and cache_mode='static'")
+        self.cache_fmt = cache_fmt
+        self.cache = torch.zeros((max(self.C, 1) if cache_mode == "static" else 1, HOST_ROW[cache_fmt]),
+                                 dtype=torch.uint8, device=self.device)
         self.tag = torch.full((max(self.C, 1),), -1, dtype=torch.int64, device=self.device)
         self.rowmap = torch.full((max(self.R, 1),), -1, dtype=torch.int32, device=self.device)
         self._ws = {}
@@ -99,12 +106,15 @@ class LayerOffload:
             ok = (slots >= 0) & (slots < self.R)
             lines = torch.where(ok, self.rowmap[slots.clamp(0, self.R - 1)].to(torch.int64), -1)
             if compact:
-                # the cache lines get the decoded compact rows: encode the same tokens again into HBM scratch (the
-                # encoder is deterministic) and decode them into their lines
+                # the cache lines get the compact rows (decoded for Row656 lines): encode the same tokens again into
+                # HBM scratch (the encoder is deterministic) and copy or decode them into their lines
                 tmp = self._buf("wt", (n, kernels.ROW400), torch.uint8)
                 ident = torch.arange(n, dtype=torch.int64, device=self.device)
                 kernels.cache_write(kv_c_normed[:n], kpe[:n], ident, tmp, fmt=2, kv_scale=kv_scale)
-                kernels.row400_copy(tmp, ident, self.cache[:self.C], lines)
+                if self.cache_fmt == "e2m2":
+                    kernels.copy_rows(tmp, ident, self.cache[:self.C], lines)
+                else:
+                    kernels.row400_copy(tmp, ident, self.cache[:self.C], lines)
             else:
                 kernels.cache_write(kv_c_normed[:n], kpe[:n], lines, self.cache[:self.C])
 
@@ -133,7 +143,7 @@ class LayerOffload:
         m = rows.numel()
         if m:
             lines = torch.arange(m, dtype=torch.int64, device=self.device)
-            if self.row_fmt == "e2m2":
+            if self.row_fmt == "e2m2" and self.cache_fmt != "e2m2":
                 kernels.row400_copy(self.host, rows, self.cache[:self.C], lines)
             else:
                 kernels.copy_rows(self.host, rows, self.cache[:self.C], lines)
@@ -221,7 +231,15 @@ class LayerOffload:
             kernels.gather_tiers(self.host, host, mcnt, staged)
         side.wait_event(ev_split)
         with torch.cuda.stream(side):
-            kernels.attend_partial(q, self.cache[:self.C], hbm, sm_scale, kv_scale, op[0:1], lp[0:1], kcount=hcnt)
+            if self.cache_fmt == "e2m2":
+                # compact lines: decode the step's hot lines (compacted per token, -1 padded) into Row656 staging in
+                # the same order, then attend there through the identity map
+                hstaged = self._buf("hstaged", (T * K, ROW), torch.uint8)
+                kernels.row400_gather(self.cache[:self.C], hbm.reshape(-1).to(torch.int64), hstaged)
+                kernels.attend_partial(q, hstaged, sidx, sm_scale, kv_scale, op[0:1], lp[0:1], kcount=hcnt)
+            else:
+                kernels.attend_partial(q, self.cache[:self.C], hbm, sm_scale, kv_scale, op[0:1], lp[0:1],
+                                       kcount=hcnt)
             ev_hbm.record(side)
         main.wait_event(ev_hbm)
         kernels.attend_merge(q, staged, sidx, sm_scale, kv_scale, op[0], lp[0], out=out, lse=lse, kcount=mcnt)

@@ -123,17 +123,18 @@ def test_row400_gather_tiers(dev, T, K, zero0):
     assert np.array_equal(out.cpu().numpy(), exp)
 
 
-@pytest.mark.parametrize("C", [0, 300])
-def test_layer_offload_compact_rows(dev, C):
+@pytest.mark.parametrize("C,cache_fmt", [(0, "row656"), (300, "row656"), (300, "e2m2")])
+def test_layer_offload_compact_rows(dev, C, cache_fmt):
     """store -> (hot set) -> attend with compact host rows: attention over the decoded Row576 values, kv_scale applied
-    at both ends, vs the oracle; gather returns the reference's Row576 rows byte for byte."""
+    at both ends, vs the oracle; gather returns the reference's Row576 rows byte for byte. cache_fmt e2m2: the hot
+    lines stay compact Row400 rows in HBM (the stored bytes themselves, write-through included)."""
     from arcagi2_flashnext_dots3_amd.sparse_offload import LayerOffload
     R, T, H, K, kv_scale = 1200, 3, 32, 256, 0.5
     g = torch.Generator().manual_seed(21)              # O(1) rows (the codec's edge cases are covered above)
     kv = (torch.randn(R, 512, generator=g) * torch.exp(torch.randn(R, 16, generator=g) * 0.5).repeat_interleave(32, 1)
           ).to(torch.bfloat16)
     pe = torch.randn(R, 64, generator=g).to(torch.bfloat16)
-    lo = LayerOffload(R, dev, key="l0", cache_rows=C, row_fmt="e2m2")
+    lo = LayerOffload(R, dev, key="l0", cache_rows=C, row_fmt="e2m2", cache_fmt=cache_fmt)
     slots = torch.arange(R, dtype=torch.int64, device=dev)
     lo.store(kv.to(dev), pe.to(dev), slots, kv_scale=kv_scale)
     if C:
@@ -143,7 +144,9 @@ def test_layer_offload_compact_rows(dev, C):
     host_np = _oracle_rows(kv, pe, np.arange(R), R, kv_scale, 0)
     assert np.array_equal(lo.host.numpy(), host_np)
     rows576 = ref.row400_gather(host_np, np.arange(R), fmt=576)
-    if C:
+    if C and cache_fmt == "e2m2":
+        assert np.array_equal(lo.cache[:C].cpu().numpy(), host_np[np.arange(0, 2 * C, 2)])
+    elif C:
         assert np.array_equal(lo.cache[:C].cpu().numpy(), ref.row400_gather(host_np, np.arange(0, 2 * C, 2), fmt=656))
     g = torch.full((10, 576), 1, dtype=torch.uint8, device=dev)
     lo.gather(torch.tensor([5, -1, 7, R, 0, 1199, 3, 2, 1, 4], device=dev), g)
@@ -157,3 +160,10 @@ def test_layer_offload_compact_rows(dev, C):
     # bf16 output: 1e-2 absolute plus its own rounding (2^-9 relative)
     assert np.all(np.abs(out.float().cpu().numpy() - eo) <= 1e-2 + 2.0 ** -9 * np.abs(eo))
     assert np.abs(lse.cpu().numpy() - el).max() < 1e-3
+    if C and cache_fmt == "e2m2":                      # same values as Row656 lines: bit-identical attention
+        lo2 = LayerOffload(R, dev, key="l1", cache_rows=C, row_fmt="e2m2")
+        lo2.host.copy_(lo.host)
+        lo2.set_hot_rows(torch.arange(0, 2 * C, 2, dtype=torch.int64))
+        o2, l2 = lo2.attend(q.to(dev), idx.to(dev), sm, kv_scale, return_lse=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out, o2) and torch.equal(lse, l2)
