@@ -123,3 +123,19 @@ def test_product_package_does_not_import_oracle():
             if f.endswith(".py"):
                 txt = open(os.path.join(dp, f)).read()
                 assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", txt, re.M), f
+
+
+@pytest.mark.parametrize("lang", ["c", "c++"])
+def test_header_compiles_standalone(tmp_path, lang):
+    """include/spmla.h is a plain C-ABI header: it compiles on its own as C99 and as C++17 with warnings as errors."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc" if lang == "c" else "g++")
+    if cc is None:
+        pytest.skip("no host compiler")
+    src = tmp_path / "hdr.c"
+    src.write_text('#include "spmla.h"\nint main(void) { return 0; }\n')
+    std = "-std=c99" if lang == "c" else "-std=c++17"
+    r = subprocess.run([cc, std, "-Wall", "-Werror", "-fsyntax-only", "-I", os.path.join(ROOT, "include"), "-x", lang,
+                        str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
