@@ -23,6 +23,8 @@ SIGNATURES = {
     "spmla_topk": [P, LL, P, I, I, I, P, LL, P],
     "spmla_topk_ws_bytes": [I, I, I],
     "spmla_topk_ws": [P, LL, P, I, I, I, P, LL, P, LL, P],
+    "spmla_topk_scratch_bytes": [],
+    "spmla_topk_scratch": [P, LL, P, I, I, I, P, LL, P],
     "spmla_topk_local": [P, LL, P, I, I, I, I, I, P, P],
     "spmla_topk_merge": [P, I, I, I, I, I, P, LL, P],
     "spmla_rows_from_topk": [P, LL, P, P, LL, I, I, LL, I, I, P, LL, P, P],
@@ -56,7 +58,8 @@ SIGNATURES = {
     "spmla_version": [],
     "spmla_host_e4m3_encode": [P, P, LL],
 }
-_RESTYPE = {"spmla_version": ctypes.c_char_p, "spmla_host_e4m3_encode": None, "spmla_topk_ws_bytes": LL}
+_RESTYPE = {"spmla_version": ctypes.c_char_p, "spmla_host_e4m3_encode": None, "spmla_topk_ws_bytes": LL,
+            "spmla_topk_scratch_bytes": LL}
 
 ERRORS = {-2: "bad argument", -3: "misaligned pointer or stride", -5: "size beyond the kernel's limit"}
 

@@ -979,8 +979,41 @@ __global__ void zero_i32(int* p, int n) {
   if (i < n) p[i] = 0;
 }
 
+// ---- scratch of the no-allocation top-k entry point (spmla_topk_scratch) ---------------------------------------
+// File-scope device memory (each GPU holds its own copy from module load until the process ends). Host code never
+// passes `scratch` itself to a kernel: its name is a host-side stand-in, not a device address. The device address
+// comes from hipGetSymbolAddress, once per device, and is kept in scratch_dev[].
+constexpr long long TOPK_SCRATCH_BYTES = 16ll << 20;
+static __device__ __align__(256) uint8_t scratch[TOPK_SCRATCH_BYTES];
+
 }  // namespace idx
 }  // namespace spmla
+
+#include <mutex>
+
+namespace {
+constexpr int SCRATCH_MAX_DEV = 64;
+std::mutex scratch_mu;
+void* scratch_dev[SCRATCH_MAX_DEV] = {};
+
+// Device address of this device's `scratch` array (looked up on the first call on the device).
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= SCRATCH_MAX_DEV) return spmla::SPMLA_ELIMIT;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(spmla::idx::scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return (int)hipErrorInvalidSymbol;
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return spmla::SPMLA_OK;
+}
+}  // namespace
 
 using namespace spmla;
 
@@ -1106,6 +1139,23 @@ int spmla_topk_ws(const float* logits, long long lg_st, const int* ctx, int rows
   p.level = 2;                                      // header 2: the state after both levels
   hipLaunchKernelGGL(idx::topk_finish_kernel, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
+}
+
+long long spmla_topk_scratch_bytes(void) { return idx::TOPK_SCRATCH_BYTES; }
+
+int spmla_topk_scratch(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                       long long out_st, void* stream) {
+  if (rows < 0 || Lc < 0 || K <= 0) return SPMLA_EARG;
+  if (K > idx::TK_KMAX) return SPMLA_ELIMIT;
+  if (rows == 0) return SPMLA_OK;
+  if (!logits || !ctx || !out) return SPMLA_EARG;
+  const long long need = spmla_topk_ws_bytes(rows, Lc, K);
+  if (need <= 0) return SPMLA_EARG;
+  if (need > idx::TOPK_SCRATCH_BYTES) return SPMLA_ELIMIT;   // beyond the fixed scratch: use spmla_topk_ws
+  void* ws = nullptr;
+  const int rc = scratch_ptr(&ws);
+  if (rc != SPMLA_OK) return rc;
+  return spmla_topk_ws(logits, lg_st, ctx, rows, Lc, K, out, out_st, ws, need, stream);
 }
 
 int spmla_topk_local(const float* logits, long long lg_st, const int* ctx, int rows, int rank, int P, int Lc, int kl,

@@ -203,6 +203,21 @@ def topk(logits, ctx, K, out=None, single_pass=False):
     return out
 
 
+def topk_scratch(logits, ctx, K, out=None):
+    """topk without a workspace or any allocation in the library (spmla_topk_scratch): the passes use the library's
+    fixed per-GPU scratch. Calls that overlap on one GPU race. Sizes beyond the scratch raise (SPMLA_ELIMIT)."""
+    rows, Lc = logits.shape
+    _need(logits.dtype == torch.float32 and logits.stride(1) == 1, "fp32 logits with contiguous rows")
+    _need(ctx.dtype == torch.int32 and ctx.is_contiguous() and ctx.shape[0] >= rows, "ctx int32 [rows]")
+    if out is None:
+        out = torch.empty(rows, K, dtype=torch.int32, device=logits.device)
+    _need(out.dtype == torch.int32 and out.stride(1) == 1 and out.shape[0] >= rows and out.shape[1] >= K,
+          "out int32 [rows, >= K]")
+    _lib.call("spmla_topk_scratch", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K,
+              out.data_ptr(), out.stride(0), _stream(logits))
+    return out
+
+
 def topk_local(lg, ctx, rank, P, kl, pk=None):
     """fast_topk.local: lg [rows, Lc] fp32 (column j = position j * P + rank), ctx [rows] int32 positions ->
     pk [rows, 2 * kl] fp32 = [top-kl values | their positions as int32 bits], ascending column order, -inf padded."""

@@ -79,6 +79,18 @@ long long spmla_topk_ws_bytes(int rows, int Lc, int K);
 int spmla_topk_ws(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
                   long long out_st, void* ws, long long ws_bytes, void* stream);
 
+/* spmla_topk_ws without a caller workspace and without any allocation: the passes use the library's own
+ * fixed device scratch (a file-scope array of spmla_topk_scratch_bytes() = 16 MiB per GPU, held from library load
+ * until the process ends; its device address is looked up once per device on the first call there). Same result
+ * as spmla_topk_ws. Sizes whose workspace (spmla_topk_ws_bytes) exceeds the scratch return SPMLA_ELIMIT (e.g. 64 rows
+ * fit at any Lc up to 2^31). All calls on one GPU share the scratch: calls that overlap on one GPU (other streams,
+ * other threads) race and must not be issued. The scratch keeps the last call's contents; the passes need no
+ * particular initial contents. No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). */
+long long spmla_topk_scratch_bytes(void);
+int spmla_topk_scratch(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                       long long out_st, void* stream);
+
 /* fast_topk.local at rank `rank` of P: the row's valid columns are j < ceil((ctx[row] - rank) / P) (clipped to Lc);
  * the top kl of them by the same key and tie rule as spmla_topk go to pk[row] = [kl values fp32 | kl positions
  * j * P + rank as int32 bits] (pk row stride 2 * kl floats) in ascending column order; rows with fewer than kl valid
