@@ -7,58 +7,67 @@
 //   p = exp2(s * log2e - m), o[h] = kv_scale * sum_k p latent / sum_k p,  lse = ln sum_k exp(s)
 //   invalid entries contribute nothing; a token with no valid entry gives o = 0 and lse = -inf.
 //
-// gfx950 mapping. One workgroup = (token t, group of 32 heads, split s), 4 waves, one wave per SIMD (each wave
-// holds its 32 heads' query in VGPRs and their 32 x 512 fp32 output accumulator in AGPRs). The rows of the split
-// are cut into 32-row tiles; wave w streams tiles w, w + 4, w + 8, ... on its own, so the main loop has no
-// workgroup barrier and no exchange between waves:
-//   * a tile (codes + scales) is copied into the wave's private double buffer in LDS with direct global->LDS
-//     copies (global_load_lds_dwordx4), chunk-major [chunk][row][16 B], while the rope of its rows goes straight
-//     into VGPRs (the rope is an MFMA A operand as stored); the copy of tile j + 1 runs during the math of tile j;
-//   * S^T (32 rows x 32 heads) on bf16 MFMA (32x32x16): e4m3 codes convert exactly to bf16, two per
-//     v_cvt_scalef32_pk_bf16_fp8; each scale group's partial is multiplied by the row's fp32 scale (the fp8 MFMA
-//     is not used: its internal accumulation keeps only ~2^-12 of the largest product, measured on gfx950);
-//   * the C layout puts one head in each lane (16 rows; the other 16 in lane + 32), so the online softmax is
-//     in-lane plus one cross-half exchange, and P feeds the PV B operand without data movement (the row order of
-//     the V^T operand, read with ds_read_b64_tr_b8, follows the lane's rows);
-//   * PV on f16 MFMA with P' = P * scale (fp16, RNE) and the codes in fp16; p <= 2^TAU keeps P' finite for
-//     scales up to 65504 / 2^TAU (rows whose largest latent magnitude is below 458,000);
-//   * lazy rescaling: a head's reference max moves only when a tile exceeds it by more than TAU (log2 units),
-//     so p <= 2^TAU: exact either way, and O is rescaled rarely;
-//   * at the end the 4 waves' (m, l, O) merge through LDS (the tile buffers are free by then).
+// gfx950 mapping. One workgroup = (token t, group of up to 128 heads, split s of the token's rows), 4 waves, one per
+// SIMD; wave w owns heads 32 w .. 32 w + 31 of the group: their query in VGPRs and their 32 x 512 fp32 output
+// accumulator in AGPRs. All four waves walk the same 32-row tiles, so every e4m3 code is converted once per
+// workgroup and read by the four head blocks from LDS:
+//   * staging: wave w copies the codes of scale group w (32 rows x 128 B) into a private 3-deep LDS ring with
+//     direct global->LDS copies (global_load_lds_dwordx4), plus a quarter of the rows' bf16 rope and scale w of all
+//     32 rows; entries that are invalid or past the split's end copy a file-scope zero row, so they feed exact zeros
+//     into both products;
+//   * conversion: wave w converts its group exactly to f16 (v_cvt_scalef32_pk_f16_fp8; every e4m3 value is an f16)
+//     into the shared tile [32 rows][64 chunks of 16 B], chunk c of row r stored at (c & ~15) | ((c & 15) ^ g(r)),
+//     g(r) = 4 (r & 3) | ((r >> 2) & 3): the row-major QK operand reads (16 rows per LDS cycle) and the transposed PV
+//     operand reads (ds_read_b64_tr_b16, 4 rows x 64 B per 32 lanes) are then both free of bank conflicts. The
+//     conversion of tile j + 1 runs between the QK MFMAs of tile j; one workgroup barrier per tile;
+//   * QK: S^T (32 rows x 32 heads) with VGPR accumulators: the latent on f16 MFMA (32x32x16; the query converted to
+//     f16 once, exact in f16's normal range, as the reference's fp16 QK), one partial per 128-value scale group
+//     combined with the rows' fp32 scales (a DPP operand: see fmac4_dpp), so no product of a code and a scale is
+//     rounded; the rope on bf16 MFMA;
+//   * softmax: the C layout puts one head in each lane (16 rows; the other 16 in lane + 32): in-lane plus one
+//     cross-half exchange, base 2, lazy rescaling (a head's reference max moves only when a tile exceeds it by more
+//     than TAU, so p <= 2^TAU and O is rescaled rarely);
+//   * PV: f16 MFMA, V^T read transposed from the shared f16 tile, P' = P * scale(row, group) rounded to f16 (11
+//     significant bits); a power-of-two factor 2^-eps carried by P, O and l keeps P' inside f16's range for any
+//     row scale (see the softmax).
 #include "spmla_common.h"
-#include <stdlib.h>
 
 namespace spmla {
 namespace attn {
 
-constexpr int HG = 32;                // heads per workgroup
-constexpr int NW = 4;                 // waves per workgroup
+constexpr int NW = 4;                 // waves per workgroup = head blocks
+constexpr int HB = 32;                // heads per wave
+constexpr int HGW = NW * HB;          // heads per workgroup
 constexpr int TR = 32;                // rows per tile
-constexpr int KMAX = 2048;            // selected rows per (token, split) staged in LDS
+constexpr int KMAX = 2048;            // rows per (token, split): their ids are staged in LDS
 constexpr float TAU = 6.0f;
 
-// tile layout (bytes): 32 code chunks [c][r][16] (chunk-major: each MFMA operand read is one conflict-free
-// ds_read_b128, each V^T operand one ds_read_b64_tr_b8), then the row scales transposed to [g][r] fp32 (the copy
-// writes them in that order: one 4-byte copy per (row, group))
-constexpr int T_SCT = 32 * TR * 16;            // 16384
-constexpr int TILE = T_SCT + 4 * TR * 4;       // 16896
-constexpr int NBUF = 2;
-// Query in LDS (shared by the 4 waves): the rope (64 dims) and latent groups 2, 3 (dims 256..511) of each head;
-// latent groups 0, 1 stay in VGPRs. Row stride padded so 16-byte reads of 32 consecutive heads hit distinct banks.
-constexpr int QRS = (64 + 256) * 2 + 16;       // 656
-constexpr int QPIECES = (64 + 256) / 8;        // 16-byte pieces per head in LDS
-constexpr int L_TILES = 0;
-constexpr int L_QROPE = NW * NBUF * TILE;      // 135168
-constexpr int L_ML = L_QROPE + HG * QRS;       // 156160: per wave m[32], l[32]
-constexpr int L_TOTAL = L_ML + NW * 64 * 4;    // 157184
+// LDS map (bytes)
+constexpr int BF_TILE = TR * 1024;            // bf16 latent tile, swizzled chunks
+constexpr int RP_TILE = TR * 128;             // bf16 rope tile [32 rows][8 chunks], swizzled
+constexpr int SC_TILE = 4 * TR * 4;           // fp32 scales [group][32], row order zrow (see issue_tile)
+constexpr int STG_W = TR * 128;               // e4m3 staging of one wave's group: [part][half][row][16 B]
+constexpr int NBF = 2, NRP = 4, NSTG = 3;     // ring depths
+constexpr int L_BF = 0;
+constexpr int L_RP = L_BF + NBF * BF_TILE;    // 65536
+constexpr int L_SC = L_RP + NRP * RP_TILE;    // 81920
+constexpr int L_STG = L_SC + NRP * SC_TILE;   // 83968
+constexpr int L_QR = L_STG + NSTG * NW * STG_W;   // 133120: query rope, [wave][head][8 chunks] swizzled
+constexpr int L_IDS = L_QR + NW * HB * 128;   // 149504: validated row ids of the split (-1: none)
+constexpr int L_TOTAL = L_IDS + KMAX * 4;     // 157696
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget");
-static_assert(NW * 8 * 4 * 64 * 16 <= L_QROPE, "merge staging (8 output tiles per wave) fits the tile buffers");
 
-// e4m3 pairs -> bf16 / f16 pairs (exact), through the compiler builtins so that the hazard recognizer sees the
-// VALU writes that feed MFMA operands. The packed result is bit-cast whole (extracting single bf16 lanes from
-// the builtin's vector result miscompiles on this toolchain).
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+// Source of invalid and padding rows: zero codes, zero scales, zero rope.
+__device__ __attribute__((aligned(16))) uint8_t zero_row[ROW656];
+
+// bf16 tile: byte offset of chunk c (8 values) of row r
+__device__ inline int gsw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ inline int bf_off(int r, int c) { return r * 1024 + 16 * ((c & ~15) | ((c & 15) ^ gsw(r))); }
+// rope tile and query rope: chunk c (8 values) of row r
+__device__ inline int rp_off(int r, int c) { return r * 128 + 16 * (c ^ ((r >> 1) & 7)); }
+
+// e4m3 pairs -> bf16 pairs (exact), through the compiler builtins so that the hazard recognizer sees the VALU
+// writes. The packed result is bit-cast whole.
 __device__ inline uint32_t fp8lo_bf16x2(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
 }
@@ -71,41 +80,68 @@ __device__ inline uint32_t fp8lo_f16x2(uint32_t w) {
 __device__ inline uint32_t fp8hi_f16x2(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
 }
-// two fp32 -> packed fp16 / bf16, round to nearest even (v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32)
-__device__ inline uint32_t pk_f16(float a, float b) {
-  const f16x2_t v = {(_Float16)a, (_Float16)b};
-  return __builtin_bit_cast(uint32_t, v);
-}
-__device__ inline uint32_t pk_bf16(float a, float b) {
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ inline uint32_t pk_bf16(float a, float b) {      // v_cvt_pk_bf16_f32, round to nearest even
   const bf16x2_t v = {(__bf16)a, (__bf16)b};
   return __builtin_bit_cast(uint32_t, v);
 }
+__device__ inline uint32_t pk_f16(float a, float b) {       // round to nearest even
+  const f16x2_t v = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// 8 bf16 (one 16-byte chunk) -> 8 f16: exact for |x| in [2^-14, 65504] (f16 carries 11 significant bits)
+__device__ inline f16x8 bf16x8_to_f16(u32x4 r) {
+  f16x8 h;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[2 * e] = (_Float16)__builtin_bit_cast(float, r[e] << 16);
+    h[2 * e + 1] = (_Float16)__builtin_bit_cast(float, r[e] & 0xffff0000u);
+  }
+  return h;
+}
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+// The value of lane l ^ 32 (v_permlane32_swap: one VALU op, no LDS round trip).
+__device__ inline float half_swap(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (__lane_id() & 32) ? r[0] : r[1]);
+}
 
 // QK MFMAs with the accumulator in VGPRs. The compiler builtin puts every MFMA result in AGPRs when the function
 // uses AGPRs, which here would evict part of the PV accumulator around each QK phase; inline asm pins the QK
-// accumulator (read by the scale FMAs) to VGPRs. Hazards the compiler cannot see inside asm are covered here:
-// "s_nop 1" before the MFMA for VALU-written operands (2 wait states), and after the last MFMA of a chain
-// 16 wait states before any VALU reads the result (8-pass XDL write -> VALU read). Back-to-back MFMAs of one
-// chain have srcC == vdst exactly, which the hardware forwards.
+// accumulator to VGPRs; the statements are volatile so that they keep their order (with the group combines pinned
+// between them, at most one group partial is live). Hazards the compiler cannot see inside asm are covered here: "s_nop 1" before the MFMA for
+// VALU-written operands (2 wait states), and after the last MFMA of a chain 16 wait states before any VALU reads
+// the result (XDL write -> VALU read). Back-to-back MFMAs of one chain have srcC == vdst exactly (forwarded).
 __device__ inline f32x16 qk_first(bf16x8 a, bf16x8 b) {
   f32x16 d;
-  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
   return d;
 }
 __device__ inline f32x16 qk_next(bf16x8 a, bf16x8 b, f32x16 c) {
-  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
   return c;
 }
-__device__ inline f32x16 qk_last(bf16x8 a, bf16x8 b, f32x16 c) {
-  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7" : "+v"(c) : "v"(a), "v"(b));
+// the same on f16 operands (latent chains)
+__device__ inline f32x16 qkh_first(f16x8 a, f16x8 b) {
+  f32x16 d;
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "v"(b));
+  return d;
+}
+__device__ inline f32x16 qkh_next(f16x8 a, f16x8 b, f32x16 c) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+  return c;
+}
+__device__ inline f32x16 qkh_last(f16x8 a, f16x8 b, f32x16 c) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7" : "+v"(c) : "v"(a), "v"(b));
   return c;
 }
 
-// O *= a for the 256 AGPR accumulator values of a lane, one register at a time through one VGPR. Written as
-// inline asm on the AGPRs: a plain C++ multiply makes the register allocator move the whole accumulator into
-// VGPRs (and spill), although the rescale is a rare path.
+// O *= a for the 256 AGPR accumulator values of a lane, one register at a time through one VGPR (a plain C++
+// multiply makes the register allocator move the whole accumulator into VGPRs; the rescale is a rare path).
 __device__ inline void scale_acc(f32x16 (&O)[16], float a) {
 #pragma unroll
   for (int b = 0; b < 16; ++b)
@@ -123,7 +159,7 @@ struct Params {
   const uint8_t* pool; long long R;               // Row656 rows
   const int* idx; long long idx_st; int K;        // idx[t][k]
   const int* kcount;                              // optional per-token count of leading valid entries
-  int T, H, S, HGN;                               // tokens, heads, splits, head groups
+  int T, H, S, HG;                                // tokens, heads, splits, head groups of 128
   float c;                                        // sm_scale * kv_scale * log2(e)
   float kv_scale;
   uint16_t* out; long long o_st, o_sh;            // bf16 out[t][h][512] (when opart is null)
@@ -132,366 +168,413 @@ struct Params {
   // optional prior partial merged into the bf16 output (S == 1): normalized fp32 o and natural-log lse
   const float* prior_o; long long po_st, po_sh;
   const float* prior_lse; long long pl_st;
-  // request-packed MTP decode (attn_kernel<true>): work item t is a request; its rows are its union list (idx = u,
-  // idx_st = nmax, kcount = union sizes) and mk[t * idx_st + i] is row i's token mask. Column c of a workgroup is
-  // token t0 + (c >> (5 - tsh)) (t0 = cu[t] or t * ql) and head hg * (32 >> tsh) + c % (32 >> tsh); a column's
-  // softmax keeps the rows its token selected. T = total tokens (output rows), NR = requests.
-  const uint8_t* mk; const int* cu; int ql, tsh, NR;
 };
 
-// Copy one tile (32 rows: codes + scales) into the wave's buffer and load the rows' rope into VGPRs.
-// rid: the tile's 32 row ids (-1 = none: such a row copies row 0, which exists whenever a tile is read, and is
-// masked out of the softmax). 18 vector-memory instructions of the copy + 4 rope loads.
-constexpr int VM_PER_TILE = 22;
-__device__ inline void issue_tile(const uint8_t* __restrict__ pool, const SPMLA_LDS int* rid,
-                                  SPMLA_LDS uint8_t* tb, int lane, u32x4 (&rp)[4]) {
-  const int x = rid[lane & 31];
-  const uint8_t* src = pool + (long long)(x >= 0 ? x : 0) * ROW656;
-  const int h = lane >> 5;
+// Copies of tile jj for wave w: the codes of scale group w of the tile's 32 rows (4 x 16 B per lane; staging slot
+// [part i][half][row][16 B] holds e4m3 chunk 8 w + 2 i + half of the row), rows 8 w .. 8 w + 7 of the rope tile (lane
+// l fills stored chunk l % 8 of row 8 w + l / 8), and scale w of all 32 rows: lane l < 32 copies it for row
+// zrow(l) = 8 (l % 4) + 4 (l / 16) + (l / 4) % 4 to float l of the group's 128 bytes (lanes 32 .. 63 are masked off),
+// so that lane 4 hh + b of a group's floats holds rows 8 a + 4 hh + b, a = 0 .. 3, in one 16-byte slot.
+// VM_TILE vector-memory instructions. x0 = id of row lane & 31, x1 = id of row 8 w + lane / 8, x2 = id of row
+// zrow(lane & 31) (read a step ahead, so that issuing the copies waits for nothing).
+constexpr int VM_TILE = 6;
+__device__ inline int zrow(int l) { return 8 * (l & 3) + 4 * ((l >> 4) & 1) + ((l >> 2) & 3); }
+__device__ inline void issue_tile(const Params& p, SPMLA_LDS uint8_t* lds, int jj, int w, int lane, int x0, int x1,
+                                  int x2) {
+  const int hh = lane >> 5, rr = 8 * w + (lane >> 3);
+  const uint8_t* src = (x0 >= 0 ? p.pool + (long long)x0 * ROW656 : zero_row) + (8 * w + hh) * 16;
+  SPMLA_LDS uint8_t* stg = lds + L_STG + ((jj % NSTG) * NW + w) * STG_W;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) dma16(src + (2 * i + h) * 16, tb + i * 1024);
-  // scales: copy e, lane l -> group 2e + h of row l % 32 at float (2e + h) * 32 + l % 32
-  dma4(src + SC_OFF + h * 4, tb + T_SCT);
-  dma4(src + SC_OFF + (2 + h) * 4, tb + T_SCT + 256);
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(src + ROPE_OFF + ks * 32 + h * 16);
+  for (int i = 0; i < 4; ++i) dma16(src + 32 * i, stg + i * 1024);
+  const uint8_t* rsrc = x1 >= 0 ? p.pool + (long long)x1 * ROW656 : zero_row;
+  dma16(rsrc + ROPE_OFF + 16 * ((lane & 7) ^ ((rr >> 1) & 7)), lds + L_RP + (jj % NRP) * RP_TILE + w * 1024);
+  const uint8_t* zsrc = x2 >= 0 ? p.pool + (long long)x2 * ROW656 : zero_row;
+  if (lane < 32) dma4(zsrc + SC_OFF + 4 * w, lds + L_SC + (jj % NRP) * SC_TILE + w * 128);
 }
 
-template <bool PK>
-__global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
+// Row scales as DPP operands. z[a] of lane l = scale g of row 8 a + 4 hh + l % 4 (one 16-byte read per group); value
+// i = 4 a + b of a C-layout accumulator (row 8 a + 4 hh + b) takes its scale from lane 4 (l / 4) + b of the same quad
+// (quad_perm b,b,b,b), so one register per a serves the four rows of a quad. "s_nop 1": a VALU write of the DPP source needs 2 wait
+// states before the DPP read (the compiler cannot see inside asm).
+// s[4 A + b] += z (row of value 4 A + b) * x[4 A + b], b = 0..3
+template <int A>
+__device__ inline void fmac4_dpp(f32x16& s, float z, const f32x16& x) {
+  asm volatile("s_nop 1\n\t"
+               "v_fmac_f32_dpp %0, %4, %5 quad_perm:[0,0,0,0] row_mask:0xf bank_mask:0xf\n\t"
+               "v_fmac_f32_dpp %1, %4, %6 quad_perm:[1,1,1,1] row_mask:0xf bank_mask:0xf\n\t"
+               "v_fmac_f32_dpp %2, %4, %7 quad_perm:[2,2,2,2] row_mask:0xf bank_mask:0xf\n\t"
+               "v_fmac_f32_dpp %3, %4, %8 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf"
+               : "+v"(s[4 * A]), "+v"(s[4 * A + 1]), "+v"(s[4 * A + 2]), "+v"(s[4 * A + 3])
+               : "v"(z), "v"(x[4 * A]), "v"(x[4 * A + 1]), "v"(x[4 * A + 2]), "v"(x[4 * A + 3]));
+}
+// P' of values 4 A .. 4 A + 3: (p z) with the row scales as above, as two packed f16 pairs (elements 2 (A & 1) and
+// 2 (A & 1) + 1 of the operand dst)
+template <int A>
+__device__ inline void mul4_dpp_f16(u32x4& dst, float z, const float (&p)[16]) {
+  const float p0 = p[4 * A], p1 = p[4 * A + 1], p2 = p[4 * A + 2], p3 = p[4 * A + 3];
+  float t0, t1, t2, t3;
+  asm volatile("s_nop 1\n\t"
+               "v_mul_f32_dpp %0, %4, %5 quad_perm:[0,0,0,0] row_mask:0xf bank_mask:0xf\n\t"
+               "v_mul_f32_dpp %1, %4, %6 quad_perm:[1,1,1,1] row_mask:0xf bank_mask:0xf\n\t"
+               "v_mul_f32_dpp %2, %4, %7 quad_perm:[2,2,2,2] row_mask:0xf bank_mask:0xf\n\t"
+               "v_mul_f32_dpp %3, %4, %8 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf"
+               : "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+               : "v"(z), "v"(p0), "v"(p1), "v"(p2), "v"(p3));
+  dst[2 * (A & 1)] = pk_f16(t0, t1);
+  dst[2 * (A & 1) + 1] = pk_f16(t2, t3);
+}
+
+// Staged part i of wave w's group of tile jj: 16 codes of row r = lane & 31, e4m3 chunk 8 w + 2 i + hh = bf16 chunks
+// c = 16 w + 4 i + 2 hh + b (b = 0, 1). Byte offset of chunk c in the swizzled tile: r * 1024 + 256 w +
+// ((64 i + 16 b) ^ key), key = 32 hh ^ 16 gsw(r) (one xor-add per write). The 16 lanes of one LDS cycle (rows r0 ..
+// r0 + 15, one chunk) land on 16 distinct 16-byte bank groups.
+__device__ inline u32x4 read_part(SPMLA_LDS uint8_t* lds, int jj, int w, int lane, int i) {
+  return *(SPMLA_LDS u32x4*)(lds + L_STG + ((jj % NSTG) * NW + w) * STG_W + i * 1024 + lane * 16);
+}
+__device__ inline void write_part(SPMLA_LDS uint8_t* lds, int jj, int w, const int (&wo)[2], int i, u32x4 v) {
+  u32x4 a, b;
+  a[0] = fp8lo_f16x2(v[0]); a[1] = fp8hi_f16x2(v[0]); a[2] = fp8lo_f16x2(v[1]); a[3] = fp8hi_f16x2(v[1]);
+  b[0] = fp8lo_f16x2(v[2]); b[1] = fp8hi_f16x2(v[2]); b[2] = fp8lo_f16x2(v[3]); b[3] = fp8hi_f16x2(v[3]);
+  // wo[0] = r * 1024 (row base), wo[1] = key
+  SPMLA_LDS uint8_t* bf = lds + L_BF + (jj & 1) * BF_TILE + 256 * w;
+  *(SPMLA_LDS u32x4*)(bf + wo[0] + ((64 * i) ^ wo[1])) = a;
+  *(SPMLA_LDS u32x4*)(bf + wo[0] + ((64 * i + 16) ^ wo[1])) = b;
+}
+
+__global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_generic[];
   SPMLA_LDS uint8_t* lds = (SPMLA_LDS uint8_t*)smem_generic;
 
-  const int nwork = (PK ? p.NR : p.T) * p.S * p.HGN;
+  const int nwork = p.T * p.S * p.HG;
   const int f = remap_xcd(blockIdx.x, nwork);
   if (f < 0) return;
-  const int hg = f % p.HGN;
-  const int ts = f / p.HGN;
+  const int hg = f % p.HG;
+  const int ts = f / p.HG;
   const int s = ts % p.S;
   const int t = ts / p.S;
-  // columns -> (token, head): 32 heads of token t, or (packed) 2^tsh tokens of request t x (32 >> tsh) heads
-  int t0 = t, ntok = 1;
-  if (PK) {
-    t0 = p.cu ? p.cu[t] : min(t * p.ql, p.T);
-    const int t1 = p.cu ? p.cu[t + 1] : min(t0 + p.ql, p.T);
-    ntok = min(max(t1 - t0, 0), min(1 << p.tsh, 6));
-  }
-  const int csh = PK ? 5 - p.tsh : 5;          // log2 heads per token in a workgroup
-  auto col_tok = [&](int c) -> int { return PK ? t0 + (c >> csh) : t; };
-  auto col_head = [&](int c) -> int { return PK ? (hg << csh) + (c & ((1 << csh) - 1)) : hg * HG + c; };
-  auto col_ok = [&](int c) -> bool { return (!PK || (c >> csh) < ntok) && col_head(c) < p.H; };
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar control flow
-  const int half = lane >> 5, l32 = lane & 31;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int hbase = hg * HGW + w * HB;                      // first head of this wave
+  const bool wact = hbase < p.H;                            // the wave has heads (uniform)
+  const int h = hbase + l32;
+  const bool hval = h < p.H;
 
   // ---- row range of this split
   const int kc = ((p.K + p.S - 1) / p.S + TR - 1) / TR * TR;
   const int kb = s * kc;
   int ke = kb + kc < p.K ? kb + kc : p.K;
-  if (p.kcount) { const int c = p.kcount[t]; ke = ke < c ? ke : c; }
+  if (p.kcount) { const int cc = p.kcount[t]; ke = ke < cc ? ke : cc; }
   const int nrow = ke > kb ? ke - kb : 0;
   const int ntile = p.R > 0 ? (nrow + TR - 1) / TR : 0;     // no rows to read: o = 0, lse = -inf
 
-  SPMLA_LDS uint8_t* qrope = lds + L_QROPE;
-
-  // ---- prologue, two memory round trips: (1) the row ids of this wave's first two tiles and the query parts
-  // that go to LDS; (2) the first tile's copy, its rope and the latent query fragments (in flight while the query
-  // staging is written). Row ids of later tiles are loaded one tile ahead, into registers.
+  // ---- prologue: validated row ids -> LDS, query rope -> LDS, query latent -> VGPRs (B operands: lane holds head
+  // l32, dims 16 ks + 8 hh .. + 7 of MFMA ks)
   const int* idxrow = p.idx + (long long)t * p.idx_st + kb;
-  const int h = col_head(l32);
-  const bool hval = col_ok(l32);
-  const uint8_t* mkrow = PK ? p.mk + (long long)t * p.idx_st + kb : nullptr;
-  auto mk_raw = [&](int tile) -> uint32_t {   // token mask of this lane's row in `tile` (packed decode)
-    const int i = tile * TR + l32;
-    uint32_t m = 0u;
-    if (PK && i < nrow) m = mkrow[i];
-    return m;
-  };
-  auto row_raw = [&](int tile) -> int {       // index entry of this lane's row in `tile` (-1: past the end)
-    const int i = tile * TR + l32;
+  int xs[KMAX / 256];
+#pragma unroll
+  for (int k = 0; k < KMAX / 256; ++k) {
+    const int i = tid + 256 * k;
     int x = -1;
     if (i < nrow) x = idxrow[i];
-    return x;
-  };
-  auto row_ok = [&](int x) -> int { return (x >= 0 && (long long)x < p.R) ? x : -1; };   // -1: none / invalid
-  int rcur = row_ok(row_raw(w)), rnxt = row_ok(row_raw(w + NW));
-  int rnn = -1;                        // raw entry two tiles ahead: loaded in one iteration, checked in the next
-  uint32_t mcur = mk_raw(w), mnxt = mk_raw(w + NW), mnn = 0u;
+    xs[k] = (x >= 0 && (long long)x < p.R) ? x : -1;
+  }
+  const uint16_t* qrow = p.q + (long long)t * p.q_st + (long long)(hval ? h : 0) * p.q_sh;
+  const uint32_t qmask = hval ? 0xffffffffu : 0u;          // heads past H: zero query
+  f16x8 qf[32];
+#pragma unroll
+  for (int ks = 0; ks < 32; ++ks) qf[ks] = bf16x8_to_f16(*(const u32x4*)(qrow + 16 * ks + 8 * hh) & qmask);
+  u32x4 qrv[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {                              // rope: 32 heads x 8 chunks, 4 per lane
+    const int cc = lane + 64 * k, qh = hbase + (cc >> 3);
+    const bool ok = qh < p.H;
+    const uint16_t* src = p.q + (long long)t * p.q_st + (long long)(ok ? qh : 0) * p.q_sh + D_LAT + 8 * (cc & 7);
+    qrv[k] = *(const u32x4*)src & (ok ? 0xffffffffu : 0u);
+  }
+  wait_vm<0>();
+  SPMLA_LDS int* ids = (SPMLA_LDS int*)(lds + L_IDS);
+#pragma unroll
+  for (int k = 0; k < KMAX / 256; ++k) {
+    const int i = tid + 256 * k;
+    if (i < ntile * TR) ids[i] = xs[k];
+  }
+  SPMLA_LDS uint8_t* qr = lds + L_QR + w * (HB * 128);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int cc = lane + 64 * k;
+    *(SPMLA_LDS u32x4*)(qr + rp_off(cc >> 3, cc & 7)) = qrv[k];
+  }
+  lds_barrier();
+
+  int wo[2];                                                // conversion write row base and key (see write_part)
   {
-    u32x4 qv[HG * QPIECES / 256];
-#pragma unroll
-    for (int k = 0; k < HG * QPIECES / 256; ++k) {          // 32 heads x 40 pieces (rope, latent groups 2, 3)
-      const int i = tid + 256 * k, qh = i / QPIECES, part = i % QPIECES;
-      const bool ok = col_ok(qh);
-      const uint16_t* qsrc = p.q + (long long)(ok ? col_tok(qh) : 0) * p.q_st + (long long)(ok ? col_head(qh) : 0) * p.q_sh;
-      const uint16_t* src = part < 8 ? qsrc + D_LAT + part * 8 : qsrc + 2 * QGROUP + (part - 8) * 8;
-      qv[k] = *(const u32x4*)src & (ok ? 0xffffffffu : 0u);
-    }
-    wait_vm<0>();
-#pragma unroll
-    for (int k = 0; k < HG * QPIECES / 256; ++k) {
-      const int i = tid + 256 * k;
-      *(SPMLA_LDS u32x4*)(qrope + (i / QPIECES) * QRS + (i % QPIECES) * 16) = qv[k];
-    }
+    const int r = lane & 31;
+    wo[0] = r * 1024;
+    wo[1] = 32 * hh ^ 16 * gsw(r);
   }
-  const int ntw = ntile > w ? (ntile - w + NW - 1) / NW : 0;   // tiles w, w + 4, ...
-  SPMLA_LDS uint8_t* mybuf = lds + L_TILES + w * NBUF * TILE;
-  u32x4 rp[4];
-  if (ntw > 0) {
-    const uint8_t* src = p.pool + (long long)(rcur >= 0 ? rcur : 0) * ROW656;
+  // ---- copies of tiles 0, 1, 2; tile 0 converted
+  const int r_dma1 = 8 * w + (lane >> 3);                    // the rope row this lane copies
+  const int r_dma2 = zrow(lane & 31);                        // the row whose scale this lane copies
 #pragma unroll
-    for (int i = 0; i < 16; ++i) dma16(src + (2 * i + half) * 16, mybuf + i * 1024);
-    dma4(src + SC_OFF + half * 4, mybuf + T_SCT);
-    dma4(src + SC_OFF + (2 + half) * 4, mybuf + T_SCT + 256);
+  for (int jj = 0; jj < 3; ++jj)
+    if (jj < ntile)
+      issue_tile(p, lds, jj, w, lane, ids[jj * TR + (lane & 31)], ids[jj * TR + r_dma1], ids[jj * TR + r_dma2]);
+  // row ids of tile 3 (the first copies the loop issues)
+  int nx0 = 3 < ntile ? ids[3 * TR + (lane & 31)] : -1, nx1 = 3 < ntile ? ids[3 * TR + r_dma1] : -1;
+  int nx2 = 3 < ntile ? ids[3 * TR + r_dma2] : -1;
+  if (ntile > 0) {
+    if (ntile >= 3) wait_vm<2 * VM_TILE>();
+    else if (ntile == 2) wait_vm<VM_TILE>();
+    else wait_vm<0>();
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(src + ROPE_OFF + ks * 32 + half * 16);
+    for (int i = 0; i < 4; ++i) write_part(lds, 0, w, wo, i, read_part(lds, 0, w, lane, i));
   }
-  // latent query fragments of groups 0, 1 (bf16 B operands), k-pair kp (32 dims = chunks 2kp, 2kp + 1): lane half
-  // h holds the dims of chunk 2kp + h; MFMA 2kp + e uses its bytes 8e .. 8e + 7 (the K operand is read the same
-  // way). They are waited for with the first tile.
-  const uint16_t* qrow = p.q + (long long)(hval ? col_tok(l32) : 0) * p.q_st + (long long)(hval ? h : 0) * p.q_sh;
-  bf16x8 qf[16];
-  const uint32_t qmask = hval ? 0xffffffffu : 0u;       // heads past H: zero query (row 0 is read instead)
-#pragma unroll
-  for (int kp = 0; kp < 8; ++kp) {
-    const uint16_t* src = qrow + (2 * kp + half) * 16;
-    const u32x4 a = *(const u32x4*)src & qmask;
-    const u32x4 b = *(const u32x4*)(src + 8) & qmask;
-    qf[2 * kp] = __builtin_bit_cast(bf16x8, a);
-    qf[2 * kp + 1] = __builtin_bit_cast(bf16x8, b);
-  }
-  lds_barrier();                                // query staging visible to all waves (copies stay in flight)
-  wait_vm<0>();                                 // query fragments (and the first tile) landed
+  lds_barrier();
 
   const float c = p.c;
   float m_run = -__builtin_inff();     // reference max of this lane's head (log2 units)
   float l_run = 0.f;                   // sum of p over this lane's 16 rows of every tile
   bool started = false;                // wave-uniform: O holds contributions
+  int eps = 0;                         // P, O and l_run carry a factor 2^-eps (f16 range of P')
+  float elim = 0.f;                    // 2^(9 + eps) once eps is set
 
   f32x16 O[16];
 #pragma unroll
   for (int b = 0; b < 16; ++b) O[b] = f32x16{};
 
-  // per-lane V^T transpose-read address (16-lane group G reads 8 rows x 16 columns: lane 2i + c supplies row i,
-  // bytes 8c .. 8c + 7; the rows follow the C-layout rows of the lane's P values)
-  const int G = lane >> 4, gi = (lane & 15) >> 1, gc = lane & 1;
-  const int tr_off = ((G & 1) * 32 + 8 * (gi >> 2) + 4 * (G >> 1) + (gi & 3)) * 16 + gc * 8;
+  // QK operand of MFMA u = 8 g + kk: row l32, chunk 2 u + hh at l32 * 1024 + 256 g + ((32 kk) ^ qk_key) (one xor-add
+  // per read; 32 kk and 16 hh occupy disjoint bits, so 16 ((2 kk + hh) ^ gsw) = (32 kk) ^ (16 hh ^ 16 gsw))
+  const int qk_base = l32 * 1024, qk_key = 16 * (hh ^ gsw(l32));
+  // PV transposed reads (ds_read_b64_tr_b16): in each 16-lane group G the source lane 4k + q reads 4 values of
+  // row 16 ks + 8 r + 4 (G >> 1) + k, dims 32 mt + 16 (G & 1) + 4 q .. + 3; result lane i of the group receives
+  // value k from source lane 4k + i / 4, so lane L ends with V^T[32 mt + L % 32][8 (L / 32) + 4 r + k], the K order of
+  // the P' operand (row 16 ks + 8 (e / 4) + 4 (L / 32) + e % 4 for e = 4 r + k).
+  // (offset of read r of block m4 = pv_base[r] + ((64 m4) ^ pv_key): 64 (m4 ^ k) = (64 m4) ^ (64 k))
+  int pv_base[2], pv_key;
+  {
+    const int G = lane >> 4, k = (lane & 15) >> 2, q = lane & 3;
+    const int rl = 4 * (G >> 1) + k, cl = 2 * (G & 1) + (q >> 1);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) pv_base[r] = (8 * r + rl) * 1024 + 16 * (cl ^ ((2 * r + (G >> 1)) & 3)) + 8 * (lane & 1);
+    pv_key = 64 * k;
+  }
 
 #pragma unroll 1
-  for (int j = 0; j < ntw; ++j) {
-    wait_vm<0>();                               // tile j copied, its rope loaded
-    SPMLA_LDS uint8_t* tb = mybuf + (j & 1) * TILE;
-    const int tix = w + NW * j;
-
-    // ---- first LDS reads of the tile: query rope, K group 0, the row ids of this and of the next tile
-    u32x4 qr[4], kr[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qr[ks] = *(SPMLA_LDS u32x4*)(qrope + l32 * QRS + (16 * ks + 8 * half) * 2);
-#pragma unroll
-    for (int kq = 0; kq < 4; ++kq) kr[kq] = *(SPMLA_LDS u32x4*)(tb + (2 * kq + half) * 512 + l32 * 16);
-    const bool more = j + 1 < ntw;
-    // the entries loaded one iteration ago are checked only now, after the wait above: checking them where they
-    // are loaded would stall every tile on a global-memory round trip
-    if (j > 0) { rnxt = row_ok(rnn); mnxt = mnn; }
-    rnn = j + 2 < ntw ? row_raw(tix + 2 * NW) : -1;
-    if (PK) mnn = j + 2 < ntw ? mk_raw(tix + 2 * NW) : 0u;
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- rope part of S^T (operands in VGPRs / LDS)
-    f32x16 S;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 a = __builtin_bit_cast(bf16x8, rp[ks]), b = __builtin_bit_cast(bf16x8, qr[ks]);
-      S = ks == 0 ? qk_first(a, b) : (ks == 3 ? qk_last(a, b, S) : qk_next(a, b, S));
+  for (int j = 0; j < ntile; ++j) {
+    const bool nxt = j + 1 < ntile;        // tile j + 1 is converted during this step
+    if (nxt) {                             // its copies have landed (the copies of tile j + 2 may stay in flight)
+      if (j + 2 < ntile) wait_vm<VM_TILE>();
+      else wait_vm<0>();
     }
-    const unsigned vmask = (unsigned)__ballot(rcur >= 0);  // rows of the tile that exist
-    // the next tile's copy is issued in four parts, one per latent group, between that group's MFMAs
-    const uint8_t* nsrc = p.pool + (long long)(rnxt >= 0 ? rnxt : 0) * ROW656;
-    SPMLA_LDS uint8_t* nbuf = mybuf + ((j + 1) & 1) * TILE;
+    SPMLA_LDS uint8_t* bf = lds + L_BF + (j & 1) * BF_TILE;
+    SPMLA_LDS uint8_t* rp = lds + L_RP + (j % NRP) * RP_TILE;
+    SPMLA_LDS uint8_t* scb = lds + L_SC + (j % NRP) * SC_TILE;
 
-    // ---- latent part of S^T: group g = chunks 8g .. 8g + 7; group g + 1's K is read while group g's MFMAs run
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32x4 kn[4];
-      if (g < 3) {
-#pragma unroll
-        for (int kq = 0; kq < 4; ++kq) kn[kq] = *(SPMLA_LDS u32x4*)(tb + (2 * (4 * g + 4 + kq) + half) * 512 + l32 * 16);
-      }
-      if (more) {                                  // part g of the next tile's copy
-#pragma unroll
-        for (int i = 4 * g; i < 4 * g + 4; ++i) dma16(nsrc + (2 * i + half) * 16, nbuf + i * 1024);
-        if (g == 3) {
-          dma4(nsrc + SC_OFF + half * 4, nbuf + T_SCT);
-          dma4(nsrc + SC_OFF + (2 + half) * 4, nbuf + T_SCT + 256);
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(nsrc + ROPE_OFF + ks * 32 + half * 16);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      f32x16 acc;
-#pragma unroll
-      for (int kq = 0; kq < 4; ++kq) {
-        const int kp = 4 * g + kq;
-        const u32x4 raw = kr[kq];
-        i32x4 a0, a1;
-        a0[0] = (int)fp8lo_bf16x2(raw[0]); a0[1] = (int)fp8hi_bf16x2(raw[0]);
-        a0[2] = (int)fp8lo_bf16x2(raw[1]); a0[3] = (int)fp8hi_bf16x2(raw[1]);
-        a1[0] = (int)fp8lo_bf16x2(raw[2]); a1[1] = (int)fp8hi_bf16x2(raw[2]);
-        a1[2] = (int)fp8lo_bf16x2(raw[3]); a1[3] = (int)fp8hi_bf16x2(raw[3]);
-        bf16x8 b0, b1;
-        if (g < 2) {
-          b0 = qf[2 * kp];
-          b1 = qf[2 * kp + 1];
-        } else {                                   // dims 16 (2kp + half) + 8e of latent groups 2, 3, from LDS
-          const SPMLA_LDS uint8_t* qp = qrope + l32 * QRS + 128 + ((2 * kp + half) * 16 - 2 * QGROUP) * 2;
-          b0 = __builtin_bit_cast(bf16x8, *(const SPMLA_LDS u32x4*)qp);
-          b1 = __builtin_bit_cast(bf16x8, *(const SPMLA_LDS u32x4*)(qp + 16));
-        }
-        acc = kq == 0 ? qk_first(__builtin_bit_cast(bf16x8, a0), b0) : qk_next(__builtin_bit_cast(bf16x8, a0), b0, acc);
-        acc = kq == 3 ? qk_last(__builtin_bit_cast(bf16x8, a1), b1, acc) : qk_next(__builtin_bit_cast(bf16x8, a1), b1, acc);
-      }
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x4 sg = *(SPMLA_LDS f32x4*)(tb + T_SCT + (g * 32 + 8 * qd + 4 * half) * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) S[4 * qd + e] = __builtin_fmaf(acc[4 * qd + e], sg[e], S[4 * qd + e]);
-      }
-      if (g < 3) {
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) kr[q4] = kn[q4];
-      }
-    }
-
-    // ---- PV operands of group 0 (scales, V^T codes) read while the softmax runs
-    f32x4 ps[4];
-    i32x2 tv[8];
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) ps[qd] = *(SPMLA_LDS f32x4*)(tb + T_SCT + (8 * qd + 4 * half) * 4);
-#pragma unroll
-    for (int f8 = 0; f8 < 8; ++f8)
-      tv[f8] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((SPMLA_LDS i32x2*)(tb + (f8 >> 1) * 1024 + (f8 & 1) * 256 + tr_off));
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- rows that do not exist: -inf (C-layout row of value i: 8 (i / 4) + 4 half + i % 4)
-    unsigned rm = vmask;                                 // rows of the tile this lane's column may use
-    if (PK) {                                            // its token's rows (padding tokens: every row)
-      const int ct = l32 >> csh;
-      for (int jt = 0; jt < ntok; ++jt) {
-        const unsigned bj = (unsigned)__ballot(rcur >= 0 && ((mcur >> jt) & 1u));
-        if (ct == jt) rm = bj;
-      }
-    }
-    const bool anymask = PK ? __ballot(rm != 0xffffffffu) != 0ull : vmask != 0xffffffffu;
-    if (__builtin_expect(anymask, 0)) {                  // rare: keep it a branch, not 48 selects per tile
-      asm volatile("" ::: "memory");
-      const unsigned lm = rm >> (4 * half);
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (!((lm >> (8 * (i >> 2) + (i & 3))) & 1u)) S[i] = -__builtin_inff();
-    }
-
-    // ---- online softmax of this lane's head
-    float mx = S[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, S[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;             // c > 0; -inf stays -inf
-    const bool need = mx > m_run + TAU;                      // also true for the first finite tile
-    if (__ballot(need)) {
-      const float mn = need ? mx : m_run;
-      const float alpha = need ? (m_run > -__builtin_inff() ? __builtin_amdgcn_exp2f(m_run - mn) : 0.f) : 1.f;
-      l_run *= alpha;
-      if (started) scale_acc(O, alpha);
-      m_run = mn;
-    }
-    const float mref = m_run > -__builtin_inff() ? m_run : 0.f;
-    float P[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      P[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[i], c, -mref));   // exp2(-inf) = 0
-      l_run += P[i];
-    }
-    started = true;
-
-    // ---- PV: output columns of group g use P' = P * scale(row, g) (fp16). Group g + 1's scales and V^T codes are
-    // read at the start of group g and its P' is formed between group g's MFMAs, so that VALU work overlaps the
-    // matrix core instead of preceding each group's first MFMA.
-    auto p_scaled = [&](const f32x4* sc, f16x8* pb) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const f32x4 s0 = sc[2 * ks], s1 = sc[2 * ks + 1];
-        const float* pp = P + 8 * ks;
-        i32x4 o;
-        o[0] = (int)pk_f16(pp[0] * s0[0], pp[1] * s0[1]);
-        o[1] = (int)pk_f16(pp[2] * s0[2], pp[3] * s0[3]);
-        o[2] = (int)pk_f16(pp[4] * s1[0], pp[5] * s1[1]);
-        o[3] = (int)pk_f16(pp[6] * s1[2], pp[7] * s1[3]);
-        pb[ks] = __builtin_bit_cast(f16x8, o);
-      }
+    // ---- S^T of tile j: the rope chain (4 MFMAs) into S, then latent group g (8 MFMAs) into acc[g & 1], its fp32
+    // scales combined into S during group g + 1 (group 3's after the last MFMA). With one wave per SIMD only a few
+    // VALU instructions hide behind each MFMA, so all side work is cut into slices of that size, one slice per MFMA
+    // (a scheduling fence after every MFMA keeps the slices where they are): the K reads (D MFMAs ahead), the
+    // conversion of tile j + 1 (part g: staged read in group g - 1, 4 + 4 conversions and two writes in group g), the
+    // combine of the previous group, and the copies of tile j + 3. Waves without heads compute on a zero query.
+    constexpr int D = 2;
+    auto kread = [&](int u) -> f16x8 {
+      return __builtin_bit_cast(f16x8, *(SPMLA_LDS u32x4*)(bf + 256 * (u >> 3) + qk_base + ((32 * (u & 7)) ^ qk_key)));
     };
-    f16x8 pb[2];
-    p_scaled(ps, pb);
+    auto rread = [&](int ks, bf16x8& ra, bf16x8& rb) {
+      ra = __builtin_bit_cast(bf16x8, *(SPMLA_LDS u32x4*)(rp + rp_off(l32, 2 * ks + hh)));
+      rb = __builtin_bit_cast(bf16x8, *(SPMLA_LDS u32x4*)(qr + rp_off(l32, 2 * ks + hh)));
+    };
+    SPMLA_LDS uint8_t* cbf = lds + L_BF + ((j + 1) & 1) * BF_TILE + 256 * w;   // conversion target (tile j + 1)
+    // (past the last tile the staged bytes are stale and are converted into the unused buffer)
+    u32x4 cv = read_part(lds, j + 1, w, lane, 0);
+    bf16x8 ra[4], rb[4];
+    rread(0, ra[0], rb[0]);
+    // row scales of group g of tile j as DPP operands (see fmac4_dpp)
+    auto zload = [&](int g) -> f32x4 { return *(SPMLA_LDS f32x4*)(scb + g * 128 + (4 * hh + (lane & 3)) * 16); };
+    f32x4 zq, zq3;
+    float smx = 0.f;                       // largest row scale of the tile seen by this lane
+    f16x8 kr[4];
+    f32x16 S, acc[2];
+    u32x4 cva;                             // converted half of the current part
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      f32x4 pn[4];
-      i32x2 vn[8];
-      if (g < 3) {
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) pn[qd] = *(SPMLA_LDS f32x4*)(tb + T_SCT + ((g + 1) * 32 + 8 * qd + 4 * half) * 4);
-#pragma unroll
-        for (int f8 = 0; f8 < 8; ++f8)
-          vn[f8] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-              (SPMLA_LDS i32x2*)(tb + (4 * (g + 1) + (f8 >> 1)) * 1024 + (f8 & 1) * 256 + tr_off));
+    for (int t = 0; t < 36; ++t) {
+      if (t < 4) {                          // ---- rope chain
+        if (t + 1 < 4) rread(t + 1, ra[t + 1], rb[t + 1]);
+        if (t + D - 4 >= 0) kr[(t + D - 4) & 3] = kread(t + D - 4);
+        if (t == 0) kr[0] = kread(0);
+        S = t == 0 ? qk_first(ra[0], rb[0]) : qk_next(ra[t], rb[t], S);
+      } else {                              // ---- latent MFMA u = 8 g + kk
+        const int u = t - 4, g = u >> 3, kk = u & 7;
+        if (u + D < 32) kr[(u + D) & 3] = kread(u + D);
+        // conversion of part g of tile j + 1
+        if (kk == 1) {
+          cva[0] = fp8lo_f16x2(cv[0]); cva[1] = fp8hi_f16x2(cv[0]); cva[2] = fp8lo_f16x2(cv[1]); cva[3] = fp8hi_f16x2(cv[1]);
+        }
+        if (kk == 2) {
+          *(SPMLA_LDS u32x4*)(cbf + wo[0] + ((64 * g) ^ wo[1])) = cva;
+          cva[0] = fp8lo_f16x2(cv[2]); cva[1] = fp8hi_f16x2(cv[2]); cva[2] = fp8lo_f16x2(cv[3]); cva[3] = fp8hi_f16x2(cv[3]);
+        }
+        if (kk == 3) *(SPMLA_LDS u32x4*)(cbf + wo[0] + ((64 * g + 16) ^ wo[1])) = cva;
+        if (kk == 6 && g < 3) cv = read_part(lds, j + 1, w, lane, g + 1);
+        // combine of group g - 1: quarter qd = kk - 4 at kk 4 .. 7 (at least 4 MFMAs after the group's last one, so
+        // the XDL-write -> VALU-read distance holds)
+        if (g >= 1 && kk == 0) zq = zload(g - 1);
+        if (g >= 1 && kk == 1) smx = fmaxf(fmaxf(smx, fmaxf(zq[0], zq[1])), fmaxf(zq[2], zq[3]));
+        if (g >= 1 && kk >= 4) {
+          const f32x16& ap = acc[(g - 1) & 1];
+          if (kk == 4) fmac4_dpp<0>(S, zq[0], ap);
+          if (kk == 5) fmac4_dpp<1>(S, zq[1], ap);
+          if (kk == 6) fmac4_dpp<2>(S, zq[2], ap);
+          if (kk == 7) fmac4_dpp<3>(S, zq[3], ap);
+        }
+        if (g == 3 && kk == 7) zq3 = zload(3);
+        // copies of tile j + 3 (row ids read one step ahead)
+        if (kk == 7 && g == 0 && j + 3 < ntile) {
+          const uint8_t* dsrc = (nx0 >= 0 ? p.pool + (long long)nx0 * ROW656 : zero_row) + (8 * w + hh) * 16;
+          SPMLA_LDS uint8_t* stg = lds + L_STG + (((j + 3) % NSTG) * NW + w) * STG_W;
+          dma16(dsrc, stg);
+          dma16(dsrc + 32, stg + 1024);
+        }
+        if (kk == 7 && g == 1 && j + 3 < ntile) {
+          const uint8_t* dsrc = (nx0 >= 0 ? p.pool + (long long)nx0 * ROW656 : zero_row) + (8 * w + hh) * 16;
+          const uint8_t* rsrc = nx1 >= 0 ? p.pool + (long long)nx1 * ROW656 : zero_row;
+          SPMLA_LDS uint8_t* stg = lds + L_STG + (((j + 3) % NSTG) * NW + w) * STG_W;
+          dma16(dsrc + 64, stg + 2048);
+          dma16(dsrc + 96, stg + 3072);
+          const int rr = r_dma1;
+          dma16(rsrc + ROPE_OFF + 16 * ((lane & 7) ^ ((rr >> 1) & 7)), lds + L_RP + ((j + 3) % NRP) * RP_TILE + w * 1024);
+          const uint8_t* zsrc = nx2 >= 0 ? p.pool + (long long)nx2 * ROW656 : zero_row;
+          if (lane < 32) dma4(zsrc + SC_OFF + 4 * w, lds + L_SC + ((j + 3) % NRP) * SC_TILE + w * 128);
+        }
+        if (kk == 7 && g == 2) {
+          nx0 = j + 4 < ntile ? ids[(j + 4) * TR + (lane & 31)] : -1;   // ids of tile j + 4, used next step
+          nx1 = j + 4 < ntile ? ids[(j + 4) * TR + r_dma1] : -1;
+          nx2 = j + 4 < ntile ? ids[(j + 4) * TR + r_dma2] : -1;
+        }
+        const f16x8 ka = kr[u & 3];
+        if (kk == 0) acc[g & 1] = qkh_first(ka, qf[u]);
+        else if (u == 31) acc[1] = qkh_last(ka, qf[u], acc[1]);
+        else acc[g & 1] = qkh_next(ka, qf[u], acc[g & 1]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      f16x8 pbn[2];
+    }
+    {                                        // combine of group 3 (after qkh_last's wait states)
+      smx = fmaxf(fmaxf(smx, fmaxf(zq3[0], zq3[1])), fmaxf(zq3[2], zq3[3]));
+      fmac4_dpp<0>(S, zq3[0], acc[1]);
+      fmac4_dpp<1>(S, zq3[1], acc[1]);
+      fmac4_dpp<2>(S, zq3[2], acc[1]);
+      fmac4_dpp<3>(S, zq3[3], acc[1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    {
+      // ---- rows that do not exist: -inf (C-layout row of value i: 8 (i / 4) + 4 hh + i % 4)
+      const unsigned vmask = (unsigned)__ballot(ids[j * TR + l32] >= 0);
+      if (__builtin_expect(vmask != 0xffffffffu, 0)) {     // rare: keep it a branch, not 16 selects per tile
+        asm volatile("" ::: "memory");
+        const unsigned lm = vmask >> (4 * hh);
 #pragma unroll
-      for (int f8 = 0; f8 < 8; ++f8) {
-        const int mt = 4 * g + (f8 >> 1), ks = f8 & 1;     // output columns 32 mt .. 32 mt + 31, rows 16 ks ..
-        const i32x2 raw = tv[f8];
-        i32x4 a;
-        a[0] = (int)fp8lo_f16x2((uint32_t)raw[0]); a[1] = (int)fp8hi_f16x2((uint32_t)raw[0]);
-        a[2] = (int)fp8lo_f16x2((uint32_t)raw[1]); a[3] = (int)fp8hi_f16x2((uint32_t)raw[1]);
-        O[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), pb[ks], O[mt], 0, 0, 0);
-        if (f8 == 3 && g < 3) p_scaled(pn, pbn);          // next group's P', behind four MFMAs
+        for (int i = 0; i < 16; ++i)
+          if (!((lm >> (8 * (i >> 2) + (i & 3))) & 1u)) S[i] = -__builtin_inff();
       }
-      if (g < 3) {
-        pb[0] = pbn[0];
-        pb[1] = pbn[1];
+
+      // ---- online softmax of this lane's head (tree reductions)
+      float m8[8];
 #pragma unroll
-        for (int f8 = 0; f8 < 8; ++f8) tv[f8] = vn[f8];
+      for (int i = 0; i < 8; ++i) m8[i] = fmaxf(S[i], S[i + 8]);
+      float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[4]), fmaxf(m8[1], m8[5])), fmaxf(fmaxf(m8[2], m8[6]), fmaxf(m8[3], m8[7])));
+      mx = fmaxf(mx, half_swap(mx)) * c;                       // c > 0; -inf stays -inf
+      const bool need = mx > m_run + TAU;                      // also true for the first finite tile
+      if (__ballot(need)) {
+        const float mn = need ? mx : m_run;
+        const float alpha = need ? (m_run > -__builtin_inff() ? __builtin_amdgcn_exp2f(m_run - mn) : 0.f) : 1.f;
+        l_run *= alpha;
+        if (started) scale_acc(O, alpha);
+        m_run = mn;
+      }
+      // ---- f16 range of P' = P * scale: P carries a factor 2^-eps (O and l_run too; the lse adds eps back), so that
+      // P' < 2^TAU * 2^9 = 2^15 while every row scale of the tile is below 2^(9 + eps). eps is set by the first tile
+      // with a positive scale and rises (exact power-of-two rescale of O and l_run) when a later tile's largest
+      // scale passes 2^(9 + eps) -- rare: scales sit near amax / 448 of their rows.
+      if (__ballot(smx > elim)) {
+        float wm = smx;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o));
+        const int en = __builtin_amdgcn_frexp_expf(wm) - 9;     // wm * 2^-en < 2^9
+        if (elim == 0.f || en > eps) {
+          const float f = __builtin_ldexpf(1.f, eps - en);
+          l_run *= f;
+          if (started) scale_acc(O, f);
+          eps = en;
+          elim = __builtin_ldexpf(1.f, 9 + eps);
+        }
+      }
+      const float mref = (m_run > -__builtin_inff() ? m_run : 0.f) + (float)eps;
+      float P[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) P[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[i], c, -mref));   // exp2(-inf) = 0
+      float s8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s8[i] = P[i] + P[i + 8];
+      l_run += ((s8[0] + s8[4]) + (s8[1] + s8[5])) + ((s8[2] + s8[6]) + (s8[3] + s8[7]));
+      started = true;
+
+      // ---- PV: output dims of group g (MFMA blocks mt = 4g .. 4g + 3) use P' = P * scale(row, g) in f16. The
+      // transposed V^T reads run VD MFMAs ahead; group g + 1's P' is formed during group g, one quarter of its rows
+      // per MFMA (4 products, 2 packs), from scales read one MFMA earlier.
+      typedef short i16x8 __attribute__((ext_vector_type(8)));
+      constexpr int VD = 2;
+      auto vread = [&](int v) -> f16x8 {          // MFMA v = (group g, block m4, k half ks): v = 8 g + 2 m4 + ks
+        SPMLA_LDS uint8_t* base = bf + 16384 * (v & 1) + 256 * (v >> 3);
+        const int m4 = (v >> 1) & 3;
+        const int mo = (64 * m4) ^ pv_key;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPMLA_LDS i16x4*)(base + pv_base[0] + mo));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPMLA_LDS i16x4*)(base + pv_base[1] + mo));
+        return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      };
+      f16x8 vr[4];
+#pragma unroll
+      for (int v = 0; v < VD; ++v) vr[v] = vread(v);
+      u32x4 pbw[2], pbn[2];                  // P' of the current / next group, as packed bf16 pairs
+      {
+        const f32x4 z0 = zload(0);
+        mul4_dpp_f16<0>(pbw[0], z0[0], P);
+        mul4_dpp_f16<1>(pbw[0], z0[1], P);
+        mul4_dpp_f16<2>(pbw[1], z0[2], P);
+        mul4_dpp_f16<3>(pbw[1], z0[3], P);
+      }
+      f32x4 zp = zload(1);                   // scales of the P' formed during the group (group g + 1)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int v = 0; v < 32; ++v) {
+        const int g = v >> 3, v8 = v & 7, mt = 4 * g + (v8 >> 1);
+        if (v + VD < 32) vr[(v + VD) & 3] = vread(v + VD);
+        if (g < 3) {                             // quarter v8 - 1 of group g + 1 at v8 = 1 .. 4
+          if (v8 == 1) mul4_dpp_f16<0>(pbn[0], zp[0], P);
+          if (v8 == 2) mul4_dpp_f16<1>(pbn[0], zp[1], P);
+          if (v8 == 3) mul4_dpp_f16<2>(pbn[1], zp[2], P);
+          if (v8 == 4) mul4_dpp_f16<3>(pbn[1], zp[3], P);
+        }
+        if (g < 2 && v8 == 6) zp = zload(g + 2);
+        O[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[v & 3], __builtin_bit_cast(f16x8, pbw[v8 & 1]), O[mt], 0, 0, 0);
+        if (v8 == 7 && g < 3) { pbw[0] = pbn[0]; pbw[1] = pbn[1]; }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    rcur = rnxt;
-    mcur = mnxt;
+    lds_barrier();                          // tile j + 1 converted; tile j's buffers free
   }
 
-  // ---- merge the 4 waves: per head M = max m_w, L = sum l_w 2^(m_w - M), O = sum O_w 2^(m_w - M) / L
-  l_run += __shfl_xor(l_run, 32, 64);
-  SPMLA_LDS float* s_ml = (SPMLA_LDS float*)(lds + L_ML);
-  lds_barrier();                                 // every wave is done with its tiles (no copy in flight)
-  if (half == 0) { s_ml[w * 64 + l32] = m_run; s_ml[w * 64 + 32 + l32] = l_run; }
-  lds_barrier();
-  // weight of wave v's partial for this lane's head: 2^(m_v - M) kv_scale / L (applied by the reducing wave, so
-  // the partials go to LDS straight from the accumulator registers)
-  float M = -__builtin_inff();
-#pragma unroll
-  for (int v = 0; v < NW; ++v) M = fmaxf(M, s_ml[v * 64 + l32]);
-  float fv[NW];
-  float L = 0.f;
-#pragma unroll
-  for (int v = 0; v < NW; ++v) {
-    const float mv = s_ml[v * 64 + l32];
-    fv[v] = mv > -__builtin_inff() ? __builtin_amdgcn_exp2f(mv - M) : 0.f;
-    L += s_ml[v * 64 + 32 + l32] * fv[v];
-  }
+  if (!wact) return;
+  // ---- epilogue: this wave's 32 heads are complete (no other wave holds them)
+  l_run += half_swap(l_run);
+  const float L = l_run;
   float inv = L > 0.f ? p.kv_scale / L : 0.f;
-  float lse_v = L > 0.f ? (M + log2f(L)) * 0.69314718055994531f : -__builtin_inff();
-  // merge with a prior partial of the same (token, head): weights exp(lse_i - max) / sum, the lse of the union
-  float wp = 0.f;
-  if (p.prior_o) {
-    const int hh = hg * HG + (lane & 31);
-    const float lp = hh < p.H ? p.prior_lse[(long long)t * p.pl_st + hh] : -__builtin_inff();
+  float lse_v = L > 0.f ? (m_run + (float)eps + log2f(L)) * 0.69314718055994531f : -__builtin_inff();
+  float wp = 0.f;                           // weight of the prior partial (merge of two normalized partials)
+  if (p.prior_o && hval) {
+    const float lp = p.prior_lse[(long long)t * p.pl_st + h];
     const float mf = fmaxf(lse_v, lp);
     if (mf > -__builtin_inff()) {
       const float a = expf(lse_v - mf), b = expf(lp - mf);     // exp(-inf) = 0
@@ -501,60 +584,32 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
       lse_v = mf + logf(z);
     }
   }
+  if (!hval) return;
+  // C layout of O[mt]: lane holds head l32, dims 32 mt + 8 a + 4 hh + b in value 4 a + b. One block at a time (the
+  // fences keep the compiler from reading all 256 accumulators into VGPRs at once).
+  const bool part = p.opart != nullptr;
+  uint16_t* orow = part ? nullptr : p.out + (long long)t * p.o_st + (long long)h * p.o_sh;
+  float* frow = part ? p.opart + (((long long)s * p.T + t) * p.H + h) * D_LAT : nullptr;
+  const float* prow = p.prior_o ? p.prior_o + (long long)t * p.po_st + (long long)h * p.po_sh : nullptr;
 #pragma unroll
-  for (int v = 0; v < NW; ++v) fv[v] *= inv;
-
-  SPMLA_LDS f32x4* xo = (SPMLA_LDS f32x4*)(lds + L_TILES);   // [wave][tile 0..7][qd][lane]
-  // output head of this lane, recomputed from the lane id (cheaper than keeping it live across the loop)
-  const int oc = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31);
-  const int ho = col_head(oc), to = col_tok(oc);
-  const bool hoval = col_ok(oc);
+  for (int mt = 0; mt < 16; ++mt) {
 #pragma unroll
-  for (int rnd = 0; rnd < 2; ++rnd) {
+    for (int a = 0; a < 4; ++a) {
+      const int col = 32 * mt + 8 * a + 4 * hh;
+      f32x4 v = f32x4{O[mt][4 * a] * inv, O[mt][4 * a + 1] * inv, O[mt][4 * a + 2] * inv, O[mt][4 * a + 3] * inv};
+      if (prow) {
+        const f32x4 x = *(const f32x4*)(prow + col);
 #pragma unroll
-    for (int b = 0; b < 8; ++b)
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x16& o = O[8 * rnd + b];
-        xo[((w * 8 + b) * 4 + qd) * 64 + lane] = f32x4{o[4 * qd], o[4 * qd + 1], o[4 * qd + 2], o[4 * qd + 3]};
+        for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(x[e], wp, v[e]);
       }
-    lds_barrier();
-    // wave w reduces output tiles 2w, 2w + 1 of this round and writes them
-#pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-      const int b = 2 * w + bb;
-      const int mt = 8 * rnd + b;
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int v = 0; v < NW; ++v) {
-          const f32x4 x = xo[((v * 8 + b) * 4 + qd) * 64 + lane];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(x[e], fv[v], acc[e]);
-        }
-        if (hoval) {
-          const int col = 32 * mt + 8 * qd + 4 * half;      // C-layout rows of values 4qd .. 4qd + 3
-          if (p.prior_o) {
-            const f32x4 x = *(const f32x4*)(p.prior_o + (long long)t * p.po_st + (long long)ho * p.po_sh + col);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(x[e], wp, acc[e]);
-          }
-          if (p.opart == nullptr) {
-            uint16_t* orow = p.out + (long long)to * p.o_st + (long long)ho * p.o_sh;
-            *(uint2*)(orow + col) = make_uint2(pk_bf16(acc[0], acc[1]), pk_bf16(acc[2], acc[3]));
-          } else {
-            float* orow = p.opart + (((long long)s * p.T + to) * p.H + ho) * D_LAT;
-            *(f32x4*)(orow + col) = acc;
-          }
-        }
-      }
+      if (part) *(f32x4*)(frow + col) = v;
+      else *(uint2*)(orow + col) = make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]));
     }
-    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
   }
-  if (w == 0 && half == 0 && hoval) {
-    if (p.opart == nullptr) p.lse[(long long)to * p.lse_st + ho] = lse_v;
-    else p.lsepart[((long long)s * p.T + to) * p.H + ho] = lse_v;
+  if (hh == 0) {
+    if (part) p.lsepart[((long long)s * p.T + t) * p.H + h] = lse_v;
+    else p.lse[(long long)t * p.lse_st + h] = lse_v;
   }
 }
 
@@ -638,68 +693,29 @@ static int attn_launch(const void* q, long long q_st, long long q_sh, const void
   if (f32part ? !lsepart : (S != 1 || !out || !lse)) return SPMLA_EARG;
   if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)pool & 15)) return SPMLA_EALIGN;
   if (out && (((uintptr_t)out & 7) || (o_st & 3) || (o_sh & 3))) return SPMLA_EALIGN;
+  if (f32part && ((uintptr_t)opart & 15)) return SPMLA_EALIGN;
   if (((K + S - 1) / S + attn::TR - 1) / attn::TR * attn::TR > attn::KMAX) return SPMLA_ELIMIT;
   attn::Params p;
   p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh;
   p.pool = (const uint8_t*)pool; p.R = R;
   p.idx = idx; p.idx_st = idx_st; p.K = K; p.kcount = kcount;
-  p.T = T; p.H = H; p.S = S; p.HGN = (H + attn::HG - 1) / attn::HG;
+  p.T = T; p.H = H; p.S = S; p.HG = (H + attn::HGW - 1) / attn::HGW;
   p.c = sm_scale * kv_scale * 1.4426950408889634f;
   p.kv_scale = kv_scale;
   p.out = (uint16_t*)out; p.o_st = o_st; p.o_sh = o_sh; p.lse = lse; p.lse_st = lse_st;
   p.opart = f32part ? opart : nullptr; p.lsepart = lsepart;
   p.prior_o = prior_o; p.po_st = po_st; p.po_sh = po_sh; p.prior_lse = prior_lse; p.pl_st = pl_st;
-  p.mk = nullptr; p.cu = nullptr; p.ql = 1; p.tsh = 0; p.NR = T;
-  const long long nwork = (long long)T * S * p.HGN;
+  const long long nwork = (long long)T * S * p.HG;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);
   static bool attr = false;
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)attn::attn_kernel<false>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, attn::L_TOTAL);
+    hipError_t e = hipFuncSetAttribute((const void*)attn::fwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       attn::L_TOTAL);
     if (e != hipSuccess) return (int)e;
     attr = true;
   }
-  hipLaunchKernelGGL(attn::attn_kernel<false>, dim3(grid), dim3(256), attn::L_TOTAL, (hipStream_t)stream, p);
-  return (int)hipGetLastError();
-}
-
-int spmla_attn_packed(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* u,
-                      const unsigned char* mk, const int* cnt, int nmax, const int* cu, int ql, int nreq, int T,
-                      int H, int tpg, float sm_scale, float kv_scale, int S, void* out, long long o_st,
-                      long long o_sh, float* lse, long long lse_st, float* opart, float* lsepart, void* stream) {
-  if (T < 0 || nreq < 0 || H <= 0 || nmax < 0 || S <= 0 || R < 0 || (!cu && ql <= 0)) return SPMLA_EARG;
-  if (tpg != 1 && tpg != 2 && tpg != 4 && tpg != 8) return SPMLA_EARG;
-  if (T == 0 || nreq == 0) return SPMLA_OK;
-  if (!q || !u || !mk || !cnt || (R > 0 && !pool)) return SPMLA_EARG;
-  const bool f32part = opart != nullptr;
-  if (f32part ? !lsepart : (S != 1 || !out || !lse)) return SPMLA_EARG;
-  if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)pool & 15)) return SPMLA_EALIGN;
-  if (out && (((uintptr_t)out & 7) || (o_st & 3) || (o_sh & 3))) return SPMLA_EALIGN;
-  attn::Params p;
-  p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh;
-  p.pool = (const uint8_t*)pool; p.R = R;
-  p.idx = u; p.idx_st = nmax; p.K = nmax; p.kcount = cnt;
-  p.T = T; p.H = H; p.S = S;
-  p.tsh = tpg == 1 ? 0 : (tpg == 2 ? 1 : (tpg == 4 ? 2 : 3));
-  p.HGN = (H + (attn::HG >> p.tsh) - 1) / (attn::HG >> p.tsh);
-  p.c = sm_scale * kv_scale * 1.4426950408889634f;
-  p.kv_scale = kv_scale;
-  p.out = (uint16_t*)out; p.o_st = o_st; p.o_sh = o_sh; p.lse = lse; p.lse_st = lse_st;
-  p.opart = f32part ? opart : nullptr; p.lsepart = lsepart;
-  p.prior_o = nullptr; p.po_st = p.po_sh = 0; p.prior_lse = nullptr; p.pl_st = 0;
-  p.mk = (const uint8_t*)mk; p.cu = cu; p.ql = ql; p.NR = nreq;
-  const long long nwork = (long long)nreq * S * p.HGN;
-  if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
-  const int grid = (int)((nwork + 7) / 8 * 8);
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)attn::attn_kernel<true>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, attn::L_TOTAL);
-    if (e != hipSuccess) return (int)e;
-    attr = true;
-  }
-  hipLaunchKernelGGL(attn::attn_kernel<true>, dim3(grid), dim3(256), attn::L_TOTAL, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(attn::fwd_kernel, dim3(grid), dim3(256), attn::L_TOTAL, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 

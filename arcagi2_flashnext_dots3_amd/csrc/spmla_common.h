@@ -138,11 +138,13 @@ __device__ inline void dma4(const void* g, SPMLA_LDS void* l) {
 // Workgroup barrier for data exchanged through LDS only (no vector-memory drain).
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// vmcnt-only wait (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
+// vmcnt-only wait (expcnt and lgkmcnt left at their maxima), gfx9 encoding. Also a compiler memory barrier, so
+// that reads of LDS filled by the copies are not moved above the wait.
 template <int N>
 __device__ inline void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
 }
 
 }  // namespace spmla

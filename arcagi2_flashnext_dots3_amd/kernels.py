@@ -480,11 +480,24 @@ def attention_ok(q, idx):
             and idx.dtype == torch.int32 and idx.stride(1) == 1)
 
 
-def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=1, kcount=None, ws=None, R=None):
+def auto_split(T, H, K, cus=256):
+    """Row splits per token: doubled while the launch has fewer workgroups than compute units and every split keeps
+    at least 8 tiles of 32 rows (at most 8 splits)."""
+    n = T * ((H + 127) // 128)
+    s = 1
+    while s < 8 and n * s < cus and K >= 2 * s * 256:
+        s *= 2
+    return s
+
+
+def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None, kcount=None, ws=None, R=None):
     """q [T, H, 576] bf16, pool [R, 656] uint8 Row656 rows (or a mapped host address with R given), idx [T, K]
-    int32 rows -> (out [T, H, 512] bf16, lse [T, H] fp32). split > 1 cuts K into partials merged by lse_merge."""
+    int32 rows -> (out [T, H, 512] bf16, lse [T, H] fp32). split > 1 cuts K into partials merged by lse_merge
+    (None: auto_split)."""
     T, H, _ = q.shape
     K = idx.shape[1]
+    if split is None:
+        split = auto_split(T, H, K)
     _need(attention_ok(q, idx), "attend: q must be bf16 [T, H, 576] with 16-byte aligned rows, idx int32")
     if out is None:
         out = torch.empty(T, H, D_LAT, dtype=torch.bfloat16, device=q.device)

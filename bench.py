@@ -150,7 +150,7 @@ def run_config2(a, dev):
     gbs = ALG_BYTES / (ms * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "spmla::attn::attn_kernel", "alg_bytes_per_launch": ALG_BYTES,
+            "kernel": "spmla::attn::fwd_kernel", "alg_bytes_per_launch": ALG_BYTES,
             "mfma_tflops": round(ALG_FLOPS / (ms * 1e-3) / 1e12, 2),
             "mfma_frac_bf16_peak": round(ALG_FLOPS / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
     tf = os.path.join(ROOT, "profiles", "attn_kernel_config2_traffic.json")
@@ -159,7 +159,7 @@ def run_config2(a, dev):
     cfg = {"workload": "BASELINE config 2: all-HBM sparse-MLA decode, B=64, H=128, ctx=32768/seq, top-2048, Row656 "
                        "rows, bf16 out + fp32 LSE; launches replayed from a HIP graph",
            "global_batch": B, "heads": H, "ctx": CTX, "topk": K, "row_bytes": ROWB, "idx_sets": a.idx_sets}
-    res = _line(METRIC, gbs, "GB/s", a, ms, "fp8e4m3 rows x bf16 q: bf16 MFMA (QK), f16 MFMA (PV), fp32 accumulate",
+    res = _line(METRIC, gbs, "GB/s", a, ms, "fp8e4m3 rows x bf16 q: bf16 MFMA (QK and PV), fp32 accumulate",
                 cfg, roof, step_us=round(ms * 1e3, 2), eager_step_us=round(eager_ms * 1e3, 2))
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(pool, q, idxs[0])
@@ -448,9 +448,9 @@ def run_config5(a, dev):
         cpu = {"value": round(t * 1e3, 1), "unit": "ms per prefill chunk (attention only)", "cores": nt,
                "kind": "port", "sample": f"{ns} of {NQ} queries in fp32 torch, scaled linearly"}
     roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None, "kernel": "spmla::attn::attn_kernel"}
+            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None, "kernel": "spmla::attn::fwd_kernel"}
     res = _line("chunked prefill attention ms (8192 queries x 128 heads x top-2048) + cache write us", ms_a, "ms", a,
-                ms_a + ms_w, "bf16 MFMA (QK), f16 MFMA (PV), fp32 accumulate",
+                ms_a + ms_w, "bf16 MFMA (QK and PV), fp32 accumulate",
                 {"workload": "BASELINE config 5: 8192 queries, 128 heads, top-2048 of <= 65536 prior rows; write "
                              "8192 rows at random slots of a paged cache (block 64)"}, roof, cpu, hib=False,
                 cache_write_us=round(ms_w * 1e3, 2),
@@ -617,7 +617,7 @@ def run_config7(a, dev):
                               "of a request's rows shared; union then packed attention (graph of 20 steps)"},
                  {"bound": "hbm", "achieved": round(rows_loaded * ROWB / (ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
                   "unit": "GB/s", "frac": round(rows_loaded * ROWB / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                  "traffic": None, "kernel": "spmla::attn::attn_kernel<true>"},
+                  "traffic": None, "kernel": "spmla::pk::attn_kernel<true>"},
                  hib=False, per_token_us=round(ms_tok * 1e3, 2), union_us=round(ms_union * 1e3, 2),
                  union_rows_per_request=round(rows_loaded / NRQ, 1), rows_per_request_per_token=K * QL,
                  max_rel_diff_vs_per_token=round(diff, 5))
@@ -644,7 +644,7 @@ def run_config1(a, dev):
     tc = (time.perf_counter() - t0) / 20
     alg = K1 * ROWB + H1 * D * 2 + H1 * 512 * 2 + H1 * 4 + K1 * 4
     return _line("sparse-MLA decode us, B=1, 16 heads, top-256 of 4096", ms * 1e3, "us", a, ms,
-                 "bf16 / f16 MFMA, fp32 accumulate", {"workload": "BASELINE config 1"},
+                 "bf16 MFMA, fp32 accumulate", {"workload": "BASELINE config 1"},
                  {"bound": "hbm", "achieved": round(alg / (ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS,
                   "unit": "GB/s", "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5), "traffic": None},
                  {"value": round(tc * 1e6, 1), "unit": "us", "cores": cpu_port.threads(), "kind": "port",
@@ -709,7 +709,7 @@ def main():
         r = run_config3_ways(a, dev, row_fmt=a.host_rows, W=a.ways, two=a.two_choice) if a.cache == "ways" else \
             run_config3(a, dev, row_fmt=a.host_rows, cache_fmt=a.cache_fmt)
         res = _line("offload split-K decode step us (host tier + HBM hot rows), B=64 top2048", r["ms_per_step"] * 1e3,
-                    "us", a, r["ms_per_step"], "bf16 / f16 MFMA, fp32 accumulate", {"workload": r["workload"]},
+                    "us", a, r["ms_per_step"], "bf16 MFMA, fp32 accumulate", {"workload": r["workload"]},
                     {"bound": "pcie", "achieved": r["pcie_gbs_achieved"], "peak": r["h2d_copy_gbs"], "unit": "GB/s",
                      "frac": round(r["pcie_gbs_achieved"] / max(r["h2d_copy_gbs"], 1e-9), 4), "traffic": None},
                     hib=False, detail=r)
