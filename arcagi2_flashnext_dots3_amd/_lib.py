@@ -45,6 +45,8 @@ SIGNATURES = {
     "spmla_wcache_split": [P, LL, I, I, P, I, P, P, LL, P, P, LL, P, P],
     "spmla_compact_stage": [P, I, P, LL, I, I, P, P, P, P, LL, P],
     "spmla_attn_splitk": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, I, P, LL, LL, P, LL, P, P, P],
+    "spmla_attn": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, I, P, LL, LL, P, LL, P, LL, P],
+    "spmla_attn_ws_bytes": [I, I, I],
     "spmla_attn_merge": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, P, LL, LL, P, LL, P, LL, LL, P, LL, P],
     "spmla_lse_merge": [P, I, LL, LL, LL, P, LL, LL, I, I, I, P, LL, LL, P, P, LL, P],
     "spmla_bmm_fp8": [P, LL, LL, LL, P, LL, LL, LL, P, LL, LL, LL, I, P, LL, LL, LL, I, I, I, I, I, P],
@@ -59,7 +61,7 @@ SIGNATURES = {
     "spmla_host_e4m3_encode": [P, P, LL],
 }
 _RESTYPE = {"spmla_version": ctypes.c_char_p, "spmla_host_e4m3_encode": None, "spmla_topk_ws_bytes": LL,
-            "spmla_topk_scratch_bytes": LL}
+            "spmla_topk_scratch_bytes": LL, "spmla_attn_ws_bytes": LL}
 
 ERRORS = {-2: "bad argument", -3: "misaligned pointer or stride", -5: "size beyond the kernel's limit"}
 

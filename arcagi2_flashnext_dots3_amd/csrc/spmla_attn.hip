@@ -91,13 +91,14 @@ __device__ inline uint32_t pk_f16(float a, float b) {       // round to nearest 
   const f16x2_t v = {(_Float16)a, (_Float16)b};
   return __builtin_bit_cast(uint32_t, v);
 }
-// 8 bf16 (one 16-byte chunk) -> 8 f16: exact for |x| in [2^-14, 65504] (f16 carries 11 significant bits)
-__device__ inline f16x8 bf16x8_to_f16(u32x4 r) {
+// 8 bf16 (one 16-byte chunk) times 2^k -> 8 f16: exact for |x 2^k| in [2^-14, 65504] (f16 carries 11 significant
+// bits, bf16 8)
+__device__ inline f16x8 bf16x8_to_f16(u32x4 r, int k) {
   f16x8 h;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    h[2 * e] = (_Float16)__builtin_bit_cast(float, r[e] << 16);
-    h[2 * e + 1] = (_Float16)__builtin_bit_cast(float, r[e] & 0xffff0000u);
+    h[2 * e] = (_Float16)__builtin_ldexpf(__builtin_bit_cast(float, r[e] << 16), k);
+    h[2 * e + 1] = (_Float16)__builtin_ldexpf(__builtin_bit_cast(float, r[e] & 0xffff0000u), k);
   }
   return h;
 }
@@ -168,7 +169,17 @@ struct Params {
   // optional prior partial merged into the bf16 output (S == 1): normalized fp32 o and natural-log lse
   const float* prior_o; long long po_st, po_sh;
   const float* prior_lse; long long pl_st;
+  // split merge inside the kernel (S > 1 with the bf16 output): per (token, head group) arrival counters (zero
+  // between launches), per split and head the lse and the partial's exponent, and the f16 partials in the lanes'
+  // order ([split][token][head group][wave][mt][a][lane][4]); null otherwise
+  int* ws_cnt; float* ws_lse; float* ws_exp; uint16_t* ws_o;
 };
+
+// Workspace of the in-kernel split merge (bytes, each part 256-byte aligned).
+__host__ __device__ inline long long ws_align(long long b) { return (b + 255) / 256 * 256; }
+inline long long ws_cnt_bytes(int T, int HG) { return ws_align(4ll * T * HG); }
+inline long long ws_lse_bytes(int T, int HG, int S) { return ws_align(4ll * S * T * HG * HGW); }
+inline long long ws_o_bytes(int T, int HG, int S) { return 2ll * S * T * HG * HGW * D_LAT; }
 
 // Copies of tile jj for wave w: the codes of scale group w of the tile's 32 rows (4 x 16 B per lane; staging slot
 // [part i][half][row][16 B] holds e4m3 chunk 8 w + 2 i + half of the row), rows 8 w .. 8 w + 7 of the rope tile (lane
@@ -241,6 +252,97 @@ __device__ inline void write_part(SPMLA_LDS uint8_t* lds, int jj, int w, const i
   *(SPMLA_LDS u32x4*)(bf + wo[0] + ((64 * i + 16) ^ wo[1])) = b;
 }
 
+// bf16 output of a wave's 32 heads through LDS: the C-layout values of block mt (head l32, dims 32 mt + 8 a + 4 hh +
+// b in v[4 a + b]) go to the wave's region [head][512] (row stride 1040 B: heads 16 apart share banks, so a write
+// costs 2 passes); then every head row leaves as 64 lanes x 16 B. Used after the last tile's barrier (the LDS is
+// free); heads >= H are not written.
+constexpr int OROW = 1040;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+static_assert(NW * HB * OROW <= L_IDS, "output staging fits below the flag word");
+__device__ inline void put_block(SPMLA_LDS uint8_t* reg, int lane, int mt, const float (&v)[16]) {
+  const int l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+    *(SPMLA_LDS u32x2*)(reg + l32 * OROW + (32 * mt + 8 * a + 4 * hh) * 2) =
+        u32x2{pk_bf16(v[4 * a], v[4 * a + 1]), pk_bf16(v[4 * a + 2], v[4 * a + 3])};
+}
+__device__ inline void flush_rows(const Params& p, SPMLA_LDS uint8_t* reg, int t, int hbase, int lane) {
+  const bool al16 = !(((uintptr_t)p.out | (uintptr_t)(p.o_st * 2) | (uintptr_t)(p.o_sh * 2)) & 15);
+  const int nh = p.H - hbase < HB ? p.H - hbase : HB;
+  uint16_t* ob = p.out + (long long)t * p.o_st + (long long)hbase * p.o_sh + 8 * lane;
+  for (int r = 0; r < nh; ++r) {
+    const u32x4 v = *(SPMLA_LDS u32x4*)(reg + r * OROW + 16 * lane);
+    uint16_t* dst = ob + (long long)r * p.o_sh;
+    if (al16) *(u32x4*)dst = v;
+    else { *(uint2*)dst = make_uint2(v[0], v[1]); *(uint2*)(dst + 4) = make_uint2(v[2], v[3]); }
+  }
+}
+
+// The in-kernel split merge for NS splits, run by the last split to arrive at (token t, head group hg): o = sum_u
+// f[u] * partial_u with f[u] = e^(lse_u - M) kv_scale 2^exp_u / Z (the f16 partials of every split, this one's
+// included), one output block at a time with the next block's loads in flight; lse = M + ln Z.
+template <int NS>
+__device__ inline void merge_splits(const Params& p, SPMLA_LDS uint8_t* reg, int t, int hg, int hbase, int w,
+                                    int lane) {
+  const int l32 = lane & 31, hh = lane >> 5;
+  float lu[NS], f[NS];
+  uint64_t* pu[NS];
+  float lmax = -__builtin_inff();
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    const long long bu = ((long long)u * p.T + t) * p.HG + hg;
+    lu[u] = __builtin_bit_cast(float, __hip_atomic_load((uint32_t*)p.ws_lse + bu * HGW + w * HB + l32,
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    f[u] = (float)(int)__hip_atomic_load((uint32_t*)p.ws_exp + bu * HGW + w * HB + l32, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    pu[u] = (uint64_t*)(p.ws_o + (bu * NW + w) * (16 * 4 * 64 * 4)) + lane;
+    lmax = fmaxf(lmax, lu[u]);
+  }
+  float z = 0.f;
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    lu[u] = lmax > -__builtin_inff() ? expf(lu[u] - lmax) : 0.f;     // exp(-inf) = 0
+    z += lu[u];
+  }
+  const float zi = z > 0.f ? p.kv_scale / z : 0.f;
+#pragma unroll
+  for (int u = 0; u < NS; ++u) f[u] = lu[u] * zi * __builtin_ldexpf(1.f, (int)f[u]);
+  const int h = hbase + l32;
+  if (h < p.H && hh == 0) p.lse[(long long)t * p.lse_st + h] = lmax > -__builtin_inff() ? lmax + logf(z) : lmax;
+  uint64_t x[2][NS][4];
+#pragma unroll
+  for (int u = 0; u < NS; ++u)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) x[0][u][a] = __hip_atomic_load(pu[u] + a * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int mt = 0; mt < 16; ++mt) {
+    if (mt + 1 < 16) {
+#pragma unroll
+      for (int u = 0; u < NS; ++u)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+          x[(mt + 1) & 1][u][a] =
+              __hip_atomic_load(pu[u] + ((mt + 1) * 4 + a) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float v[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = 0.f;
+#pragma unroll
+    for (int u = 0; u < NS; ++u)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const f16x2_t lo = __builtin_bit_cast(f16x2_t, (uint32_t)x[mt & 1][u][a]);
+        const f16x2_t hi = __builtin_bit_cast(f16x2_t, (uint32_t)(x[mt & 1][u][a] >> 32));
+        v[4 * a] = __builtin_fmaf((float)lo[0], f[u], v[4 * a]);
+        v[4 * a + 1] = __builtin_fmaf((float)lo[1], f[u], v[4 * a + 1]);
+        v[4 * a + 2] = __builtin_fmaf((float)hi[0], f[u], v[4 * a + 2]);
+        v[4 * a + 3] = __builtin_fmaf((float)hi[1], f[u], v[4 * a + 3]);
+      }
+    put_block(reg, lane, mt, v);
+  }
+  flush_rows(p, reg, t, hbase, lane);
+}
+
 __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_generic[];
   SPMLA_LDS uint8_t* lds = (SPMLA_LDS uint8_t*)smem_generic;
@@ -282,9 +384,9 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
   }
   const uint16_t* qrow = p.q + (long long)t * p.q_st + (long long)(hval ? h : 0) * p.q_sh;
   const uint32_t qmask = hval ? 0xffffffffu : 0u;          // heads past H: zero query
-  f16x8 qf[32];
+  u32x4 qraw[32];                                            // bf16, converted to f16 once the first copies are issued
 #pragma unroll
-  for (int ks = 0; ks < 32; ++ks) qf[ks] = bf16x8_to_f16(*(const u32x4*)(qrow + 16 * ks + 8 * hh) & qmask);
+  for (int ks = 0; ks < 32; ++ks) qraw[ks] = *(const u32x4*)(qrow + 16 * ks + 8 * hh) & qmask;
   u32x4 qrv[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {                              // rope: 32 heads x 8 chunks, 4 per lane
@@ -299,12 +401,6 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
   for (int k = 0; k < KMAX / 256; ++k) {
     const int i = tid + 256 * k;
     if (i < ntile * TR) ids[i] = xs[k];
-  }
-  SPMLA_LDS uint8_t* qr = lds + L_QR + w * (HB * 128);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int cc = lane + 64 * k;
-    *(SPMLA_LDS u32x4*)(qr + rp_off(cc >> 3, cc & 7)) = qrv[k];
   }
   lds_barrier();
 
@@ -324,6 +420,43 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
   // row ids of tile 3 (the first copies the loop issues)
   int nx0 = 3 < ntile ? ids[3 * TR + (lane & 31)] : -1, nx1 = 3 < ntile ? ids[3 * TR + r_dma1] : -1;
   int nx2 = 3 < ntile ? ids[3 * TR + r_dma2] : -1;
+
+  // ---- query scaled per head by 2^kq, a power of two that puts its largest latent magnitude in [2^14, 2^15): the
+  // latent then converts to f16 exactly wherever it matters (values below 2^-29 of the head's largest are the only
+  // ones f16 cannot hold) and cannot overflow; the rope (bf16) takes the same exact factor, and the softmax the
+  // inverse (ch). Magnitudes compare as the bf16 bit patterns without sign (packed 16-bit max).
+  int kq;
+  {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 mx2 = {0, 0};
+#pragma unroll
+    for (int ks = 0; ks < 32; ++ks)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, qraw[ks][e] & 0x7fff7fffu));
+    uint32_t m = mx2[0] > mx2[1] ? mx2[0] : mx2[1];
+    const uint32_t mo = __builtin_bit_cast(uint32_t, half_swap(__builtin_bit_cast(float, m)));
+    m = m > mo ? m : mo;
+    const int ebf = (int)(m >> 7) & 0xff;                   // bf16 exponent field of the head's largest |q|
+    kq = ebf ? 141 - ebf : 0;
+  }
+  f16x8 qf[32];
+#pragma unroll
+  for (int ks = 0; ks < 32; ++ks) qf[ks] = bf16x8_to_f16(qraw[ks], kq);
+  SPMLA_LDS uint8_t* qr = lds + L_QR + w * (HB * 128);      // this wave's query rope
+  {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int cc = lane + 64 * k;
+      const int kr = __shfl(kq, (cc >> 3) & 31);             // the factor of the chunk's head
+      u32x4 r = qrv[k];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        r[e] = pk_bf16(__builtin_ldexpf(__builtin_bit_cast(float, r[e] << 16), kr),
+                       __builtin_ldexpf(__builtin_bit_cast(float, r[e] & 0xffff0000u), kr));
+      *(SPMLA_LDS u32x4*)(qr + rp_off(cc >> 3, cc & 7)) = r;
+    }
+  }
   if (ntile > 0) {
     if (ntile >= 3) wait_vm<2 * VM_TILE>();
     else if (ntile == 2) wait_vm<VM_TILE>();
@@ -333,7 +466,7 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
   }
   lds_barrier();
 
-  const float c = p.c;
+  const float ch = __builtin_ldexpf(p.c, -kq);   // sm_scale * kv_scale * log2(e) / 2^kq
   float m_run = -__builtin_inff();     // reference max of this lane's head (log2 units)
   float l_run = 0.f;                   // sum of p over this lane's 16 rows of every tile
   bool started = false;                // wave-uniform: O holds contributions
@@ -432,19 +565,26 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
         if (g == 3 && kk == 7) zq3 = zload(3);
         // copies of tile j + 3 (row ids read one step ahead)
         if (kk == 7 && g == 0 && j + 3 < ntile) {
-          const uint8_t* dsrc = (nx0 >= 0 ? p.pool + (long long)nx0 * ROW656 : zero_row) + (8 * w + hh) * 16;
+          // source offsets recomputed here from an opaque lane id (hoisted out of the loop they would be spilled)
+          int ln = lane;
+          asm volatile("" : "+v"(ln));
+          const int doff = (8 * w + (ln >> 5)) * 16;
+          const uint8_t* dsrc = (nx0 >= 0 ? p.pool + (long long)nx0 * ROW656 : zero_row) + doff;
           SPMLA_LDS uint8_t* stg = lds + L_STG + (((j + 3) % NSTG) * NW + w) * STG_W;
           dma16(dsrc, stg);
           dma16(dsrc + 32, stg + 1024);
         }
         if (kk == 7 && g == 1 && j + 3 < ntile) {
-          const uint8_t* dsrc = (nx0 >= 0 ? p.pool + (long long)nx0 * ROW656 : zero_row) + (8 * w + hh) * 16;
+          int ln = lane;
+          asm volatile("" : "+v"(ln));
+          const int doff = (8 * w + (ln >> 5)) * 16;
+          const uint8_t* dsrc = (nx0 >= 0 ? p.pool + (long long)nx0 * ROW656 : zero_row) + doff;
           const uint8_t* rsrc = nx1 >= 0 ? p.pool + (long long)nx1 * ROW656 : zero_row;
           SPMLA_LDS uint8_t* stg = lds + L_STG + (((j + 3) % NSTG) * NW + w) * STG_W;
           dma16(dsrc + 64, stg + 2048);
           dma16(dsrc + 96, stg + 3072);
-          const int rr = r_dma1;
-          dma16(rsrc + ROPE_OFF + 16 * ((lane & 7) ^ ((rr >> 1) & 7)), lds + L_RP + ((j + 3) % NRP) * RP_TILE + w * 1024);
+          const int roff = ROPE_OFF + 16 * ((ln & 7) ^ (((8 * w + (ln >> 3)) >> 1) & 7));
+          dma16(rsrc + roff, lds + L_RP + ((j + 3) % NRP) * RP_TILE + w * 1024);
           const uint8_t* zsrc = nx2 >= 0 ? p.pool + (long long)nx2 * ROW656 : zero_row;
           if (lane < 32) dma4(zsrc + SC_OFF + 4 * w, lds + L_SC + ((j + 3) % NRP) * SC_TILE + w * 128);
         }
@@ -485,7 +625,7 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) m8[i] = fmaxf(S[i], S[i + 8]);
       float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[4]), fmaxf(m8[1], m8[5])), fmaxf(fmaxf(m8[2], m8[6]), fmaxf(m8[3], m8[7])));
-      mx = fmaxf(mx, half_swap(mx)) * c;                       // c > 0; -inf stays -inf
+      mx = fmaxf(mx, half_swap(mx)) * ch;                      // ch > 0; -inf stays -inf
       const bool need = mx > m_run + TAU;                      // also true for the first finite tile
       if (__ballot(need)) {
         const float mn = need ? mx : m_run;
@@ -499,22 +639,25 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
       // with a positive scale and rises (exact power-of-two rescale of O and l_run) when a later tile's largest
       // scale passes 2^(9 + eps) -- rare: scales sit near amax / 448 of their rows.
       if (__ballot(smx > elim)) {
-        float wm = smx;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o));
-        const int en = __builtin_amdgcn_frexp_expf(wm) - 9;     // wm * 2^-en < 2^9
+        float wm = fmaxf(smx, half_swap(smx));                // wave max (ds_swizzle xor within 32 lanes)
+        wm = fmaxf(wm, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, wm), 0x401F)));
+        wm = fmaxf(wm, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, wm), 0x201F)));
+        wm = fmaxf(wm, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, wm), 0x101F)));
+        wm = fmaxf(wm, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, wm), 0x081F)));
+        wm = fmaxf(wm, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, wm), 0x041F)));
+        const int en = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_frexp_expf(wm) - 9);   // wm * 2^-en < 2^9
         if (elim == 0.f || en > eps) {
           const float f = __builtin_ldexpf(1.f, eps - en);
           l_run *= f;
           if (started) scale_acc(O, f);
           eps = en;
-          elim = __builtin_ldexpf(1.f, 9 + eps);
+          elim = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, __builtin_ldexpf(1.f, 9 + eps))));
         }
       }
       const float mref = (m_run > -__builtin_inff() ? m_run : 0.f) + (float)eps;
       float P[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) P[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[i], c, -mref));   // exp2(-inf) = 0
+      for (int i = 0; i < 16; ++i) P[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[i], ch, -mref));  // exp2(-inf) = 0
       float s8[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) s8[i] = P[i] + P[i + 8];
@@ -566,12 +709,63 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
     lds_barrier();                          // tile j + 1 converted; tile j's buffers free
   }
 
-  if (!wact) return;
-  // ---- epilogue: this wave's 32 heads are complete (no other wave holds them)
+  // ---- epilogue: this wave's 32 heads are complete (no other wave holds them). C layout of O[mt]: lane holds head
+  // l32, dims 32 mt + 8 a + 4 hh + b in value 4 a + b.
   l_run += half_swap(l_run);
   const float L = l_run;
-  float inv = L > 0.f ? p.kv_scale / L : 0.f;
   float lse_v = L > 0.f ? (m_run + (float)eps + log2f(L)) * 0.69314718055994531f : -__builtin_inff();
+  if (p.ws_o) {                            // ---- split merge in the kernel (all waves reach the barriers)
+    const long long blk = ((long long)s * p.T + t) * p.HG + hg;   // this split's partial
+    if (wact) {
+      // partial o / 2^(eps + 3) in f16: every row scale is <= 2^(9 + eps), so |o| < 448 * 2^(9 + eps) < 2^(18 + eps)
+      const float f = L > 0.f ? __builtin_ldexpf(1.f, -(eps + 3)) / L : 0.f;
+      // agent-scope stores (written through to the device's coherence point: the merging split may run on another
+      // XCD, whose L2 does not see this one's) -- no L2 write-back fence needed
+      uint64_t* po = (uint64_t*)(p.ws_o + (blk * NW + w) * (16 * 4 * 64 * 4)) + lane;
+#pragma unroll
+      for (int mt = 0; mt < 16; ++mt) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const uint64_t v = (uint64_t)pk_f16(O[mt][4 * a] * f, O[mt][4 * a + 1] * f) |
+                             ((uint64_t)pk_f16(O[mt][4 * a + 2] * f, O[mt][4 * a + 3] * f) << 32);
+          __hip_atomic_store(po + (mt * 4 + a) * 64, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (hh == 0) {
+        __hip_atomic_store((uint32_t*)p.ws_lse + blk * HGW + w * HB + l32, __builtin_bit_cast(uint32_t, lse_v),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store((uint32_t*)p.ws_exp + blk * HGW + w * HB + l32, (uint32_t)(eps + 3), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);         // every store of the partial has completed before it is counted
+    __syncthreads();
+    SPMLA_LDS int* flag = (SPMLA_LDS int*)(lds + L_IDS);
+    if (tid == 0) {
+      int* cnt = p.ws_cnt + (long long)t * p.HG + hg;
+      const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old == p.S - 1;
+      if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next launch
+      *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;                    // another split merges this token's heads
+    if (!wact) return;                     // (the merge reads the partials with agent-scope loads)
+    SPMLA_LDS uint8_t* reg = lds + w * HB * OROW;
+    switch (p.S) {
+      case 2: merge_splits<2>(p, reg, t, hg, hbase, w, lane); break;
+      case 3: merge_splits<3>(p, reg, t, hg, hbase, w, lane); break;
+      case 4: merge_splits<4>(p, reg, t, hg, hbase, w, lane); break;
+      case 5: merge_splits<5>(p, reg, t, hg, hbase, w, lane); break;
+      case 6: merge_splits<6>(p, reg, t, hg, hbase, w, lane); break;
+      case 7: merge_splits<7>(p, reg, t, hg, hbase, w, lane); break;
+      default: merge_splits<8>(p, reg, t, hg, hbase, w, lane); break;
+    }
+    return;
+  }
+  if (!wact) return;
+  float inv = L > 0.f ? p.kv_scale / L : 0.f;
   float wp = 0.f;                           // weight of the prior partial (merge of two normalized partials)
   if (p.prior_o && hval) {
     const float lp = p.prior_lse[(long long)t * p.pl_st + h];
@@ -584,9 +778,25 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
       lse_v = mf + logf(z);
     }
   }
+  if (hh == 0 && hval) {
+    if (p.opart) p.lsepart[((long long)s * p.T + t) * p.H + h] = lse_v;
+    else p.lse[(long long)t * p.lse_st + h] = lse_v;
+  }
+  if (!p.opart && !p.prior_o) {            // bf16 rows through LDS (16-byte stores of whole head rows)
+    SPMLA_LDS uint8_t* reg = lds + w * HB * OROW;
+#pragma unroll
+    for (int mt = 0; mt < 16; ++mt) {
+      float v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = O[mt][e] * inv;
+      put_block(reg, lane, mt, v);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    flush_rows(p, reg, t, hbase, lane);
+    return;
+  }
   if (!hval) return;
-  // C layout of O[mt]: lane holds head l32, dims 32 mt + 8 a + 4 hh + b in value 4 a + b. One block at a time (the
-  // fences keep the compiler from reading all 256 accumulators into VGPRs at once).
+  // One block at a time (the fences keep the compiler from reading all 256 accumulators into VGPRs at once).
   const bool part = p.opart != nullptr;
   uint16_t* orow = part ? nullptr : p.out + (long long)t * p.o_st + (long long)h * p.o_sh;
   float* frow = part ? p.opart + (((long long)s * p.T + t) * p.H + h) * D_LAT : nullptr;
@@ -606,10 +816,6 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
       else *(uint2*)(orow + col) = make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]));
     }
     __builtin_amdgcn_sched_barrier(0);
-  }
-  if (hh == 0) {
-    if (part) p.lsepart[((long long)s * p.T + t) * p.H + h] = lse_v;
-    else p.lse[(long long)t * p.lse_st + h] = lse_v;
   }
 }
 
@@ -685,12 +891,21 @@ static int attn_launch(const void* q, long long q_st, long long q_sh, const void
                        long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale, int S,
                        void* out, long long o_st, long long o_sh, float* lse, long long lse_st, float* opart,
                        float* lsepart, const float* prior_o, long long po_st, long long po_sh, const float* prior_lse,
-                       long long pl_st, void* stream) {
+                       long long pl_st, void* ws, long long ws_bytes, void* stream) {
   if (T < 0 || H <= 0 || K < 0 || S <= 0 || R < 0) return SPMLA_EARG;
   if (T == 0) return SPMLA_OK;
   if (!q || !idx || (R > 0 && !pool)) return SPMLA_EARG;
-  const bool f32part = opart != nullptr;   // fp32 partials (any S) instead of the bf16 output (S == 1 only)
-  if (f32part ? !lsepart : (S != 1 || !out || !lse)) return SPMLA_EARG;
+  const bool f32part = opart != nullptr;   // fp32 partials (any S) instead of the bf16 output
+  const bool fused = !f32part && S > 1;    // bf16 output of S splits merged in the kernel (workspace ws)
+  if (f32part ? !lsepart : (!out || !lse)) return SPMLA_EARG;
+  const int HG = (H + attn::HGW - 1) / attn::HGW;
+  if (fused) {
+    if (!ws || prior_o) return SPMLA_EARG;
+    if (S > 8) return SPMLA_ELIMIT;
+    if ((uintptr_t)ws & 255) return SPMLA_EALIGN;
+    if (ws_bytes < attn::ws_cnt_bytes(T, HG) + 2 * attn::ws_lse_bytes(T, HG, S) + attn::ws_o_bytes(T, HG, S))
+      return SPMLA_EARG;
+  }
   if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)pool & 15)) return SPMLA_EALIGN;
   if (out && (((uintptr_t)out & 7) || (o_st & 3) || (o_sh & 3))) return SPMLA_EALIGN;
   if (f32part && ((uintptr_t)opart & 15)) return SPMLA_EALIGN;
@@ -705,6 +920,17 @@ static int attn_launch(const void* q, long long q_st, long long q_sh, const void
   p.out = (uint16_t*)out; p.o_st = o_st; p.o_sh = o_sh; p.lse = lse; p.lse_st = lse_st;
   p.opart = f32part ? opart : nullptr; p.lsepart = lsepart;
   p.prior_o = prior_o; p.po_st = po_st; p.po_sh = po_sh; p.prior_lse = prior_lse; p.pl_st = pl_st;
+  p.ws_cnt = nullptr; p.ws_lse = nullptr; p.ws_exp = nullptr; p.ws_o = nullptr;
+  if (fused) {
+    uint8_t* b = (uint8_t*)ws;
+    p.ws_cnt = (int*)b;
+    b += attn::ws_cnt_bytes(T, HG);
+    p.ws_lse = (float*)b;
+    b += attn::ws_lse_bytes(T, HG, S);
+    p.ws_exp = (float*)b;
+    b += attn::ws_lse_bytes(T, HG, S);
+    p.ws_o = (uint16_t*)b;
+  }
   const long long nwork = (long long)T * S * p.HG;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);
@@ -725,7 +951,22 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
                       float kv_scale, int S, void* out, long long o_st, long long o_sh, float* lse,
                       long long lse_st, float* opart, float* lsepart, void* stream) {
   return attn_launch(q, q_st, q_sh, pool, R, idx, idx_st, K, kcount, T, H, sm_scale, kv_scale, S, out, o_st, o_sh, lse,
-                     lse_st, opart, lsepart, nullptr, 0, 0, nullptr, 0, stream);
+                     lse_st, opart, lsepart, nullptr, 0, 0, nullptr, 0, nullptr, 0, stream);
+}
+
+long long spmla_attn_ws_bytes(int T, int H, int S) {
+  if (T < 0 || H <= 0 || S <= 0) return -1;
+  if (S == 1) return 0;
+  const int HG = (H + attn::HGW - 1) / attn::HGW;
+  return attn::ws_cnt_bytes(T, HG) + 2 * attn::ws_lse_bytes(T, HG, S) + attn::ws_o_bytes(T, HG, S);
+}
+
+int spmla_attn(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
+               long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale, int S,
+               void* out, long long o_st, long long o_sh, float* lse, long long lse_st, void* ws, long long ws_bytes,
+               void* stream) {
+  return attn_launch(q, q_st, q_sh, pool, R, idx, idx_st, K, kcount, T, H, sm_scale, kv_scale, S, out, o_st, o_sh, lse,
+                     lse_st, nullptr, nullptr, nullptr, 0, 0, nullptr, 0, S > 1 ? ws : nullptr, ws_bytes, stream);
 }
 
 int spmla_attn_merge(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
@@ -735,7 +976,7 @@ int spmla_attn_merge(const void* q, long long q_st, long long q_sh, const void* 
   if (T > 0 && (!prior_o || !prior_lse)) return SPMLA_EARG;
   if (((uintptr_t)prior_o & 15) || (po_st & 3) || (po_sh & 3)) return SPMLA_EALIGN;
   return attn_launch(q, q_st, q_sh, pool, R, idx, idx_st, K, kcount, T, H, sm_scale, kv_scale, 1, out, o_st, o_sh, lse,
-                     lse_st, nullptr, nullptr, prior_o, po_st, po_sh, prior_lse, pl_st, stream);
+                     lse_st, nullptr, nullptr, prior_o, po_st, po_sh, prior_lse, pl_st, nullptr, 0, stream);
 }
 
 int spmla_lse_merge(const void* parts, int parts_bf16, long long o_ps, long long o_st, long long o_sh,

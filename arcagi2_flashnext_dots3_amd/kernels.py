@@ -170,16 +170,21 @@ def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P
     return out
 
 
-_TOPK_WS = {}
+_WS = {}
 
 
-def _topk_ws(device, nbytes):
-    """Per-device workspace of spmla_topk_ws (grown on demand; reused by calls on the same stream)."""
-    key = torch.device(device)
-    b = _TOPK_WS.get(key)
+def _workspace(kind, device, nbytes, zero=False):
+    """Device workspace of one kind of call, per (device, current stream): calls queued on one stream run in order,
+    so they can share it; calls on other streams get their own. Grown on demand; a replaced buffer returns to
+    torch's caching allocator under its stream, which hands it only to later work of that stream. zero: allocated
+    zero-filled (the attention's arrival counters; the kernel leaves them at zero after every launch)."""
+    dev = torch.device(device)
+    key = (kind, dev, torch.cuda.current_stream(dev).cuda_stream)
+    b = _WS.get(key)
     if b is None or b.numel() < nbytes:
-        b = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=key)
-        _TOPK_WS[key] = b
+        n = max(nbytes, 256)
+        b = torch.zeros(n, dtype=torch.uint8, device=dev) if zero else torch.empty(n, dtype=torch.uint8, device=dev)
+        _WS[key] = b
     return b
 
 
@@ -197,7 +202,7 @@ def topk(logits, ctx, K, out=None, single_pass=False):
                   out.stride(0), _stream(logits))
         return out
     nb = int(_lib.lib().spmla_topk_ws_bytes(rows, Lc, K))
-    ws = _topk_ws(logits.device, nb)
+    ws = _workspace("topk", logits.device, nb)
     _lib.call("spmla_topk_ws", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
               out.stride(0), ws.data_ptr(), ws.numel(), _stream(logits))
     return out
@@ -492,8 +497,9 @@ def auto_split(T, H, K, cus=256):
 
 def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None, kcount=None, ws=None, R=None):
     """q [T, H, 576] bf16, pool [R, 656] uint8 Row656 rows (or a mapped host address with R given), idx [T, K]
-    int32 rows -> (out [T, H, 512] bf16, lse [T, H] fp32). split > 1 cuts K into partials merged by lse_merge
-    (None: auto_split)."""
+    int32 rows -> (out [T, H, 512] bf16, lse [T, H] fp32). split > 1 (at most 8) cuts K into partials that the
+    kernel merges (spmla_attn; ws: a zero-initialized uint8 workspace of spmla_attn_ws_bytes, else a cached one);
+    None: auto_split."""
     T, H, _ = q.shape
     K = idx.shape[1]
     if split is None:
@@ -511,14 +517,14 @@ def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None,
                   idx.stride(0), K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), 1, out.data_ptr(),
                   out.stride(0), out.stride(1), lse.data_ptr(), lse.stride(0), None, None, st)
         return out, lse
+    _need(1 <= split <= 8, "attend: split must be 1 .. 8")
+    nb = int(_lib.lib().spmla_attn_ws_bytes(T, H, split))
     if ws is None:
-        ws = (torch.empty(split, T, H, D_LAT, dtype=torch.float32, device=q.device),
-              torch.empty(split, T, H, dtype=torch.float32, device=q.device))
-    opart, lpart = ws
-    _lib.call("spmla_attn_splitk", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(), idx.stride(0),
-              K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), split, None, 0, 0, None, 0,
-              opart.data_ptr(), lpart.data_ptr(), st)
-    lse_merge(opart, lpart, out=out, lse=lse)
+        ws = _workspace("attn", q.device, nb, zero=True)
+    _need(ws.dtype == torch.uint8 and ws.numel() >= nb, "attend: workspace too small")
+    _lib.call("spmla_attn", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(), idx.stride(0), K,
+              _ptr(kcount), T, H, float(sm_scale), float(kv_scale), split, out.data_ptr(), out.stride(0),
+              out.stride(1), lse.data_ptr(), lse.stride(0), ws.data_ptr(), ws.numel(), st)
     return out, lse
 
 

@@ -256,6 +256,22 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
                       float kv_scale, int S, void* out, long long o_st, long long o_sh, float* lse,
                       long long lse_st, float* opart, float* lsepart, void* stream);
 
+/* Bytes of the workspace spmla_attn needs for T tokens, H heads and S splits (0 for S = 1; -1 for bad sizes). */
+long long spmla_attn_ws_bytes(int T, int H, int S);
+
+/* spmla_attn_splitk with the bf16 out + lse for any S in 1 .. 8: the S splits of a (token, group of 128 heads) merge
+ * in the kernel -- each writes its normalized partial (f16, with a power-of-two exponent per head that keeps it in
+ * range) and lse to ws, and the last split to arrive merges all of them (weights e^(lse_s - M) / Z) into out / lse.
+ * ws: spmla_attn_ws_bytes(T, H, S) bytes, 256-byte aligned, zero-filled once when allocated (the kernel leaves its
+ * arrival counters at zero after every launch, so one workspace serves launches that run one after another; launches
+ * that may overlap need workspaces of their own). out 16-byte aligned rows give 16-byte stores. S > 8: SPMLA_ELIMIT.
+ * Replaces the split-K decode launch with its partial combine (oa2_v2_launch dotsnote/engine/arcstats_pkg/arcstats/
+ * csrc/offload_attn2.cu:2021-2104; _sparse_mla_offload_split_kernel + _combine_kernel sparse_offload.py:419-538). */
+int spmla_attn(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
+               long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale, int S,
+               void* out, long long o_st, long long o_sh, float* lse, long long lse_st, void* ws, long long ws_bytes,
+               void* stream);
+
 /* spmla_attn_splitk (S = 1) whose result is merged with a prior partial of the same tokens and heads before the bf16
  * write: prior_o [T][H][512] fp32 normalized (strides po_st, po_sh; 16-byte aligned), prior_lse [T][H] (stride
  * pl_st, natural log). out = w o + w' prior_o with w = e^lse / (e^lse + e^lse'), w' = e^lse' / (e^lse + e^lse'),
