@@ -33,6 +33,7 @@ SIGNATURES = {
     "spmla_gather_tiers": [P, LL, I, P, LL, P, I, I, P, LL, P],
     "spmla_copy_rows": [P, LL, P, P, LL, P, I, I, P],
     "spmla_row400_gather": [P, LL, P, I, P, LL, I, I, P],
+    "spmla_row576_gather": [P, LL, P, I, P, LL, P],
     "spmla_row400_copy": [P, LL, P, P, LL, P, I, I, P],
     "spmla_row400_gather_tiers": [P, LL, P, LL, P, I, I, P, LL, I, P],
     "spmla_tier_split": [P, LL, I, I, P, LL, P, LL, P, P, LL, P, P],

@@ -560,6 +560,7 @@ int spmla_attn_packed(const void* q, long long q_st, long long q_sh, const void*
                       long long o_sh, float* lse, long long lse_st, float* opart, float* lsepart, void* stream) {
   if (T < 0 || nreq < 0 || H <= 0 || nmax < 0 || S <= 0 || R < 0 || (!cu && ql <= 0)) return SPMLA_EARG;
   if (tpg != 1 && tpg != 2 && tpg != 4 && tpg != 8) return SPMLA_EARG;
+  if (!cu && ql > 6) return SPMLA_EARG;                                // at most 6 tokens per request
   if (T == 0 || nreq == 0) return SPMLA_OK;
   if (!q || !u || !mk || !cnt || (R > 0 && !pool)) return SPMLA_EARG;
   const bool f32part = opart != nullptr;

@@ -104,6 +104,37 @@ struct DecodeRow400 {
   }
 };
 
+// Row576 (the reference's per-tensor rows: 512 + 64 e4m3 codes) -> Row656 staging for the attention: the codes as
+// they are, scales 1.0 (0 for an absent row, which is all zeros), the rope widened to bf16 (exact for every e4m3
+// value; the NaN codes widen to 0x7fc0 as above). Lanes 0..35 hold the row's chunks: lanes 0..31 write the codes,
+// lanes 32..35 widen 16 rope codes each, lanes 0..3 write the scales.
+struct DecodeRow576 {
+  static constexpr int LDS = 0;
+  __device__ u32x4 load(const uint8_t* s, int lane) const { return load_row(s, ROW576, lane); }
+  __device__ void emit(u32x4 v, bool valid, uint8_t* d, int lane, SPMLA_LDS uint8_t*) const {
+    if (lane < 32) *(u32x4*)(d + 16 * lane) = v;
+    if (lane < 4) *(float*)(d + SC_OFF + 4 * lane) = valid ? 1.0f : 0.0f;
+    if (lane >= 32 && lane < 36) {
+      uint32_t b[8];
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          uint32_t h[2];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const uint8_t x = (uint8_t)(v[w] >> (8 * (e + i)));
+            h[i] = (x & 0x7fu) == 0x7fu ? 0x7fc0u : f2u(e4m3_to_f32(x)) >> 16;
+          }
+          b[2 * w + e / 2] = h[0] | (h[1] << 16);
+        }
+      uint8_t* r = d + ROPE_OFF + 32 * (lane - 32);
+      *(u32x4*)r = u32x4{b[0], b[1], b[2], b[3]};
+      *(u32x4*)(r + 16) = u32x4{b[4], b[5], b[6], b[7]};
+    }
+  }
+};
+
 __device__ inline long long readlane64(long long x, int j) {
   const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)x, j), hi = __builtin_amdgcn_readlane((uint32_t)(x >> 32), j);
   return (long long)(((uint64_t)hi << 32) | lo);
@@ -449,6 +480,18 @@ int spmla_row400_gather(const void* src, long long R, const long long* rows, int
   hipLaunchKernelGGL(gth::gather_kernel<gth::DecodeRow400>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      (const uint8_t*)src, R, ROW400, rows, n, (uint8_t*)dst, dst_stride, (const long long*)nullptr,
                      0ll, gth::DecodeRow400{dst_fmt});
+  return (int)hipGetLastError();
+}
+
+int spmla_row576_gather(const void* src, long long R, const long long* rows, int n, void* dst, long long dst_stride,
+                        void* stream) {
+  if (n < 0 || R < 0) return SPMLA_EARG;
+  if (n == 0) return SPMLA_OK;
+  if (!src || !rows || !dst) return SPMLA_EARG;
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < ROW656) return SPMLA_EALIGN;
+  hipLaunchKernelGGL(gth::gather_kernel<gth::DecodeRow576>, dim3((unsigned)((n + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)src, R, ROW576, rows, n, (uint8_t*)dst, dst_stride,
+                     (const long long*)nullptr, 0ll, gth::DecodeRow576{});
   return (int)hipGetLastError();
 }
 

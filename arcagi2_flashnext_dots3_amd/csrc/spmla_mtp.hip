@@ -139,6 +139,7 @@ extern "C" {
 int spmla_mtp_union(const int* idx, long long idx_st, int T, int ql, const int* cu, int nreq, long long R, int topk,
                     int nmax, int* u, unsigned char* mk, int* cnt, void* stream) {
   if (T < 0 || nreq < 0 || topk < 0 || nmax < 0 || R < 0 || (!cu && ql <= 0)) return SPMLA_EARG;
+  if (!cu && ql > mtp::GB) return SPMLA_EARG;                          // at most 6 tokens per request
   if (nreq == 0) return SPMLA_OK;
   if (!idx || !u || !mk || !cnt) return SPMLA_EARG;
   if (R >= (1ll << (32 - mtp::GB)) - 1) return SPMLA_ELIMIT;          // (row + 1) << 6 fits 32 bits

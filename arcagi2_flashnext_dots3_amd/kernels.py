@@ -163,6 +163,8 @@ def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P
         rpb, bstride = max(1, R), max(1, R) * KEYROW
     if out is None:
         out = torch.empty(rows, max(Lc, 1), dtype=torch.float32, device=q.device)
+    _need(out.dtype == torch.float32 and out.stride(1) == 1 and out.shape[0] >= rows and out.shape[1] >= Lc,
+          "out fp32 [rows, >= Lc] with contiguous rows")
     _lib.call("spmla_index_logits", q.data_ptr(), q.stride(0), q.stride(1), w.data_ptr(), w.stride(0),
               store.data_ptr(), R, rpb, bstride, block_table.data_ptr(), block_table.stride(0), block_size,
               req.data_ptr(), ctx.data_ptr(), rows, H, D, Lc, P, rank, int(bool(noinf)), out.data_ptr(),
@@ -196,7 +198,8 @@ def topk(logits, ctx, K, out=None, single_pass=False):
     _need(ctx.dtype == torch.int32 and ctx.is_contiguous(), "ctx int32")
     if out is None:
         out = torch.empty(rows, K, dtype=torch.int32, device=logits.device)
-    _need(out.dtype == torch.int32 and out.stride(1) == 1, "out int32")
+    _need(out.dtype == torch.int32 and out.stride(1) == 1 and out.shape[0] >= rows and out.shape[1] >= K,
+          "out int32 [rows, >= K] with contiguous rows")
     if single_pass:
         _lib.call("spmla_topk", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
                   out.stride(0), _stream(logits))
@@ -264,7 +267,9 @@ def gather(src, rows, out, R=None, pcie=False):
     pcie: src is pinned host memory; the copy then runs on a fixed 64-workgroup grid (spmla_gather_pcie)."""
     n = rows.shape[0]
     rowb = out.shape[-1]
-    _need(rows.dtype == torch.int64, "rows int64")
+    _need(rows.dtype == torch.int64 and rows.is_contiguous(), "rows int64 contiguous")
+    _need(out.element_size() == 1 and out.dim() == 2 and out.stride(1) == 1 and out.shape[0] >= n,
+          "out of bytes (uint8 / float8) [>= n, row] with contiguous rows")
     _lib.call("spmla_gather_pcie" if pcie else "spmla_gather", src.data_ptr() if torch.is_tensor(src) else int(src),
               int(R if R is not None else src.shape[0]), rowb, rows.data_ptr(), n, out.data_ptr(), out.stride(0),
               _stream(out))
@@ -292,10 +297,26 @@ def row400_gather(src, rows, out, R=None, pcie=False):
     """out[i] = the GPU row (Row656 or Row576, by out's row width) of compact Row400 row src[rows[i]]; zero row when
     rows[i] is outside [0, R). src [R, 400] uint8 (pinned host memory with pcie=True, or HBM)."""
     n = rows.shape[0]
-    _need(rows.dtype == torch.int64, "rows int64")
+    _need(rows.dtype == torch.int64 and rows.is_contiguous(), "rows int64 contiguous")
+    _need(out.element_size() == 1 and out.dim() == 2 and out.stride(1) == 1 and out.shape[0] >= n,
+          "out of bytes (uint8 / float8) [>= n, row] with contiguous rows")
     _lib.call("spmla_row400_gather", src.data_ptr() if torch.is_tensor(src) else int(src),
               int(R if R is not None else src.shape[0]), rows.data_ptr(), n, out.data_ptr(), out.stride(0),
               _dst_fmt(out), int(bool(pcie)), _stream(out))
+    return out
+
+
+def row576_gather(src, rows, out, R=None):
+    """out[i] = Row656 staging of Row576 row src[rows[i]] (codes as they are, scales 1.0, rope widened to bf16); zero
+    row when rows[i] is outside [0, R). src [R, 576] uint8 (or a flat view of a paged cache), rows int64 [n]."""
+    n = rows.numel()
+    _need(rows.dtype == torch.int64 and rows.is_contiguous(), "rows int64 contiguous")
+    _need(out.dtype == torch.uint8 and out.dim() == 2 and out.shape[1] == ROW656 and out.stride(1) == 1,
+          "out [n, 656] uint8 rows")
+    _need(out.shape[0] >= n, "out has fewer rows than rows")
+    Rv = int(R if R is not None else src.shape[0])
+    _lib.call("spmla_row576_gather", src.data_ptr(), Rv, rows.data_ptr(), n, out.data_ptr(), out.stride(0),
+              _stream(out))
     return out
 
 
@@ -645,8 +666,10 @@ def mtp_union(idx, ql=None, cu=None, R=None, nmax=None):
         cu = cu.to(torch.int32).contiguous()
         nreq, ql_ = cu.shape[0] - 1, 0
         gmax = 6
+        if nreq > 0:   # the kernels take at most 6 tokens of a request: a longer request is an error, not a cut
+            _need(int((cu[1:] - cu[:-1]).max().item()) <= 6, "mtp_union: at most 6 tokens per request")
     else:
-        _need(ql is not None and ql > 0, "mtp_union: ql or cu")
+        _need(ql is not None and 0 < ql <= 6, "mtp_union: ql (1 .. 6) or cu")
         nreq, ql_ = (T + ql - 1) // ql, int(ql)
         gmax = min(ql, 6)
     if nmax is None:
@@ -668,6 +691,7 @@ def attend_packed(q, pool, idx, sm_scale, kv_scale=1.0, ql=None, cu=None, out=No
     T, H, _ = q.shape
     _need(attention_ok(q, idx), "attend_packed: q must be bf16 [T, H, 576] with 16-byte aligned rows, idx int32")
     R = int(pool.shape[0])
+    _need(cu is not None or (ql is not None and 0 < ql <= 6), "attend_packed: ql (1 .. 6) or cu")
     u, mk, cnt = union if union is not None else mtp_union(idx, ql=ql, cu=cu, R=R)
     nreq, nmax = u.shape
     if tpg is None:

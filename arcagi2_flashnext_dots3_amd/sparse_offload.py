@@ -20,12 +20,38 @@ host tier's rows are first copied over PCIe into an HBM staging area (spmla_gath
 and attended there by spmla_attn_merge, which merges the HBM tier's partial exactly in its epilogue (the
 reference's tier combine). Without a cache (C = 0) every row takes the host tier.
 """
+import os
+
 import torch
 
 from . import kernels
 
 ROW = kernels.ROW656
 HOST_ROW = {"row656": kernels.ROW656, "e2m2": kernels.ROW400}
+
+
+def host_memory_available():
+    """Bytes of host memory the kernel reports available (MemAvailable of /proc/meminfo), None when unknown."""
+    try:
+        with open("/proc/meminfo") as fh:
+            for line in fh:
+                if line.startswith("MemAvailable:"):
+                    return int(line.split()[1]) * 1024
+    except OSError:
+        pass
+    return None
+
+
+def check_host_budget(nbytes, available=None):
+    """Refuse a pinned host pool larger than a fraction of the available host memory (ARC_OFFLOAD_HOST_FRAC, default
+    0.5): pinned pages stay resident, so an oversized pool would exhaust the host instead of failing here (the
+    reference's guard, sparse_offload.py:925-932)."""
+    frac = float(os.environ.get("ARC_OFFLOAD_HOST_FRAC", "0.5"))
+    avail = host_memory_available() if available is None else available
+    if avail and nbytes > frac * avail:
+        raise RuntimeError(f"offload host pool of {nbytes / 2**30:.1f} GiB exceeds {frac:.0%} of the "
+                           f"{avail / 2**30:.1f} GiB of available host memory: give the layer fewer host rows "
+                           f"(or raise ARC_OFFLOAD_HOST_FRAC)")
 
 
 def hot_rows_by_frequency(counts, C):
@@ -66,6 +92,7 @@ class LayerOffload:
         self.device = torch.device(device)
         self.key = key
         self.row_fmt = row_fmt
+        check_host_budget(self.R * HOST_ROW[row_fmt])
         self.host = torch.zeros((self.R, HOST_ROW[row_fmt]), dtype=torch.uint8, pin_memory=True)
         self.C = min(int(cache_rows), self.R)
         if cache_fmt not in HOST_ROW or (cache_fmt == "e2m2" and (row_fmt != "e2m2" or cache_mode != "static")):

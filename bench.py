@@ -59,11 +59,31 @@ def _timed(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo, as lscpu prints it) and its logical CPU count."""
+    name, n = None, 0
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    n += 1
+                    name = name or line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return f"{name or 'unknown'} ({n} logical CPUs)" if n else (name or "unknown")
+
+
+def _with_model(cpu):
+    if isinstance(cpu, dict) and "cpu_model" not in cpu:
+        cpu = dict(cpu, cpu_model=cpu_model())
+    return cpu
+
+
 def _line(metric, value, unit, a, ms, dtype, config, roofline, cpu=None, hib=True, **extra):
     res = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": a.steps,
            "warmup": a.warmup, "ms_per_step": round(ms, 5), "higher_is_better": hib, "scaling": "weak",
            "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded)", "config": config,
-           "roofline": roofline, "cpu_baseline": cpu}
+           "roofline": roofline, "cpu_baseline": _with_model(cpu)}
     res.update(extra)
     return res
 
@@ -162,7 +182,7 @@ def run_config2(a, dev):
     res = _line(METRIC, gbs, "GB/s", a, ms, "fp8e4m3 rows x bf16 q: bf16 MFMA (QK and PV), fp32 accumulate",
                 cfg, roof, step_us=round(ms * 1e3, 2), eager_step_us=round(eager_ms * 1e3, 2))
     if not a.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(pool, q, idxs[0])
+        res["cpu_baseline"] = _with_model(cpu_baseline(pool, q, idxs[0]))
     del pool
     torch.cuda.empty_cache()
     return res

@@ -148,6 +148,15 @@ int spmla_gather_tiers(const void* src, long long R, int row_bytes, const int* r
 int spmla_row400_gather(const void* src, long long R, const long long* rows, int n, void* dst, long long dst_stride,
                         int dst_fmt, int pcie, void* stream);
 
+/* Gather of Row576 rows (the reference's per-tensor fp8 rows: 512 + 64 e4m3 codes, one kv_scale per tensor) into
+ * Row656 staging rows for the attention: dst row i = src row rows[i] with its codes as they are, scales 1.0 and the
+ * rope widened to bf16 (exact); a row id outside [0, R) gives a zero row. Attending the staging with the tensor's
+ * kv_scale equals attending the Row576 rows. Replaces the Row576 row read of the portable attention
+ * (PortableSparseImpl._run, dotsnote/engine/arcstats_pkg/arcstats/dsa_sm89.py:379-391, through
+ * triton_bf16_mla_sparse_interface, vllm_patch/vllm/v1/attention/ops/xpu_mla_sparse.py:182-278). */
+int spmla_row576_gather(const void* src, long long R, const long long* rows, int n, void* dst, long long dst_stride,
+                        void* stream);
+
 /* Row400 copy with decode: dst row dst_rows[i] (rows of dst_fmt's size) = the GPU row of src row src_rows[i]; pairs
  * with a side outside its range ([0, R_src), [0, R_dst)) are skipped. Fills GPU-format cache lines from compact host
  * rows. Replaces offload_rowfmt.refill / write_through (_rows_kernel MODE 1 and _wt_kernel, offload_rowfmt.py:187-249,
@@ -342,10 +351,11 @@ int spmla_mqa_logits(const void* q, long long q_st, long long q_sh, const float*
                      float* out, long long out_st, void* stream);
 
 /* Request-packed MTP decode, the row list: for request r (tokens cu[r] .. cu[r + 1], or r * ql .. + ql clipped to
- * T; at most the first 6 used), u[r][0 .. cnt[r]) = the distinct rows 0 <= row < R of those tokens' top-k lists
+ * T), u[r][0 .. cnt[r]) = the distinct rows 0 <= row < R of those tokens' top-k lists
  * (idx [T][topk], row stride idx_st), mk[r][i] = bit j set when token j selected row u[r][i]; ordered by mask
  * descending, then by the position j * topk + k of the row's first occurrence; u[r][cnt .. nmax) = -1.
- * nmax >= (tokens used) * topk, R < 2^26 - 1, topk <= 2048.
+ * nmax >= (tokens used) * topk, R < 2^26 - 1, topk <= 2048. A request holds at most 6 tokens: ql > 6 is
+ * SPMLA_EARG; with cu the caller guarantees it (the boundaries stay on the device; the Python wrapper checks them).
  * Replaces pk_union_kernel (dotsnote/engine/arcstats_pkg/arcstats/csrc/offload_attn.cu:586-698, ARC_OFFLOAD_CUDA_PK). */
 int spmla_mtp_union(const int* idx, long long idx_st, int T, int ql, const int* cu, int nreq, long long R, int topk,
                     int nmax, int* u, unsigned char* mk, int* cnt, void* stream);
@@ -353,7 +363,7 @@ int spmla_mtp_union(const int* idx, long long idx_st, int T, int ql, const int* 
 /* Request-packed MTP decode attention over the union rows of spmla_mtp_union (u, mk, cnt; row capacity nmax): a
  * workgroup's 32 query columns are tpg (1, 2, 4, 8) tokens of one request x 32 / tpg heads, so each union row is
  * loaded and converted once for all of them; a column's softmax uses only the rows its token's mask holds. Request
- * r = tokens cu[r] .. cu[r + 1] (or r * ql .. + ql clipped to T), the first min(tpg, 6) of them computed. Results
+ * r = tokens cu[r] .. cu[r + 1] (or r * ql .. + ql clipped to T), at most 6 of them (ql > 6: SPMLA_EARG). Results
  * and outputs as spmla_attn_splitk for each token (S splits of the union with fp32 partials, or S = 1 with the
  * bf16 out + lse), up to the fp32 summation order of the rows.
  * Replaces pk_attn_kernel (dotsnote/engine/arcstats_pkg/arcstats/csrc/offload_attn.cu:700-1153). */

@@ -96,10 +96,31 @@ def test_version():
     (("spmla_mtp_union", 256, 8, 4, 4, None, 1, 1 << 26, 8, 32, 256, 256, 256, None), -5),
     (("spmla_attn_packed", None, 0, 0, None, 0, None, None, None, 0, None, 4, 1, 4, 128, 3, 1.0, 1.0, 1, None, 0, 0,
       None, 0, None, None, None), -2),
+    # requests of more than 6 MTP tokens are rejected, not cut to their first 6
+    (("spmla_mtp_union", 256, 8, 14, 7, None, 2, 100, 8, 64, 256, 256, 256, None), -2),
+    (("spmla_attn_packed", 256, 0, 0, 256, 100, 256, 256, 256, 64, None, 7, 2, 14, 128, 8, 1.0, 1.0, 1, 256, 0, 0,
+      256, 0, None, None, None), -2),
+    (("spmla_row576_gather", None, 0, None, -1, None, 656, None), -2),
+    (("spmla_row576_gather", 256, 10, 256, 4, 256, 576, None), -3),
+    # the in-kernel split merge: a workspace is required, at most 8 splits
+    (("spmla_attn", 256, 64, 64, 256, 100, 256, 8, 8, None, 1, 1, 1.0, 1.0, 4, 256, 512, 512, 256, 1, None, 0, None),
+     -2),
+    (("spmla_attn", 256, 64, 64, 256, 100, 256, 16, 16, None, 1, 1, 1.0, 1.0, 9, 256, 512, 512, 256, 1, 256, 1 << 30,
+      None), -5),
 ])
 def test_argument_rejection(call, code):
     from arcagi2_flashnext_dots3_amd import _lib
     assert getattr(_lib.lib(), call[0])(*call[1:]) == code
+
+
+def test_attention_workspace_size():
+    from arcagi2_flashnext_dots3_amd import _lib
+    L = _lib.lib()
+    assert L.spmla_attn_ws_bytes(64, 128, 1) == 0 and L.spmla_attn_ws_bytes(-1, 128, 4) == -1
+    four = L.spmla_attn_ws_bytes(64, 128, 4)
+    # the f16 partials (4 splits x 64 tokens x 128 heads x 512) plus counters, lse and exponents
+    assert four >= 4 * 64 * 128 * 512 * 2 and four % 256 == 0
+    assert L.spmla_attn_ws_bytes(64, 160, 4) > four                 # two head groups
 
 
 def test_topk_workspace_size():

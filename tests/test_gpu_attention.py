@@ -109,3 +109,17 @@ def test_attend_merge_two_tiers(dev):
     assert np.abs(l[fin] - l_ref[fin]).max() <= LSE_TOL
     assert np.abs(o - o_m.float().cpu().numpy()).max() <= 2.0 ** -7 * max(1.0, np.abs(o).max())
     assert np.abs(l[fin] - l_m.cpu().numpy()[fin]).max() <= 1e-5
+
+
+def test_nan_row_zero_is_never_read(dev):
+    """Invalid entries (-1, out of range, past kcount) read the kernel's own zero row, not row 0 of the pool: with
+    row 0 set to NaN codes, scales and rope, and never selected, outputs and lse stay finite and equal the oracle."""
+    T, H, R, K = 3, 64, 2048, 512
+    pool, _, _ = make_pool_656(R, seed=13)
+    pool[0, :] = 0xFF                                      # e4m3 NaN codes, NaN scales and rope
+    g = torch.Generator().manual_seed(14)
+    idx = (torch.randperm(R - 1, generator=g)[:T * K] + 1).view(T, K).to(torch.int32)   # row 0 never selected
+    idx[0, ::3] = -1
+    idx[1, 100:] = R + 7
+    kc = torch.tensor([K, K, 37], dtype=torch.int32)
+    _check(dev, T=T, H=H, R=R, K=K, idx=idx, kcount=kc, seed=14, pool=pool)

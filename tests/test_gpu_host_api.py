@@ -256,3 +256,76 @@ def test_portable_impl_offload_decode_and_prefill(dev):
     e_o = np.max(np.abs(out.float().cpu().numpy() - eo) / np.maximum(1.0, np.abs(eo)))
     print(f"[offload impl] err o {e_o:.2e}", flush=True)
     assert e_o <= 1e-2
+
+
+def test_portable_impl_paged_decode_row576(dev):
+    """The reference's deployed cache: 576-byte per-tensor fp8 rows ("fp8", dsa_sm89.py:551-562) written with a
+    k_scale and attended with the layer's _k_scale_float (dsa_sm89.py:379-391), against the fp64 oracle over the same
+    Row576 rows; the Row576 -> Row656 staging gather byte-checked (codes as stored, scales 1.0, rope widened: torch's
+    float8_e4m3fn -> bfloat16 conversion)."""
+    from types import SimpleNamespace
+    from arcagi2_flashnext_dots3_amd import kernels
+    from arcagi2_flashnext_dots3_amd.dsa import CommonAttentionMetadata, PortableSparseBackend
+    nreq, bs, nb, L, H, K, ks = 3, 64, 64, 1000, 128, 256, 0.05
+    Impl, bt, slots, kv, pe = _paged_setup(dev, nreq, bs, nb, L, 16)
+    cache = torch.zeros(nb, bs, 576, dtype=torch.uint8, device=dev)
+    g = torch.Generator().manual_seed(17)
+    topk = torch.stack([torch.randperm(L, generator=g)[:K] for _ in range(nreq)]).to(torch.int32)
+    topk[2, 50:] = -1
+    impl = Impl(H, 576, SM, 1, None, None, "fp8", None, "decoder", None, topk_indices_buffer=topk.to(dev))
+    impl.do_kv_cache_update(kv.to(dev), pe.to(dev), cache, slots.to(dev), "fp8", ks)
+    builder = PortableSparseBackend.get_builder_cls()(bs, K, 16, dev)
+    cam = CommonAttentionMetadata(query_start_loc=torch.arange(nreq + 1, dtype=torch.int32, device=dev),
+                                  num_reqs=nreq, num_actual_tokens=nreq, max_query_len=1, max_seq_len=L,
+                                  slot_mapping=slots[:nreq].to(dev), block_table_tensor=bt.to(dev))
+    md = builder.build(0, cam)
+    q = make_q(nreq, H, seed=18)
+    print("[row576] paged decode through PortableSparseImpl", flush=True)
+    out, _ = impl.forward_mqa(q.to(dev), cache, md, SimpleNamespace(_k_scale_float=ks))
+    torch.cuda.synchronize()
+    flat = cache.cpu().numpy().reshape(-1, 576)
+    rows = ref.rows_from_topk(topk.numpy(), np.arange(nreq), bt.numpy(), bs)
+    eo, el = ref.attention(q.float().numpy(), flat, rows, SM, ks, fmt=576)
+    o = out.float().cpu().numpy()
+    assert np.all(np.abs(o - eo) <= 1e-2 + 2.0 ** -7 * np.abs(eo).max(axis=-1, keepdims=True))
+    # the staging rows themselves
+    want = torch.tensor([5, -1, 17, nb * bs, 63, 0], dtype=torch.int64)
+    staged = torch.full((6, 656), 0xAB, dtype=torch.uint8, device=dev)
+    kernels.row576_gather(cache.view(-1, 576), want.to(dev), staged)
+    s = staged.cpu().numpy()
+    for i, r in enumerate(want.tolist()):
+        if 0 <= r < nb * bs:
+            src = flat[r]
+            assert np.array_equal(s[i, :512], src[:512])
+            assert np.array_equal(s[i, 512:528].view(np.float32), np.ones(4, np.float32))
+            rope = torch.from_numpy(src[512:].copy()).view(torch.float8_e4m3fn).to(torch.bfloat16)
+            assert np.array_equal(s[i, 528:].view(np.uint16), rope.view(torch.int16).numpy().view(np.uint16))
+        else:
+            assert not s[i].any()
+
+
+def test_offload_decode_q_with_extra_heads(dev):
+    """q carries more heads than the layer owns (the padded-head layout): the offload path returns the layer's heads
+    of LayerOffload.attend's result, equal to the oracle over those heads."""
+    from arcagi2_flashnext_dots3_amd.dsa import DecodeMetadata, IndexerMetadata
+    nreq, bs, nb, L, Hq, H, K = 2, 64, 40, 900, 128, 64, 128
+    Impl, bt, slots, kv, pe = _paged_setup(dev, nreq, bs, nb, L, 20)
+    cache = torch.zeros(nb, bs, 656, dtype=torch.uint8, device=dev)
+    g = torch.Generator().manual_seed(21)
+    topk = torch.stack([torch.randperm(L, generator=g)[:K] for _ in range(nreq)]).to(torch.int32)
+    impl = Impl(H, 576, SM, 1, None, None, "fp8_ds_mla", None, "decoder", None, topk_indices_buffer=topk.to(dev),
+                offload=True)
+    impl.do_kv_cache_update(kv.to(dev), pe.to(dev), cache, slots.to(dev), "fp8_ds_mla", 1.0)
+    im = IndexerMetadata(num_decode_tokens=nreq, num_decodes=nreq, num_prefill_tokens=0,
+                         decode=DecodeMetadata(block_table=bt.to(dev), seq_lens=torch.full((nreq,), L, device=dev),
+                                               decode_lens=torch.ones(nreq, device=dev)))
+    q = make_q(nreq, Hq, seed=22)
+    print("[offload] q with 128 heads, layer with 64", flush=True)
+    out, _ = impl.forward_mqa(q.to(dev), cache, im, None)
+    torch.cuda.synchronize()
+    assert out.shape == (nreq, H, 512)
+    flat = np.zeros((nb * bs, 656), dtype=np.uint8)
+    ref.cache_write_656(bf16_bits(kv), bf16_bits(pe.reshape(-1, 64)), slots.numpy(), flat)
+    rows = ref.rows_from_topk(topk.numpy(), np.arange(nreq), bt.numpy(), bs)
+    eo, _ = ref.attention(q[:, :H].float().numpy(), flat, rows.astype(np.int32), SM)
+    assert np.max(np.abs(out.float().cpu().numpy() - eo) / np.maximum(1.0, np.abs(eo))) <= 1e-2

@@ -41,11 +41,15 @@ def test_mtp_union_boundaries(dev):
     g = np.random.default_rng(9)
     T, topk, R = 9, 256, 2000
     idx = np.stack([g.choice(R, topk, replace=False) for _ in range(T)]).astype(np.int32)
-    cu = np.array([0, 2, 2, 9], dtype=np.int32)                        # an empty request; one of 7 tokens (6 used)
+    cu = np.array([0, 2, 2, 8], dtype=np.int32)                        # an empty request; one of 6 tokens
     u, mk, cnt = kernels.mtp_union(torch.from_numpy(idx).to(dev), cu=torch.from_numpy(cu).to(dev), R=R)
     torch.cuda.synchronize()
     eu, emk, ecnt = ref.mtp_union(idx, T, None, cu, 3, R, nmax=u.shape[1])
     assert np.array_equal(cnt.cpu().numpy(), ecnt) and np.array_equal(u.cpu().numpy(), eu)
+    # a request of 7 tokens is refused (the kernels take at most 6), not cut to its first 6
+    with pytest.raises(ValueError, match="at most 6"):
+        kernels.mtp_union(torch.from_numpy(idx).to(dev), cu=torch.tensor([0, 2, 9], dtype=torch.int32, device=dev),
+                          R=R)
 
 
 def _mtp_inputs(B, ql, H, R, K, shared, seed):
@@ -91,21 +95,22 @@ def test_attend_packed_vs_oracle_and_per_token(dev, B, ql, H, K, shared, split):
 
 
 def test_attend_packed_variable_requests(dev):
-    """cu boundaries: requests of 3, 1, 0 and 7 tokens (the first 6 of the last computed, the 7th left untouched)."""
+    """cu boundaries: requests of 3, 1, 0 and 6 tokens, every token computed; a request of 7 tokens is refused."""
     from arcagi2_flashnext_dots3_amd import kernels
     H, R, K = 64, 4096, 512
-    idx, pool, q = _mtp_inputs(1, 11, H, R, K, 0.7, seed=5)
-    cu = torch.tensor([0, 3, 4, 4, 11], dtype=torch.int32)
+    idx, pool, q = _mtp_inputs(1, 10, H, R, K, 0.7, seed=5)
+    cu = torch.tensor([0, 3, 4, 4, 10], dtype=torch.int32)
     sm = 192 ** -0.5
     pd = torch.from_numpy(pool).to(dev)
-    out = torch.full((11, H, 512), 7.0, dtype=torch.bfloat16, device=dev)
-    lse = torch.full((11, H), 7.0, dtype=torch.float32, device=dev)
+    out = torch.full((10, H, 512), 7.0, dtype=torch.bfloat16, device=dev)
+    lse = torch.full((10, H), 7.0, dtype=torch.float32, device=dev)
     kernels.attend_packed(q.to(dev), pd, idx.to(dev), sm, cu=cu.to(dev), out=out, lse=lse)
     torch.cuda.synchronize()
     o_ref, l_ref = ref.attention(q.float().numpy(), pool, idx.numpy(), sm)
     o = out.float().cpu().numpy()
     l = lse.cpu().numpy()
-    done = [0, 1, 2, 3, 4, 5, 6, 7, 8, 9]
-    assert (np.abs(o[done] - o_ref[done]) / np.maximum(1.0, np.abs(o_ref[done]))).max() <= 1e-2
-    assert np.abs(l[done] - l_ref[done]).max() <= 1e-3
-    assert bool((out[10] == 7.0).all()) and bool((lse[10] == 7.0).all())
+    assert (np.abs(o - o_ref) / np.maximum(1.0, np.abs(o_ref))).max() <= 1e-2
+    assert np.abs(l - l_ref).max() <= 1e-3
+    with pytest.raises(ValueError, match="at most 6"):
+        kernels.attend_packed(q.to(dev), pd, idx.to(dev), sm, cu=torch.tensor([0, 3, 10], dtype=torch.int32,
+                                                                               device=dev))

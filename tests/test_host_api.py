@@ -111,3 +111,20 @@ def test_oracle_topk_merge_brute_force_and_composition():
     ctx = np.array([200, 150, 20, 0], dtype=np.int32)
     pk = ref.topk_local(x, ctx, 0, 1, 64)
     assert np.array_equal(ref.topk_merge(pk, 4, 1, 64, 64, 64), ref.topk(x, ctx, 64))
+
+
+def test_host_pool_capacity_guard(monkeypatch):
+    """A pinned host pool beyond ARC_OFFLOAD_HOST_FRAC (default half) of the available host memory is refused before
+    anything is pinned; within it, nothing is raised."""
+    from arcagi2_flashnext_dots3_amd import sparse_offload as so
+    avail = so.host_memory_available()                    # this host's MemAvailable
+    assert avail is None or avail > 0
+    monkeypatch.delenv("ARC_OFFLOAD_HOST_FRAC", raising=False)
+    so.check_host_budget(4 << 30, available=10 << 30)
+    with pytest.raises(RuntimeError, match="exceeds 50%"):
+        so.check_host_budget(6 << 30, available=10 << 30)
+    monkeypatch.setenv("ARC_OFFLOAD_HOST_FRAC", "0.8")
+    so.check_host_budget(6 << 30, available=10 << 30)
+    monkeypatch.setattr(so, "host_memory_available", lambda: 1 << 20)   # the constructor checks before pinning
+    with pytest.raises(RuntimeError, match="host pool"):
+        so.LayerOffload(1 << 20, "cpu")
