@@ -102,6 +102,9 @@ def test_version():
       256, 0, None, None, None), -2),
     (("spmla_row576_gather", None, 0, None, -1, None, 656, None), -2),
     (("spmla_row576_gather", 256, 10, 256, 4, 256, 576, None), -3),
+    # logits: local rows times P beyond 32-bit row arithmetic (R_local = INT_MAX / 4 + 1 with P = 4)
+    (("spmla_index_logits", 256, 64, 128, 256, 64, 256, (2 ** 31 - 1) // 4 + 1, 16, 2112, 256, 8, 64, 256, 256, 1,
+      64, 128, 64, 4, 0, 0, 256, 64, None), -5),
     # the in-kernel split merge: a workspace is required, at most 8 splits
     (("spmla_attn", 256, 64, 64, 256, 100, 256, 8, 8, None, 1, 1, 1.0, 1.0, 4, 256, 512, 512, 256, 1, None, 0, None),
      -2),

@@ -62,9 +62,9 @@ def test_fused_split_vs_oracle(dev, split):
     o_ref, l_ref = ref.attention(q.float().numpy(), pool, idx.numpy(), sm, 0.7, kcount=kc.numpy())
     _vs_oracle(o, l, o_ref, l_ref)
     o1, l1 = _run(dev, q, pool, idx, sm, 0.7, split=1, kcount=kc)
-    # both bf16 (one rounding step, 2^-7 relative, apart) and each within ~4e-5 absolute of the oracle from the f16
-    # P' / partials (2^-11 per term; cancelling sums near zero keep that absolute size)
-    viol = np.abs(o - o1) - (2.0 ** -7 * np.abs(o1) + 2e-4)
+    # both bf16 (one rounding step, 2^-7 relative, apart) with f16 P' / partials whose rounding (2^-11 per term) is
+    # relative to the head's terms, so it stays of that size where they cancel into a small output value
+    viol = np.abs(o - o1) - (2.0 ** -7 * np.abs(o1) + 2.0 ** -9 * np.abs(o1).max(axis=-1, keepdims=True) + 1e-5)
     w = np.unravel_index(viol.argmax(), viol.shape)
     assert viol.max() <= 0, f"fused vs single pass at {w}: {o[w]} vs {o1[w]} (oracle {o_ref[w]}), lse {l[w[:2]]} {l1[w[:2]]}"
     fin = np.isfinite(l1)
