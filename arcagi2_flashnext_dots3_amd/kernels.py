@@ -173,13 +173,14 @@ def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P
 
 
 _WS = {}
+_WS_CNT = {}      # attention workspaces: counter bytes of the last launch (the bytes known to be zero)
 
 
 def _workspace(kind, device, nbytes, zero=False):
     """Device workspace of one kind of call, per (device, current stream): calls queued on one stream run in order,
     so they can share it; calls on other streams get their own. Grown on demand; a replaced buffer returns to
     torch's caching allocator under its stream, which hands it only to later work of that stream. zero: allocated
-    zero-filled (the attention's arrival counters; the kernel leaves them at zero after every launch)."""
+    zero-filled (the attention's counters)."""
     dev = torch.device(device)
     key = (kind, dev, torch.cuda.current_stream(dev).cuda_stream)
     b = _WS.get(key)
@@ -187,7 +188,13 @@ def _workspace(kind, device, nbytes, zero=False):
         n = max(nbytes, 256)
         b = torch.zeros(n, dtype=torch.uint8, device=dev) if zero else torch.empty(n, dtype=torch.uint8, device=dev)
         _WS[key] = b
-    return b
+        _WS_CNT[key] = n if zero else 0
+    return b, key
+
+
+def _attn_counter_bytes(T, H):
+    """Leading counter bytes of spmla_attn's workspace: 4 per (token, group of 128 heads), 256-byte rounded."""
+    return (4 * T * ((H + 127) // 128) + 255) // 256 * 256
 
 
 def topk(logits, ctx, K, out=None, single_pass=False):
@@ -205,7 +212,7 @@ def topk(logits, ctx, K, out=None, single_pass=False):
                   out.stride(0), _stream(logits))
         return out
     nb = int(_lib.lib().spmla_topk_ws_bytes(rows, Lc, K))
-    ws = _workspace("topk", logits.device, nb)
+    ws, _ = _workspace("topk", logits.device, nb)
     _lib.call("spmla_topk_ws", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
               out.stride(0), ws.data_ptr(), ws.numel(), _stream(logits))
     return out
@@ -516,11 +523,17 @@ def auto_split(T, H, K, cus=256):
     return s
 
 
+def attn_ws_bytes(T, H, split):
+    """Bytes of the workspace attend needs for T tokens, H heads and `split` splits (0 for split 1)."""
+    return int(_lib.lib().spmla_attn_ws_bytes(T, H, split))
+
+
 def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None, kcount=None, ws=None, R=None):
     """q [T, H, 576] bf16, pool [R, 656] uint8 Row656 rows (or a mapped host address with R given), idx [T, K]
     int32 rows -> (out [T, H, 512] bf16, lse [T, H] fp32). split > 1 (at most 8) cuts K into partials that the
-    kernel merges (spmla_attn; ws: a zero-initialized uint8 workspace of spmla_attn_ws_bytes, else a cached one);
-    None: auto_split."""
+    kernel merges (spmla_attn; ws: a uint8 workspace of attn_ws_bytes whose leading counter bytes are zero -- the
+    kernel leaves them so --, else a cached one per stream; under HIP graph capture pass ws, or the capture stream's
+    new workspace is zero-filled by every replay); None: auto_split."""
     T, H, _ = q.shape
     K = idx.shape[1]
     if split is None:
@@ -541,7 +554,11 @@ def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None,
     _need(1 <= split <= 8, "attend: split must be 1 .. 8")
     nb = int(_lib.lib().spmla_attn_ws_bytes(T, H, split))
     if ws is None:
-        ws = _workspace("attn", q.device, nb, zero=True)
+        ws, key = _workspace("attn", q.device, nb, zero=True)
+        cnt = _attn_counter_bytes(T, H)
+        if cnt > _WS_CNT[key]:            # counter bytes the previous launch used as scratch: cleared by a fill kernel
+            ws[_WS_CNT[key]:cnt].zero_()
+        _WS_CNT[key] = cnt
     _need(ws.dtype == torch.uint8 and ws.numel() >= nb, "attend: workspace too small")
     _lib.call("spmla_attn", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(), idx.stride(0), K,
               _ptr(kcount), T, H, float(sm_scale), float(kv_scale), split, out.data_ptr(), out.stride(0),

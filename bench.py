@@ -153,10 +153,14 @@ def run_config2(a, dev):
     pool, q, idxs = build_inputs(dev, a.idx_sets)
     out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    split = kernels.auto_split(B, H, K)
+    # the split merge's workspace, zeroed once here: one allocated inside the graph capture would be zero-filled by
+    # every replay (the kernel leaves its counters at zero, so it needs that only once)
+    ws = torch.zeros(max(1, int(kernels.attn_ws_bytes(B, H, split))), dtype=torch.uint8, device=dev)
     cur = [0]
 
     def launch(i):
-        kernels.attend(q, pool, idxs[i], SM_SCALE, out=out, lse=lse)
+        kernels.attend(q, pool, idxs[i], SM_SCALE, out=out, lse=lse, split=split, ws=ws)
 
     def step():
         launch(cur[0] % len(idxs))
@@ -453,6 +457,12 @@ def run_config5(a, dev):
     flops = NQ * H * K * (2 * 576 + 2 * 512)
     tf = flops / (ms_a * 1e-3) / 1e12
     wb = NQ * (1024 + 128 + 8) + NQ * ROWB
+    # the offload prefill's staging gather (dsa_sm89.py:341-345): the chunk's distinct selected rows copied from the
+    # HBM cache into a dense staging area (one 656-byte read and write per row)
+    uniq = torch.unique(rows[rows >= 0].long())
+    staged = torch.empty(uniq.numel(), ROWB, dtype=torch.uint8, device=dev)
+    ms_g = _timed(lambda: kernels.gather(flat, uniq, staged), a.steps, a.warmup)
+    gb = 2 * uniq.numel() * ROWB
     cpu = None
     if not a.no_cpu:
         from oracle import cpu_port
@@ -474,7 +484,9 @@ def run_config5(a, dev):
                 {"workload": "BASELINE config 5: 8192 queries, 128 heads, top-2048 of <= 65536 prior rows; write "
                              "8192 rows at random slots of a paged cache (block 64)"}, roof, cpu, hib=False,
                 cache_write_us=round(ms_w * 1e3, 2),
-                cache_write_gbs=round(wb / (ms_w * 1e-3) / 1e9, 1))
+                cache_write_gbs=round(wb / (ms_w * 1e-3) / 1e9, 1),
+                staging_gather_rows=int(uniq.numel()), staging_gather_us=round(ms_g * 1e3, 2),
+                staging_gather_gbs=round(gb / (ms_g * 1e-3) / 1e9, 1))
     return res
 
 

@@ -270,10 +270,13 @@ long long spmla_attn_ws_bytes(int T, int H, int S);
 
 /* spmla_attn_splitk with the bf16 out + lse for any S in 1 .. 8: the S splits of a (token, group of 128 heads) merge
  * in the kernel -- each writes its normalized partial (f16, with a power-of-two exponent per head that keeps it in
- * range) and lse to ws, and the last split to arrive merges all of them (weights e^(lse_s - M) / Z) into out / lse.
- * ws: spmla_attn_ws_bytes(T, H, S) bytes, 256-byte aligned, zero-filled once when allocated (the kernel leaves its
- * arrival counters at zero after every launch, so one workspace serves launches that run one after another; launches
- * that may overlap need workspaces of their own). out 16-byte aligned rows give 16-byte stores. S > 8: SPMLA_ELIMIT.
+ * range) and lse to ws, and the last split to finish merges all of them (weights e^(lse_s - M) / Z) into out / lse.
+ * ws: spmla_attn_ws_bytes(T, H, S) bytes, 256-byte aligned. Its first C = 4 * T * ceil(H / 128) bytes (rounded up
+ * to a multiple of 256) are the launch's counters and must be zero when it starts; the kernel leaves them zero, and
+ * the bytes past them are scratch. So a workspace zero-filled once serves launches that run one after another,
+ * except that a launch with a larger C than the previous launch on the same workspace needs the bytes from the
+ * previous C to its own C zeroed first. Launches that may overlap need workspaces of their own. out 16-byte aligned
+ * rows give 16-byte stores. S > 8: SPMLA_ELIMIT.
  * Replaces the split-K decode launch with its partial combine (oa2_v2_launch dotsnote/engine/arcstats_pkg/arcstats/
  * csrc/offload_attn2.cu:2021-2104; _sparse_mla_offload_split_kernel + _combine_kernel sparse_offload.py:419-538). */
 int spmla_attn(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,

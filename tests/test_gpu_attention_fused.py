@@ -98,3 +98,26 @@ def test_row_scale_range(dev, case, split):
     _vs_oracle(o, l, o_ref, l_ref)
     if case == "tiny":      # outputs ~1e-3: also within 2^-8 of their own scale, not only the absolute bar
         assert np.abs(o - o_ref).max() <= 2.0 ** -8 * np.abs(o_ref).max()
+
+
+def test_workspace_reuse_larger_counter_region(dev):
+    """The cached workspace reused by a launch whose counters take more bytes than the previous launch's (bytes that
+    launch used as scratch): attend clears them first, and every token of the second launch is merged."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    R, H, K = 4096, 128, 256
+    pool = torch.from_numpy(make_pool_656(R, seed=51)[0]).to(dev)
+    sm = 192 ** -0.5
+    print("[fused] workspace reuse: T=100 split 8, then T=399 split 2", flush=True)
+    kernels.attend(make_q(100, H, seed=52).to(dev), pool, distinct_idx(100, K, R, seed=53).to(dev), sm, split=8)
+    T = 399
+    assert kernels.attn_ws_bytes(T, H, 2) <= kernels.attn_ws_bytes(100, H, 8)       # served by the same buffer
+    q, idx = make_q(T, H, seed=54).to(dev), distinct_idx(T, K, R, seed=55).to(dev)
+    out = torch.full((T, H, 512), float("nan"), dtype=torch.bfloat16, device=dev)
+    lse = torch.full((T, H), float("nan"), device=dev)
+    kernels.attend(q, pool, idx, sm, split=2, out=out, lse=lse)
+    o1, l1 = kernels.attend(q, pool, idx, sm, split=1)
+    torch.cuda.synchronize()
+    o, o1 = out.float(), o1.float()
+    bar = 2.0 ** -7 * o1.abs() + 2.0 ** -9 * o1.abs().amax(dim=-1, keepdim=True) + 1e-5
+    assert bool(torch.isfinite(o).all()) and float(((o - o1).abs() - bar).max()) <= 0
+    assert float((lse - l1).abs().max()) <= 1e-5
