@@ -9,27 +9,26 @@
 //
 // gfx950 mapping. One workgroup = (token t, group of up to 128 heads, split s of the token's rows), 4 waves, one per
 // SIMD; wave w owns heads 32 w .. 32 w + 31 of the group: their query in VGPRs and their 32 x 512 fp32 output
-// accumulator in AGPRs. All four waves walk the same 32-row tiles, so every e4m3 code is converted once per
-// workgroup and read by the four head blocks from LDS:
-//   * staging: wave w copies the codes of scale group w (32 rows x 128 B) into a private 3-deep LDS ring with
-//     direct global->LDS copies (global_load_lds_dwordx4), plus a quarter of the rows' bf16 rope and scale w of all
-//     32 rows; entries that are invalid or past the split's end copy a file-scope zero row, so they feed exact zeros
-//     into both products;
-//   * conversion: wave w converts its group exactly to f16 (v_cvt_scalef32_pk_f16_fp8; every e4m3 value is an f16)
-//     into the shared tile [32 rows][64 chunks of 16 B], chunk c of row r stored at (c & ~15) | ((c & 15) ^ g(r)),
-//     g(r) = 4 (r & 3) | ((r >> 2) & 3): the row-major QK operand reads (16 rows per LDS cycle) and the transposed PV
-//     operand reads (ds_read_b64_tr_b16, 4 rows x 64 B per 32 lanes) are then both free of bank conflicts. The
-//     conversion of tile j + 1 runs between the QK MFMAs of tile j; one workgroup barrier per tile;
-//   * QK: S^T (32 rows x 32 heads) with VGPR accumulators: the latent on f16 MFMA (32x32x16; the query converted to
-//     f16 once, exact in f16's normal range, as the reference's fp16 QK), one partial per 128-value scale group
-//     combined with the rows' fp32 scales (a DPP operand: see fmac4_dpp), so no product of a code and a scale is
-//     rounded; the rope on bf16 MFMA;
+// accumulator in AGPRs. All four waves walk the same 32-row tiles:
+//   * staging: wave w copies the codes of scale group w (32 rows x 128 B), a quarter of the rows' bf16 rope and scale
+//     w of all 32 rows into 3-deep LDS rings with direct global->LDS copies (global_load_lds_dwordx4), two tiles
+//     ahead; entries that are invalid or past the split's end copy a file-scope zero row, so they feed exact zeros
+//     into both products. A group's codes are stored chunk-major ([16-byte chunk][row]), row r at position
+//     r ^ (4 ((r >> 3) & 1)), so that the row reads below are free of bank conflicts;
+//   * QK: S^T (32 rows x 32 heads) with VGPR accumulators on f16 MFMA (32x32x16): each lane reads 16 codes of its row
+//     (one b128 read feeds two MFMAs) and converts them exactly to f16 in registers (v_cvt_scalef32_pk_f16_fp8; every
+//     e4m3 value is an f16); the query is converted to f16 once, exact in f16's normal range, as the reference's fp16
+//     QK. One partial per 128-value scale group is combined with the rows' fp32 scales (a DPP operand: see
+//     fmac4_dpp), so no product of a code and a scale is rounded; the rope on bf16 MFMA;
+//   * V: during the QK MFMAs of tile j, wave w transposes its group of tile j + 1 with the 8-bit transposing read
+//     (ds_read_b64_tr_b8: 8 rows of one dim per lane), converts it to f16 and writes the dim-major tile V^T [512 dims]
+//     [32 rows in the P' operand's row order] (double-buffered), which the PV MFMAs of tile j + 1 read with full-rate
+//     16-byte reads (a transposing read in the PV loop itself runs at a third of the rate). One barrier per tile;
 //   * softmax: the C layout puts one head in each lane (16 rows; the other 16 in lane + 32): in-lane plus one
 //     cross-half exchange, base 2, lazy rescaling (a head's reference max moves only when a tile exceeds it by more
 //     than TAU, so p <= 2^TAU and O is rescaled rarely);
-//   * PV: f16 MFMA, V^T read transposed from the shared f16 tile, P' = P * scale(row, group) rounded to f16 (11
-//     significant bits); a power-of-two factor 2^-eps carried by P, O and l keeps P' inside f16's range for any
-//     row scale (see the softmax).
+//   * PV: f16 MFMA, P' = P * scale(row, group) rounded to f16 (11 significant bits); a power-of-two factor 2^-eps
+//     carried by P, O and l keeps P' inside f16's range for any row scale (see the softmax).
 #include "spmla_common.h"
 
 namespace spmla {
@@ -43,26 +42,25 @@ constexpr int KMAX = 2048;            // rows per (token, split): their ids are 
 constexpr float TAU = 6.0f;
 
 // LDS map (bytes)
-constexpr int BF_TILE = TR * 1024;            // bf16 latent tile, swizzled chunks
+constexpr int STG_TILE = TR * 512;            // e4m3 codes of a tile: [group][16-byte chunk][row position]
+constexpr int VT_TILE = 512 * TR * 2;         // f16 V^T [dim][4 blocks of 8 rows], block b stored at b ^ ((dim >> 1) & 3)
 constexpr int RP_TILE = TR * 128;             // bf16 rope tile [32 rows][8 chunks], swizzled
 constexpr int SC_TILE = 4 * TR * 4;           // fp32 scales [group][32], row order zrow (see issue_tile)
-constexpr int STG_W = TR * 128;               // e4m3 staging of one wave's group: [part][half][row][16 B]
-constexpr int NBF = 2, NRP = 4, NSTG = 3;     // ring depths
-constexpr int L_BF = 0;
-constexpr int L_RP = L_BF + NBF * BF_TILE;    // 65536
-constexpr int L_SC = L_RP + NRP * RP_TILE;    // 81920
-constexpr int L_STG = L_SC + NRP * SC_TILE;   // 83968
-constexpr int L_QR = L_STG + NSTG * NW * STG_W;   // 133120: query rope, [wave][head][8 chunks] swizzled
-constexpr int L_IDS = L_QR + NW * HB * 128;   // 149504: validated row ids of the split (-1: none)
-constexpr int L_TOTAL = L_IDS + KMAX * 4;     // 157696
+constexpr int NRING = 3;                      // depth of the staging, rope and scale rings
+constexpr int L_STG = 0;
+constexpr int L_VT = L_STG + NRING * STG_TILE;    // 49152: two V^T tiles
+constexpr int L_RP = L_VT + 2 * VT_TILE;          // 114688
+constexpr int L_SC = L_RP + NRING * RP_TILE;      // 126976
+constexpr int L_QR = L_SC + NRING * SC_TILE;      // 128512: query rope, [wave][head][8 chunks] swizzled
+constexpr int L_IDS = L_QR + NW * HB * 128;       // 144896: validated row ids of the split (-1: none)
+constexpr int L_TOTAL = L_IDS + KMAX * 4;         // 153088
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget");
 
 // Source of invalid and padding rows: zero codes, zero scales, zero rope.
 __device__ __attribute__((aligned(16))) uint8_t zero_row[ROW656];
 
-// bf16 tile: byte offset of chunk c (8 values) of row r
-__device__ inline int gsw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-__device__ inline int bf_off(int r, int c) { return r * 1024 + 16 * ((c & ~15) | ((c & 15) ^ gsw(r))); }
+// position of row r in a staged chunk (an involution: bit 2 flipped with bit 3)
+__device__ inline int spos(int r) { return r ^ (4 * ((r >> 3) & 1)); }
 // rope tile and query rope: chunk c (8 values) of row r
 __device__ inline int rp_off(int r, int c) { return r * 128 + 16 * (c ^ ((r >> 1) & 7)); }
 
@@ -181,26 +179,26 @@ inline long long ws_cnt_bytes(int T, int HG) { return ws_align(4ll * T * HG); }
 inline long long ws_lse_bytes(int T, int HG, int S) { return ws_align(4ll * S * T * HG * HGW); }
 inline long long ws_o_bytes(int T, int HG, int S) { return 2ll * S * T * HG * HGW * D_LAT; }
 
-// Copies of tile jj for wave w: the codes of scale group w of the tile's 32 rows (4 x 16 B per lane; staging slot
-// [part i][half][row][16 B] holds e4m3 chunk 8 w + 2 i + half of the row), rows 8 w .. 8 w + 7 of the rope tile (lane
-// l fills stored chunk l % 8 of row 8 w + l / 8), and scale w of all 32 rows: lane l < 32 copies it for row
+// Copies of tile jj for wave w: the codes of scale group w of the tile's 32 rows (copy i fills chunks 2 i and 2 i + 1:
+// lane l copies chunk 2 i + l / 32 of row spos(l % 32) to position l % 32), rows 8 w .. 8 w + 7 of the rope tile (lane l
+// fills stored chunk l % 8 of row 8 w + l / 8), and scale w of all 32 rows: lane l < 32 copies it for row
 // zrow(l) = 8 (l % 4) + 4 (l / 16) + (l / 4) % 4 to float l of the group's 128 bytes (lanes 32 .. 63 are masked off),
 // so that lane 4 hh + b of a group's floats holds rows 8 a + 4 hh + b, a = 0 .. 3, in one 16-byte slot.
-// VM_TILE vector-memory instructions. x0 = id of row lane & 31, x1 = id of row 8 w + lane / 8, x2 = id of row
+// VM_TILE vector-memory instructions. x0 = id of row spos(lane & 31), x1 = id of row 8 w + lane / 8, x2 = id of row
 // zrow(lane & 31) (read a step ahead, so that issuing the copies waits for nothing).
 constexpr int VM_TILE = 6;
 __device__ inline int zrow(int l) { return 8 * (l & 3) + 4 * ((l >> 4) & 1) + ((l >> 2) & 3); }
 __device__ inline void issue_tile(const Params& p, SPMLA_LDS uint8_t* lds, int jj, int w, int lane, int x0, int x1,
                                   int x2) {
   const int hh = lane >> 5, rr = 8 * w + (lane >> 3);
-  const uint8_t* src = (x0 >= 0 ? p.pool + (long long)x0 * ROW656 : zero_row) + (8 * w + hh) * 16;
-  SPMLA_LDS uint8_t* stg = lds + L_STG + ((jj % NSTG) * NW + w) * STG_W;
+  const uint8_t* src = (x0 >= 0 ? p.pool + (long long)x0 * ROW656 : zero_row) + 128 * w + 16 * hh;
+  SPMLA_LDS uint8_t* stg = lds + L_STG + (jj % NRING) * STG_TILE + w * 4096;
 #pragma unroll
   for (int i = 0; i < 4; ++i) dma16(src + 32 * i, stg + i * 1024);
   const uint8_t* rsrc = x1 >= 0 ? p.pool + (long long)x1 * ROW656 : zero_row;
-  dma16(rsrc + ROPE_OFF + 16 * ((lane & 7) ^ ((rr >> 1) & 7)), lds + L_RP + (jj % NRP) * RP_TILE + w * 1024);
+  dma16(rsrc + ROPE_OFF + 16 * ((lane & 7) ^ ((rr >> 1) & 7)), lds + L_RP + (jj % NRING) * RP_TILE + w * 1024);
   const uint8_t* zsrc = x2 >= 0 ? p.pool + (long long)x2 * ROW656 : zero_row;
-  if (lane < 32) dma4(zsrc + SC_OFF + 4 * w, lds + L_SC + (jj % NRP) * SC_TILE + w * 128);
+  if (lane < 32) dma4(zsrc + SC_OFF + 4 * w, lds + L_SC + (jj % NRING) * SC_TILE + w * 128);
 }
 
 // Row scales as DPP operands. z[a] of lane l = scale g of row 8 a + 4 hh + l % 4 (one 16-byte read per group); value
@@ -235,21 +233,9 @@ __device__ inline void mul4_dpp_f16(u32x4& dst, float z, const float (&p)[16]) {
   dst[2 * (A & 1) + 1] = pk_f16(t2, t3);
 }
 
-// Staged part i of wave w's group of tile jj: 16 codes of row r = lane & 31, e4m3 chunk 8 w + 2 i + hh = bf16 chunks
-// c = 16 w + 4 i + 2 hh + b (b = 0, 1). Byte offset of chunk c in the swizzled tile: r * 1024 + 256 w +
-// ((64 i + 16 b) ^ key), key = 32 hh ^ 16 gsw(r) (one xor-add per write). The 16 lanes of one LDS cycle (rows r0 ..
-// r0 + 15, one chunk) land on 16 distinct 16-byte bank groups.
-__device__ inline u32x4 read_part(SPMLA_LDS uint8_t* lds, int jj, int w, int lane, int i) {
-  return *(SPMLA_LDS u32x4*)(lds + L_STG + ((jj % NSTG) * NW + w) * STG_W + i * 1024 + lane * 16);
-}
-__device__ inline void write_part(SPMLA_LDS uint8_t* lds, int jj, int w, const int (&wo)[2], int i, u32x4 v) {
-  u32x4 a, b;
-  a[0] = fp8lo_f16x2(v[0]); a[1] = fp8hi_f16x2(v[0]); a[2] = fp8lo_f16x2(v[1]); a[3] = fp8hi_f16x2(v[1]);
-  b[0] = fp8lo_f16x2(v[2]); b[1] = fp8hi_f16x2(v[2]); b[2] = fp8lo_f16x2(v[3]); b[3] = fp8hi_f16x2(v[3]);
-  // wo[0] = r * 1024 (row base), wo[1] = key
-  SPMLA_LDS uint8_t* bf = lds + L_BF + (jj & 1) * BF_TILE + 256 * w;
-  *(SPMLA_LDS u32x4*)(bf + wo[0] + ((64 * i) ^ wo[1])) = a;
-  *(SPMLA_LDS u32x4*)(bf + wo[0] + ((64 * i + 16) ^ wo[1])) = b;
+// 8 e4m3 codes (two dwords) -> 8 f16, exact
+__device__ inline f16x8 codes8_f16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(f16x8, u32x4{fp8lo_f16x2(a), fp8hi_f16x2(a), fp8lo_f16x2(b), fp8hi_f16x2(b)});
 }
 
 // bf16 output of a wave's 32 heads through LDS: the C-layout values of block mt (head l32, dims 32 mt + 8 a + 4 hh +
@@ -372,7 +358,8 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
   const int ntile = p.R > 0 ? (nrow + TR - 1) / TR : 0;     // no rows to read: o = 0, lse = -inf
 
   // ---- prologue: validated row ids -> LDS, query rope -> LDS, query latent -> VGPRs (B operands: lane holds head
-  // l32, dims 16 ks + 8 hh .. + 7 of MFMA ks)
+  // l32, dims 32 (ks / 2) + 16 hh + 8 (ks % 2) .. + 7 of MFMA ks: the two MFMAs of a pair take the 16 codes of one
+  // b128 read)
   const int* idxrow = p.idx + (long long)t * p.idx_st + kb;
   int xs[KMAX / 256];
 #pragma unroll
@@ -386,7 +373,7 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
   const uint32_t qmask = hval ? 0xffffffffu : 0u;          // heads past H: zero query
   u32x4 qraw[32];                                            // bf16, converted to f16 once the first copies are issued
 #pragma unroll
-  for (int ks = 0; ks < 32; ++ks) qraw[ks] = *(const u32x4*)(qrow + 16 * ks + 8 * hh) & qmask;
+  for (int ks = 0; ks < 32; ++ks) qraw[ks] = *(const u32x4*)(qrow + 32 * (ks >> 1) + 16 * hh + 8 * (ks & 1)) & qmask;
   u32x4 qrv[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {                              // rope: 32 heads x 8 chunks, 4 per lane
@@ -404,22 +391,17 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
   }
   lds_barrier();
 
-  int wo[2];                                                // conversion write row base and key (see write_part)
-  {
-    const int r = lane & 31;
-    wo[0] = r * 1024;
-    wo[1] = 32 * hh ^ 16 * gsw(r);
-  }
-  // ---- copies of tiles 0, 1, 2; tile 0 converted
+  // ---- copies of tiles 0 and 1
+  const int r_dma0 = spos(lane & 31);                        // the row whose codes this lane copies
   const int r_dma1 = 8 * w + (lane >> 3);                    // the rope row this lane copies
   const int r_dma2 = zrow(lane & 31);                        // the row whose scale this lane copies
 #pragma unroll
-  for (int jj = 0; jj < 3; ++jj)
+  for (int jj = 0; jj < 2; ++jj)
     if (jj < ntile)
-      issue_tile(p, lds, jj, w, lane, ids[jj * TR + (lane & 31)], ids[jj * TR + r_dma1], ids[jj * TR + r_dma2]);
-  // row ids of tile 3 (the first copies the loop issues)
-  int nx0 = 3 < ntile ? ids[3 * TR + (lane & 31)] : -1, nx1 = 3 < ntile ? ids[3 * TR + r_dma1] : -1;
-  int nx2 = 3 < ntile ? ids[3 * TR + r_dma2] : -1;
+      issue_tile(p, lds, jj, w, lane, ids[jj * TR + r_dma0], ids[jj * TR + r_dma1], ids[jj * TR + r_dma2]);
+  // row ids of tile 2 (the first copies the loop issues)
+  int nx0 = 2 < ntile ? ids[2 * TR + r_dma0] : -1, nx1 = 2 < ntile ? ids[2 * TR + r_dma1] : -1;
+  int nx2 = 2 < ntile ? ids[2 * TR + r_dma2] : -1;
 
   // ---- query scaled per head by 2^kq, a power of two that puts its largest latent magnitude in [2^14, 2^15): the
   // latent then converts to f16 exactly wherever it matters (values below 2^-29 of the head's largest are the only
@@ -457,14 +439,37 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
       *(SPMLA_LDS u32x4*)(qr + rp_off(cc >> 3, cc & 7)) = r;
     }
   }
-  if (ntile > 0) {
-    if (ntile >= 3) wait_vm<2 * VM_TILE>();
-    else if (ntile == 2) wait_vm<VM_TILE>();
-    else wait_vm<0>();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) write_part(lds, 0, w, wo, i, read_part(lds, 0, w, lane, i));
+  // QK operand of MFMA pair pp (MFMAs 2 pp, 2 pp + 1): row l32's codes of chunk 2 (pp % 4) + hh of group pp / 4 at
+  // pp / 4 * 4096 + chunk * 512 + spos(l32) * 16 (eight rows per LDS cycle on eight bank groups)
+  const int k_off = spos(l32) * 16 + hh * 512;
+  // V^T conversion (wave w, chunk q = 0 .. 7 of its group): in 16-lane group G of the transposing read, source lane
+  // 2 k + d reads codes 8 d .. 8 d + 7 of chunk q of row rho(G, k) = 16 (G / 2) + 8 (k / 4) + 4 (G % 2) + k % 4; lane
+  // L then holds dim 16 q + L % 16 of the group for rows rho(G, 0 .. 7), which is block G of V^T (the row order of
+  // the P' operand: k-slot e of lane half hh = row 16 ks + 8 (e / 4) + 4 hh + e % 4 for block 2 ks + hh)
+  int t_off, v_dst;
+  {
+    const int G = lane >> 4, sl = lane & 15, k = sl >> 1, d = sl & 1;
+    const int rho = 16 * (G >> 1) + 8 * (k >> 2) + 4 * (G & 1) + (k & 3);
+    t_off = w * 4096 + spos(rho) * 16 + 8 * d;                       // + q * 512
+    v_dst = (128 * w + sl) * 64 + 16 * (G ^ ((sl >> 1) & 3));        // + q * 1024 (dim 128 w + 16 q + sl)
   }
-  lds_barrier();
+  // PV operand of block mt = 4 g + m4, k half ks: dim 32 mt + l32, block 2 ks + hh of V^T
+  const int pv_off0 = l32 * 64 + 16 * (hh ^ ((l32 >> 1) & 3));         // + mt * 2048
+  const int pv_off1 = l32 * 64 + 16 * ((2 + hh) ^ ((l32 >> 1) & 3));
+
+  // V^T of tile 0 (this wave's group, once its copies have landed; tile 1's may stay in flight)
+  if (ntile >= 2) wait_vm<VM_TILE>();
+  else wait_vm<0>();
+  if (ntile > 0) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const i32x2 tv = __builtin_amdgcn_ds_read_tr8_b64_v2i32((SPMLA_LDS i32x2*)(lds + L_STG + t_off + q * 512));
+      *(SPMLA_LDS u32x4*)(lds + L_VT + v_dst + q * 1024) =
+          u32x4{fp8lo_f16x2(tv[0]), fp8hi_f16x2(tv[0]), fp8lo_f16x2(tv[1]), fp8hi_f16x2(tv[1])};
+    }
+  }
+  lds_barrier();                            // tile 0 landed for every wave, its V^T written, the query rope written
+
 
   const float ch = __builtin_ldexpf(p.c, -kq);   // sm_scale * kv_scale * log2(e) / 2^kq
   float m_run = -__builtin_inff();     // reference max of this lane's head (log2 units)
@@ -477,141 +482,139 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
 #pragma unroll
   for (int b = 0; b < 16; ++b) O[b] = f32x16{};
 
-  // QK operand of MFMA u = 8 g + kk: row l32, chunk 2 u + hh at l32 * 1024 + 256 g + ((32 kk) ^ qk_key) (one xor-add
-  // per read; 32 kk and 16 hh occupy disjoint bits, so 16 ((2 kk + hh) ^ gsw) = (32 kk) ^ (16 hh ^ 16 gsw))
-  const int qk_base = l32 * 1024, qk_key = 16 * (hh ^ gsw(l32));
-  // PV transposed reads (ds_read_b64_tr_b16): in each 16-lane group G the source lane 4k + q reads 4 values of
-  // row 16 ks + 8 r + 4 (G >> 1) + k, dims 32 mt + 16 (G & 1) + 4 q .. + 3; result lane i of the group receives
-  // value k from source lane 4k + i / 4, so lane L ends with V^T[32 mt + L % 32][8 (L / 32) + 4 r + k], the K order of
-  // the P' operand (row 16 ks + 8 (e / 4) + 4 (L / 32) + e % 4 for e = 4 r + k).
-  // (offset of read r of block m4 = pv_base[r] + ((64 m4) ^ pv_key): 64 (m4 ^ k) = (64 m4) ^ (64 k))
-  int pv_base[2], pv_key;
-  {
-    const int G = lane >> 4, k = (lane & 15) >> 2, q = lane & 3;
-    const int rl = 4 * (G >> 1) + k, cl = 2 * (G & 1) + (q >> 1);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) pv_base[r] = (8 * r + rl) * 1024 + 16 * (cl ^ ((2 * r + (G >> 1)) & 3)) + 8 * (lane & 1);
-    pv_key = 64 * k;
-  }
-
 #pragma unroll 1
   for (int j = 0; j < ntile; ++j) {
-    const bool nxt = j + 1 < ntile;        // tile j + 1 is converted during this step
-    if (nxt) {                             // its copies have landed (the copies of tile j + 2 may stay in flight)
-      if (j + 2 < ntile) wait_vm<VM_TILE>();
-      else wait_vm<0>();
-    }
-    SPMLA_LDS uint8_t* bf = lds + L_BF + (j & 1) * BF_TILE;
-    SPMLA_LDS uint8_t* rp = lds + L_RP + (j % NRP) * RP_TILE;
-    SPMLA_LDS uint8_t* scb = lds + L_SC + (j % NRP) * SC_TILE;
+    // tile j's codes, rope and scales have landed for every wave and its V^T is written (barrier at the end of the
+    // previous step); the copies of tile j + 2 go out during the rope MFMAs (into tile j - 1's slots)
+    SPMLA_LDS uint8_t* stg = lds + L_STG + (j % NRING) * STG_TILE;
+    SPMLA_LDS uint8_t* rp = lds + L_RP + (j % NRING) * RP_TILE;
+    SPMLA_LDS uint8_t* scb = lds + L_SC + (j % NRING) * SC_TILE;
+    SPMLA_LDS uint8_t* vt = lds + L_VT + (j & 1) * VT_TILE;                  // V^T of tile j (PV)
+    SPMLA_LDS uint8_t* vtn = lds + L_VT + ((j + 1) & 1) * VT_TILE;           // V^T of tile j + 1 (written here)
+    SPMLA_LDS uint8_t* stn = lds + L_STG + ((j + 1) % NRING) * STG_TILE;     // codes of tile j + 1
 
-    // ---- S^T of tile j: the rope chain (4 MFMAs) into S, then latent group g (8 MFMAs) into acc[g & 1], its fp32
-    // scales combined into S during group g + 1 (group 3's after the last MFMA). With one wave per SIMD only a few
-    // VALU instructions hide behind each MFMA, so all side work is cut into slices of that size, one slice per MFMA
-    // (a scheduling fence after every MFMA keeps the slices where they are): the K reads (D MFMAs ahead), the
-    // conversion of tile j + 1 (part g: staged read in group g - 1, 4 + 4 conversions and two writes in group g), the
-    // combine of the previous group, and the copies of tile j + 3. Waves without heads compute on a zero query.
-    constexpr int D = 2;
-    auto kread = [&](int u) -> f16x8 {
-      return __builtin_bit_cast(f16x8, *(SPMLA_LDS u32x4*)(bf + 256 * (u >> 3) + qk_base + ((32 * (u & 7)) ^ qk_key)));
+    // ---- S^T of tile j: the rope chain (4 MFMAs) into S, then the latent MFMAs of groups 0 and 1 alternating (into
+    // acc[0], acc[1]), then those of groups 2 and 3 (again acc[0], acc[1]): an MFMA that takes the previous one's
+    // result waits for its write-back once VALU work sits between them, so consecutive MFMAs use different
+    // accumulators. Each pair of groups is combined with its fp32 scales into S after its last MFMA (the accumulators
+    // hold the next pair's partials from then on). With one wave per SIMD only a few VALU instructions hide behind each MFMA, so all side work is cut into
+    // slices of that size, one slice per MFMA (a scheduling fence after every MFMA keeps the slices where they are):
+    // the copies of tile j + 2, the code reads (4 MFMAs ahead) and their conversion (one MFMA ahead).
+    // Waves without heads compute on a zero query.
+    // Latent MFMA s (0 .. 31): group g = 2 (s / 16) + s % 2, k = (s / 2) % 8 (dims 128 g + 16 k .. of the group), the
+    // k / 2-th code read of the group (read r = 8 (s / 16) + 2 (k / 2) + s % 2, half k % 2 of its 16 codes).
+    auto kread = [&](int r) -> u32x4 {     // read r: group 2 (r / 8) + r % 2, chunk pair (r / 2) % 4
+      const int g = 2 * (r >> 3) + (r & 1), pp = (r >> 1) & 3;
+      return *(SPMLA_LDS u32x4*)(stg + g * 4096 + (2 * pp) * 512 + k_off);
     };
     auto rread = [&](int ks, bf16x8& ra, bf16x8& rb) {
       ra = __builtin_bit_cast(bf16x8, *(SPMLA_LDS u32x4*)(rp + rp_off(l32, 2 * ks + hh)));
       rb = __builtin_bit_cast(bf16x8, *(SPMLA_LDS u32x4*)(qr + rp_off(l32, 2 * ks + hh)));
     };
-    SPMLA_LDS uint8_t* cbf = lds + L_BF + ((j + 1) & 1) * BF_TILE + 256 * w;   // conversion target (tile j + 1)
-    // (past the last tile the staged bytes are stale and are converted into the unused buffer)
-    u32x4 cv = read_part(lds, j + 1, w, lane, 0);
     bf16x8 ra[4], rb[4];
     rread(0, ra[0], rb[0]);
     // row scales of group g of tile j as DPP operands (see fmac4_dpp)
     auto zload = [&](int g) -> f32x4 { return *(SPMLA_LDS f32x4*)(scb + g * 128 + (4 * hh + (lane & 3)) * 16); };
-    f32x4 zq, zq3;
+    f32x4 zqa, zqb;
     float smx = 0.f;                       // largest row scale of the tile seen by this lane
-    f16x8 kr[4];
+    u32x4 kc[4];                           // code reads in flight (read r in kc[r % 4])
+    f16x8 ka[2];                           // converted operands (MFMA parity)
     f32x16 S, acc[2];
-    u32x4 cva;                             // converted half of the current part
+    int idv = 0;                           // id of row l32 (the tile's valid-row mask)
+    f32x4 z0;                              // scales of group 0 (the first P')
 #pragma unroll
     for (int t = 0; t < 36; ++t) {
       if (t < 4) {                          // ---- rope chain
         if (t + 1 < 4) rread(t + 1, ra[t + 1], rb[t + 1]);
-        if (t + D - 4 >= 0) kr[(t + D - 4) & 3] = kread(t + D - 4);
-        if (t == 0) kr[0] = kread(0);
-        S = t == 0 ? qk_first(ra[0], rb[0]) : qk_next(ra[t], rb[t], S);
-      } else {                              // ---- latent MFMA u = 8 g + kk
-        const int u = t - 4, g = u >> 3, kk = u & 7;
-        if (u + D < 32) kr[(u + D) & 3] = kread(u + D);
-        // conversion of part g of tile j + 1
-        if (kk == 1) {
-          cva[0] = fp8lo_f16x2(cv[0]); cva[1] = fp8hi_f16x2(cv[0]); cva[2] = fp8lo_f16x2(cv[1]); cva[3] = fp8hi_f16x2(cv[1]);
-        }
-        if (kk == 2) {
-          *(SPMLA_LDS u32x4*)(cbf + wo[0] + ((64 * g) ^ wo[1])) = cva;
-          cva[0] = fp8lo_f16x2(cv[2]); cva[1] = fp8hi_f16x2(cv[2]); cva[2] = fp8lo_f16x2(cv[3]); cva[3] = fp8hi_f16x2(cv[3]);
-        }
-        if (kk == 3) *(SPMLA_LDS u32x4*)(cbf + wo[0] + ((64 * g + 16) ^ wo[1])) = cva;
-        if (kk == 6 && g < 3) cv = read_part(lds, j + 1, w, lane, g + 1);
-        // combine of group g - 1: quarter qd = kk - 4 at kk 4 .. 7 (at least 4 MFMAs after the group's last one, so
-        // the XDL-write -> VALU-read distance holds)
-        if (g >= 1 && kk == 0) zq = zload(g - 1);
-        if (g >= 1 && kk == 1) smx = fmaxf(fmaxf(smx, fmaxf(zq[0], zq[1])), fmaxf(zq[2], zq[3]));
-        if (g >= 1 && kk >= 4) {
-          const f32x16& ap = acc[(g - 1) & 1];
-          if (kk == 4) fmac4_dpp<0>(S, zq[0], ap);
-          if (kk == 5) fmac4_dpp<1>(S, zq[1], ap);
-          if (kk == 6) fmac4_dpp<2>(S, zq[2], ap);
-          if (kk == 7) fmac4_dpp<3>(S, zq[3], ap);
-        }
-        if (g == 3 && kk == 7) zq3 = zload(3);
-        // copies of tile j + 3 (row ids read one step ahead)
-        if (kk == 7 && g == 0 && j + 3 < ntile) {
+        if (t < 2) kc[t] = kread(t);
+        if (t < 3 && j + 2 < ntile) {        // copies of tile j + 2: codes 0-1, codes 2-3, rope and scales
           // source offsets recomputed here from an opaque lane id (hoisted out of the loop they would be spilled)
           int ln = lane;
           asm volatile("" : "+v"(ln));
-          const int doff = (8 * w + (ln >> 5)) * 16;
-          const uint8_t* dsrc = (nx0 >= 0 ? p.pool + (long long)nx0 * ROW656 : zero_row) + doff;
-          SPMLA_LDS uint8_t* stg = lds + L_STG + (((j + 3) % NSTG) * NW + w) * STG_W;
-          dma16(dsrc, stg);
-          dma16(dsrc + 32, stg + 1024);
+          if (t < 2) {
+            const uint8_t* dsrc = (nx0 >= 0 ? p.pool + (long long)nx0 * ROW656 : zero_row) + 128 * w + 16 * (ln >> 5);
+            SPMLA_LDS uint8_t* dst = lds + L_STG + ((j + 2) % NRING) * STG_TILE + w * 4096 + t * 2048;
+            dma16(dsrc + 64 * t, dst);
+            dma16(dsrc + 64 * t + 32, dst + 1024);
+          } else {
+            const uint8_t* rsrc = nx1 >= 0 ? p.pool + (long long)nx1 * ROW656 : zero_row;
+            const int roff = ROPE_OFF + 16 * ((ln & 7) ^ (((8 * w + (ln >> 3)) >> 1) & 7));
+            dma16(rsrc + roff, lds + L_RP + ((j + 2) % NRING) * RP_TILE + w * 1024);
+            const uint8_t* zsrc = nx2 >= 0 ? p.pool + (long long)nx2 * ROW656 : zero_row;
+            if (ln < 32) dma4(zsrc + SC_OFF + 4 * w, lds + L_SC + ((j + 2) % NRING) * SC_TILE + w * 128);
+          }
         }
-        if (kk == 7 && g == 1 && j + 3 < ntile) {
-          int ln = lane;
-          asm volatile("" : "+v"(ln));
-          const int doff = (8 * w + (ln >> 5)) * 16;
-          const uint8_t* dsrc = (nx0 >= 0 ? p.pool + (long long)nx0 * ROW656 : zero_row) + doff;
-          const uint8_t* rsrc = nx1 >= 0 ? p.pool + (long long)nx1 * ROW656 : zero_row;
-          SPMLA_LDS uint8_t* stg = lds + L_STG + (((j + 3) % NSTG) * NW + w) * STG_W;
-          dma16(dsrc + 64, stg + 2048);
-          dma16(dsrc + 96, stg + 3072);
-          const int roff = ROPE_OFF + 16 * ((ln & 7) ^ (((8 * w + (ln >> 3)) >> 1) & 7));
-          dma16(rsrc + roff, lds + L_RP + ((j + 3) % NRP) * RP_TILE + w * 1024);
-          const uint8_t* zsrc = nx2 >= 0 ? p.pool + (long long)nx2 * ROW656 : zero_row;
-          if (lane < 32) dma4(zsrc + SC_OFF + 4 * w, lds + L_SC + ((j + 3) % NRP) * SC_TILE + w * 128);
+        if (t == 1) idv = ids[j * TR + l32];
+        if (t == 3) {
+          ka[0] = codes8_f16(kc[0][0], kc[0][1]);
+          if (j + 2 < ntile) wait_vm<VM_TILE>();   // this wave's copies of tile j + 1 landed (tile j + 2's may not)
+          else wait_vm<0>();
         }
-        if (kk == 7 && g == 2) {
-          nx0 = j + 4 < ntile ? ids[(j + 4) * TR + (lane & 31)] : -1;   // ids of tile j + 4, used next step
-          nx1 = j + 4 < ntile ? ids[(j + 4) * TR + r_dma1] : -1;
-          nx2 = j + 4 < ntile ? ids[(j + 4) * TR + r_dma2] : -1;
+        S = t == 0 ? qk_first(ra[0], rb[0]) : qk_next(ra[t], rb[t], S);
+      } else {                              // ---- latent MFMA s
+        const int sl = t - 4, half = sl >> 4, g = 2 * half + (sl & 1), k = (sl >> 1) & 7;
+        // the read first used 4 MFMAs from now (reads 2 .. 15; 0 and 1 went out during the rope chain)
+        if ((sl & 2) == 0) {
+          const int s4 = sl + 4;
+          if (s4 < 32 && ((s4 >> 1) & 1) == 0) {
+            const int r = 8 * (s4 >> 4) + 2 * ((s4 >> 2) & 3) + (s4 & 1);
+            kc[r & 3] = kread(r);
+          }
         }
-        const f16x8 ka = kr[u & 3];
-        if (kk == 0) acc[g & 1] = qkh_first(ka, qf[u]);
-        else if (u == 31) acc[1] = qkh_last(ka, qf[u], acc[1]);
-        else acc[g & 1] = qkh_next(ka, qf[u], acc[g & 1]);
+        if (sl == 12) zqa = zload(0);
+        if (sl == 13) zqb = zload(1);
+        if (sl == 16) {                     // groups 0 and 1 complete (qkh_last at MFMA 15): combine them into S
+          smx = fmaxf(fmaxf(fmaxf(zqa[0], zqa[1]), fmaxf(zqa[2], zqa[3])),
+                      fmaxf(fmaxf(zqb[0], zqb[1]), fmaxf(zqb[2], zqb[3])));
+          fmac4_dpp<0>(S, zqa[0], acc[0]);
+          fmac4_dpp<1>(S, zqa[1], acc[0]);
+          fmac4_dpp<2>(S, zqa[2], acc[0]);
+          fmac4_dpp<3>(S, zqa[3], acc[0]);
+          fmac4_dpp<0>(S, zqb[0], acc[1]);
+          fmac4_dpp<1>(S, zqb[1], acc[1]);
+          fmac4_dpp<2>(S, zqb[2], acc[1]);
+          fmac4_dpp<3>(S, zqb[3], acc[1]);
+        }
+        if (sl == 26) zqa = zload(2);
+        if (sl == 27) zqb = zload(3);
+        if (sl == 28) z0 = zload(0);
+        if (sl == 29) {
+          nx0 = j + 3 < ntile ? ids[(j + 3) * TR + r_dma0] : -1;   // ids of tile j + 3, used next step
+          nx1 = j + 3 < ntile ? ids[(j + 3) * TR + r_dma1] : -1;
+          nx2 = j + 3 < ntile ? ids[(j + 3) * TR + r_dma2] : -1;
+        }
+        const f16x8 kcur = ka[sl & 1];
+        // the operand of MFMA s + 1
+        if (sl + 1 < 32) {
+          const int s1 = sl + 1, k1 = (s1 >> 1) & 7;
+          const int r1 = 8 * (s1 >> 4) + 2 * (k1 >> 1) + (s1 & 1);
+          const u32x4& c = kc[r1 & 3];
+          ka[s1 & 1] = (k1 & 1) ? codes8_f16(c[2], c[3]) : codes8_f16(c[0], c[1]);
+        }
+        const f16x8 qop = qf[8 * g + k];
+        if (k == 0) acc[g & 1] = qkh_first(kcur, qop);
+        else if (sl == 15 || sl == 31) acc[g & 1] = qkh_last(kcur, qop, acc[g & 1]);
+        else acc[g & 1] = qkh_next(kcur, qop, acc[g & 1]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    {                                        // combine of group 3 (after qkh_last's wait states)
-      smx = fmaxf(fmaxf(smx, fmaxf(zq3[0], zq3[1])), fmaxf(zq3[2], zq3[3]));
-      fmac4_dpp<0>(S, zq3[0], acc[1]);
-      fmac4_dpp<1>(S, zq3[1], acc[1]);
-      fmac4_dpp<2>(S, zq3[2], acc[1]);
-      fmac4_dpp<3>(S, zq3[3], acc[1]);
+    {                                        // combine of groups 2 and 3 (after qkh_last's wait states)
+      smx = fmaxf(smx, fmaxf(fmaxf(fmaxf(zqa[0], zqa[1]), fmaxf(zqa[2], zqa[3])),
+                             fmaxf(fmaxf(zqb[0], zqb[1]), fmaxf(zqb[2], zqb[3]))));
+      fmac4_dpp<0>(S, zqa[0], acc[0]);
+      fmac4_dpp<1>(S, zqa[1], acc[0]);
+      fmac4_dpp<2>(S, zqa[2], acc[0]);
+      fmac4_dpp<3>(S, zqa[3], acc[0]);
+      fmac4_dpp<0>(S, zqb[0], acc[1]);
+      fmac4_dpp<1>(S, zqb[1], acc[1]);
+      fmac4_dpp<2>(S, zqb[2], acc[1]);
+      fmac4_dpp<3>(S, zqb[3], acc[1]);
     }
     __builtin_amdgcn_sched_barrier(0);
 
     {
       // ---- rows that do not exist: -inf (C-layout row of value i: 8 (i / 4) + 4 hh + i % 4)
-      const unsigned vmask = (unsigned)__ballot(ids[j * TR + l32] >= 0);
+      const unsigned vmask = (unsigned)__ballot(idv >= 0);
       if (__builtin_expect(vmask != 0xffffffffu, 0)) {     // rare: keep it a branch, not 16 selects per tile
         asm volatile("" ::: "memory");
         const unsigned lm = vmask >> (4 * hh);
@@ -664,35 +667,36 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
       l_run += ((s8[0] + s8[4]) + (s8[1] + s8[5])) + ((s8[2] + s8[6]) + (s8[3] + s8[7]));
       started = true;
 
-      // ---- PV: output dims of group g (MFMA blocks mt = 4g .. 4g + 3) use P' = P * scale(row, g) in f16. The
-      // transposed V^T reads run VD MFMAs ahead; group g + 1's P' is formed during group g, one quarter of its rows
-      // per MFMA (4 products, 2 packs), from scales read one MFMA earlier.
-      typedef short i16x8 __attribute__((ext_vector_type(8)));
-      constexpr int VD = 2;
-      auto vread = [&](int v) -> f16x8 {          // MFMA v = (group g, block m4, k half ks): v = 8 g + 2 m4 + ks
-        SPMLA_LDS uint8_t* base = bf + 16384 * (v & 1) + 256 * (v >> 3);
-        const int m4 = (v >> 1) & 3;
-        const int mo = (64 * m4) ^ pv_key;
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPMLA_LDS i16x4*)(base + pv_base[0] + mo));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPMLA_LDS i16x4*)(base + pv_base[1] + mo));
-        return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      // ---- PV: output dims of group g (MFMA blocks mt = 4g .. 4g + 3) use P' = P * scale(row, g) in f16. The V^T
+      // reads run VD MFMAs ahead; group g + 1's P' is formed during group g, one quarter of its rows per MFMA (4
+      // products, 2 packs), from scales read one MFMA earlier. Between them, the V^T conversion of this wave's group
+      // of tile j + 1 (chunk q in MFMAs 4 q .. 4 q + 3; past the last tile it converts stale bytes into the unused
+      // buffer).
+      auto tread = [&](int q) -> i32x2 {
+        return __builtin_amdgcn_ds_read_tr8_b64_v2i32((SPMLA_LDS i32x2*)(stn + t_off + q * 512));
       };
-      f16x8 vr[4];
-#pragma unroll
-      for (int v = 0; v < VD; ++v) vr[v] = vread(v);
-      u32x4 pbw[2], pbn[2];                  // P' of the current / next group, as packed bf16 pairs
+      i32x2 tv;                            // transposed codes of the current V^T chunk
+      u32x4 tw;                            // ... converted
+      constexpr int VD = 2;
+      auto vread = [&](int v) -> f16x8 {          // MFMA v = (group g, k half ks, block m4): v = 8 g + 4 ks + m4
+        const int mt = 4 * (v >> 3) + (v & 3);
+        return __builtin_bit_cast(f16x8, *(SPMLA_LDS u32x4*)(vt + mt * 2048 + (((v >> 2) & 1) ? pv_off1 : pv_off0)));
+      };
+      u32x4 pbw[2], pbn[2];                  // P' of the current / next group, as packed f16 pairs
       {
-        const f32x4 z0 = zload(0);
         mul4_dpp_f16<0>(pbw[0], z0[0], P);
         mul4_dpp_f16<1>(pbw[0], z0[1], P);
         mul4_dpp_f16<2>(pbw[1], z0[2], P);
         mul4_dpp_f16<3>(pbw[1], z0[3], P);
       }
       f32x4 zp = zload(1);                   // scales of the P' formed during the group (group g + 1)
+      f16x8 vr[4];
+#pragma unroll
+      for (int v = 0; v < VD; ++v) vr[v] = vread(v);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int v = 0; v < 32; ++v) {
-        const int g = v >> 3, v8 = v & 7, mt = 4 * g + (v8 >> 1);
+        const int g = v >> 3, v8 = v & 7, mt = 4 * g + (v & 3);      // consecutive MFMAs: different blocks
         if (v + VD < 32) vr[(v + VD) & 3] = vread(v + VD);
         if (g < 3) {                             // quarter v8 - 1 of group g + 1 at v8 = 1 .. 4
           if (v8 == 1) mul4_dpp_f16<0>(pbn[0], zp[0], P);
@@ -701,12 +705,15 @@ __global__ void __launch_bounds__(256, 1) fwd_kernel(Params p) {
           if (v8 == 4) mul4_dpp_f16<3>(pbn[1], zp[3], P);
         }
         if (g < 2 && v8 == 6) zp = zload(g + 2);
-        O[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[v & 3], __builtin_bit_cast(f16x8, pbw[v8 & 1]), O[mt], 0, 0, 0);
+        if ((v & 3) == 0) tv = tread(v >> 2);
+        if ((v & 3) == 2) tw = u32x4{fp8lo_f16x2(tv[0]), fp8hi_f16x2(tv[0]), fp8lo_f16x2(tv[1]), fp8hi_f16x2(tv[1])};
+        if ((v & 3) == 3) *(SPMLA_LDS u32x4*)(vtn + v_dst + (v >> 2) * 1024) = tw;
+        O[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[v & 3], __builtin_bit_cast(f16x8, pbw[v8 >> 2]), O[mt], 0, 0, 0);
         if (v8 == 7 && g < 3) { pbw[0] = pbn[0]; pbw[1] = pbn[1]; }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    lds_barrier();                          // tile j + 1 converted; tile j's buffers free
+    lds_barrier();                          // tile j + 1's V^T written by every wave; tile j's slots free
   }
 
   // ---- epilogue: this wave's 32 heads are complete (no other wave holds them). C layout of O[mt]: lane holds head
