@@ -1,8 +1,12 @@
-// Request-packed MTP decode attention (spmla_attn_packed) over the union rows of spmla_mtp_union: one workgroup of
-// 4 waves per (request, column group of 32 = tokens x heads, split); each wave streams its own 32-row tiles of the
-// union (codes into a private LDS double buffer by direct global->LDS copies, rope straight into VGPRs) and keeps its
-// own online softmax; a column's softmax keeps only the rows its token selected (per-row token masks, ballots).
-// Reference: dotsnote/engine/arcstats_pkg/arcstats/csrc/offload_attn.cu:700-1153 (pk_attn_kernel).
+// Head-group attention: one workgroup of 4 waves per (work item, column group of 32, split); each wave streams its
+// own 32-row tiles (codes into a private LDS double buffer by direct global->LDS copies, rope straight into VGPRs)
+// and keeps its own online softmax, so the waves never wait for each other inside the loop. Two instances:
+//   * attn_kernel<false>, the decode kernel of spmla_attn / spmla_attn_splitk / spmla_attn_merge when a launch has
+//     few tokens (spmla_attn.hip chooses): work item = token, columns = 32 of its heads;
+//   * attn_kernel<true>, request-packed MTP decode (spmla_attn_packed) over the union rows of spmla_mtp_union: work
+//     item = request, columns = tokens x heads; a column's softmax keeps only the rows its token selected (per-row
+//     token masks, ballots). Reference: dotsnote/engine/arcstats_pkg/arcstats/csrc/offload_attn.cu:700-1153
+//     (pk_attn_kernel).
 //
 // Math (reference: dotsnote/kaggle/runtime_dataset/bench_offload_attn2.py:77-93 and
 // dotsnote/engine/vllm_patch/vllm/v1/attention/ops/xpu_mla_sparse.py:77-161):
@@ -10,10 +14,10 @@
 //   p = exp2(s * log2e - m), o = kv_scale * sum p latent / sum p, lse = ln sum exp(s).
 //
 // gfx950 mapping (per wave): S^T (32 rows x 32 columns) on bf16 MFMA (32x32x16) with the codes converted exactly to
-// bf16 and one fp32 scale combine per 128-value group; PV on f16 MFMA with P' = P * scale in fp16 (p <= 2^TAU keeps
-// P' finite for scales up to 65504 / 2^TAU) and the codes read transposed with ds_read_b64_tr_b8; lazy rescaling
-// (a column's reference max moves only when a tile exceeds it by more than TAU); the 4 waves' (m, l, O) merge
-// through LDS at the end.
+// bf16 and one fp32 scale combine per 128-value group; PV on f16 MFMA with P' = P * scale in fp16 and the codes read
+// transposed with ds_read_b64_tr_b8; lazy rescaling (a column's reference max moves only when a tile exceeds it by
+// more than TAU, so p <= 2^TAU); a power-of-two factor 2^-eps carried by P, O and l keeps P' inside f16's range for
+// any row scale; the 4 waves' (m, l, O) merge through LDS at the end.
 #include "spmla_common.h"
 #include <stdlib.h>
 
@@ -23,7 +27,6 @@ namespace pk {
 constexpr int HG = 32;                // heads per workgroup
 constexpr int NW = 4;                 // waves per workgroup
 constexpr int TR = 32;                // rows per tile
-constexpr int KMAX = 2048;            // selected rows per (token, split) staged in LDS
 constexpr float TAU = 6.0f;
 
 // tile layout (bytes): 32 code chunks [c][r][16] (chunk-major: each MFMA operand read is one conflict-free
@@ -128,23 +131,8 @@ struct Params {
   const uint8_t* mk; const int* cu; int ql, tsh, NR;
 };
 
-// Copy one tile (32 rows: codes + scales) into the wave's buffer and load the rows' rope into VGPRs.
-// rid: the tile's 32 row ids (-1 = none: such a row copies row 0, which exists whenever a tile is read, and is
-// masked out of the softmax). 18 vector-memory instructions of the copy + 4 rope loads.
-constexpr int VM_PER_TILE = 22;
-__device__ inline void issue_tile(const uint8_t* __restrict__ pool, const SPMLA_LDS int* rid,
-                                  SPMLA_LDS uint8_t* tb, int lane, u32x4 (&rp)[4]) {
-  const int x = rid[lane & 31];
-  const uint8_t* src = pool + (long long)(x >= 0 ? x : 0) * ROW656;
-  const int h = lane >> 5;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) dma16(src + (2 * i + h) * 16, tb + i * 1024);
-  // scales: copy e, lane l -> group 2e + h of row l % 32 at float (2e + h) * 32 + l % 32
-  dma4(src + SC_OFF + h * 4, tb + T_SCT);
-  dma4(src + SC_OFF + (2 + h) * 4, tb + T_SCT + 256);
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(src + ROPE_OFF + ks * 32 + h * 16);
-}
+// Source of invalid and padding rows: zero codes, zero scales, zero rope (their P is 0, and 0 * 0 stays 0 in PV).
+__device__ __attribute__((aligned(16))) uint8_t zero_row[ROW656];
 
 template <bool PK>
 __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
@@ -228,7 +216,7 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   SPMLA_LDS uint8_t* mybuf = lds + L_TILES + w * NBUF * TILE;
   u32x4 rp[4];
   if (ntw > 0) {
-    const uint8_t* src = p.pool + (long long)(rcur >= 0 ? rcur : 0) * ROW656;
+    const uint8_t* src = rcur >= 0 ? p.pool + (long long)rcur * ROW656 : zero_row;
 #pragma unroll
     for (int i = 0; i < 16; ++i) dma16(src + (2 * i + half) * 16, mybuf + i * 1024);
     dma4(src + SC_OFF + half * 4, mybuf + T_SCT);
@@ -241,7 +229,7 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   // way). They are waited for with the first tile.
   const uint16_t* qrow = p.q + (long long)(hval ? col_tok(l32) : 0) * p.q_st + (long long)(hval ? h : 0) * p.q_sh;
   bf16x8 qf[16];
-  const uint32_t qmask = hval ? 0xffffffffu : 0u;       // heads past H: zero query (row 0 is read instead)
+  const uint32_t qmask = hval ? 0xffffffffu : 0u;       // heads past H: zero query
 #pragma unroll
   for (int kp = 0; kp < 8; ++kp) {
     const uint16_t* src = qrow + (2 * kp + half) * 16;
@@ -257,6 +245,8 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   float m_run = -__builtin_inff();     // reference max of this lane's head (log2 units)
   float l_run = 0.f;                   // sum of p over this lane's 16 rows of every tile
   bool started = false;                // wave-uniform: O holds contributions
+  int eps = 0;                         // P, O and l_run carry a factor 2^-eps (f16 range of P')
+  float elim = 0.f;                    // 2^(9 + eps) once eps is set
 
   f32x16 O[16];
 #pragma unroll
@@ -296,7 +286,7 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     }
     const unsigned vmask = (unsigned)__ballot(rcur >= 0);  // rows of the tile that exist
     // the next tile's copy is issued in four parts, one per latent group, between that group's MFMAs
-    const uint8_t* nsrc = p.pool + (long long)(rnxt >= 0 ? rnxt : 0) * ROW656;
+    const uint8_t* nsrc = rnxt >= 0 ? p.pool + (long long)rnxt * ROW656 : zero_row;
     SPMLA_LDS uint8_t* nbuf = mybuf + ((j + 1) & 1) * TILE;
 
     // ---- latent part of S^T: group g = chunks 8g .. 8g + 7; group g + 1's K is read while group g's MFMAs run
@@ -355,6 +345,8 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     // ---- PV operands of group 0 (scales, V^T codes) read while the softmax runs
     f32x4 ps[4];
     i32x2 tv[8];
+    // 2 of the tile's 128 scales ([group][row]) per lane, for the range check of P' below
+    const f32x2 sc2 = *(SPMLA_LDS f32x2*)(tb + T_SCT + lane * 8);
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) ps[qd] = *(SPMLA_LDS f32x4*)(tb + T_SCT + (8 * qd + 4 * half) * 4);
 #pragma unroll
@@ -393,7 +385,25 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
       if (started) scale_acc(O, alpha);
       m_run = mn;
     }
-    const float mref = m_run > -__builtin_inff() ? m_run : 0.f;
+    // ---- f16 range of P' = P * scale: P carries a factor 2^-eps (O and l_run too; the merge adds eps back), so
+    // that P' < 2^TAU * 2^9 = 2^15 while every row scale of the tile is below 2^(9 + eps). eps is set by the first
+    // tile with a positive scale and rises (an exact power-of-two rescale of O and l_run) when a
+    // later tile's largest such scale passes 2^(9 + eps) -- rare: scales sit near amax / 448 of their rows.
+    if (__ballot(fmaxf(sc2[0], sc2[1]) > elim)) {     // (a missing row's scales are the zero row's)
+      float wm = fmaxf(sc2[0], sc2[1]);
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o, 64));
+      wm = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, wm)));
+      if (wm > elim) {                                   // then 2^(9 + en) > wm with en > eps (or eps unset)
+        const int en = __builtin_amdgcn_frexp_expf(wm) - 9;
+        const float f = __builtin_ldexpf(1.f, eps - en);
+        l_run *= f;
+        if (started) scale_acc(O, f);
+        eps = en;
+        elim = __builtin_ldexpf(1.f, 9 + eps);
+      }
+    }
+    const float mref = (m_run > -__builtin_inff() ? m_run : 0.f) + (float)eps;
     float P[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -459,7 +469,8 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   l_run += __shfl_xor(l_run, 32, 64);
   SPMLA_LDS float* s_ml = (SPMLA_LDS float*)(lds + L_ML);
   lds_barrier();                                 // every wave is done with its tiles (no copy in flight)
-  if (half == 0) { s_ml[w * 64 + l32] = m_run; s_ml[w * 64 + 32 + l32] = l_run; }
+  // the wave's (O, l_run) are relative to 2^(m_run + eps)
+  if (half == 0) { s_ml[w * 64 + l32] = m_run > -__builtin_inff() ? m_run + (float)eps : m_run; s_ml[w * 64 + 32 + l32] = l_run; }
   lds_barrier();
   // weight of wave v's partial for this lane's head: 2^(m_v - M) kv_scale / L (applied by the reducing wave, so
   // the partials go to LDS straight from the accumulator registers)
@@ -545,6 +556,39 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     if (p.opart == nullptr) p.lse[(long long)to * p.lse_st + ho] = lse_v;
     else p.lsepart[((long long)s * p.T + to) * p.H + ho] = lse_v;
   }
+}
+
+// Per-token launch of attn_kernel<false>: the arguments of spmla_attn_splitk / spmla_attn_merge, already checked by
+// the caller (spmla_attn.hip, which chooses this kernel for launches with few tokens). Any K: row ids are read from
+// global memory a tile ahead, not staged.
+int launch_tokens(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
+                  long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale, int S,
+                  void* out, long long o_st, long long o_sh, float* lse, long long lse_st, float* opart,
+                  float* lsepart, const float* prior_o, long long po_st, long long po_sh, const float* prior_lse,
+                  long long pl_st, void* stream) {
+  Params p;
+  p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh;
+  p.pool = (const uint8_t*)pool; p.R = R;
+  p.idx = idx; p.idx_st = idx_st; p.K = K; p.kcount = kcount;
+  p.T = T; p.H = H; p.S = S; p.HGN = (H + HG - 1) / HG;
+  p.c = sm_scale * kv_scale * 1.4426950408889634f;
+  p.kv_scale = kv_scale;
+  p.out = (uint16_t*)out; p.o_st = o_st; p.o_sh = o_sh; p.lse = lse; p.lse_st = lse_st;
+  p.opart = opart; p.lsepart = lsepart;
+  p.prior_o = prior_o; p.po_st = po_st; p.po_sh = po_sh; p.prior_lse = prior_lse; p.pl_st = pl_st;
+  p.mk = nullptr; p.cu = nullptr; p.ql = 1; p.tsh = 0; p.NR = T;
+  const long long nwork = (long long)T * S * p.HGN;
+  if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
+  const int grid = (int)((nwork + 7) / 8 * 8);
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute((const void*)attn_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       L_TOTAL);
+    if (e != hipSuccess) return (int)e;
+    attr = true;
+  }
+  hipLaunchKernelGGL(attn_kernel<false>, dim3(grid), dim3(256), L_TOTAL, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
 }
 
 }  // namespace pk

@@ -514,8 +514,13 @@ def attention_ok(q, idx):
 
 
 def auto_split(T, H, K, cus=256):
-    """Row splits per token: doubled while the launch has fewer workgroups than compute units and every split keeps
+    """Row splits per token. 1 when the unsplit launch has at least cus * 3 / 8 workgroups of 32 heads (the
+    head-group kernel: a workgroup of 32 heads over all K rows takes as long as one of 128 heads over K / 4 rows, so
+    a partly filled unsplit launch still beats a split one with its merge); else the in-kernel split merge over
+    128-head workgroups, doubled while that launch has fewer workgroups than compute units and every split keeps
     at least 8 tiles of 32 rows (at most 8 splits)."""
+    if T * ((H + 31) // 32) * 8 >= cus * 3:
+        return 1
     n = T * ((H + 127) // 128)
     s = 1
     while s < 8 and n * s < cus and K >= 2 * s * 256:

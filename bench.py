@@ -172,18 +172,22 @@ def run_config2(a, dev):
     reps = max(1, a.steps // n)
     ms = _timed(replay, reps, max(1, a.warmup // n)) / n
     gbs = ALG_BYTES / (ms * 1e-3) / 1e9
+    # unsplit decode launches run the head-group kernel, split ones the 128-head kernel with its in-kernel merge
+    kname = "spmla::pk::attn_kernel<false>" if split == 1 else "spmla::attn::fwd_kernel"
     roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "spmla::attn::fwd_kernel", "alg_bytes_per_launch": ALG_BYTES,
+            "kernel": kname, "alg_bytes_per_launch": ALG_BYTES,
             "mfma_tflops": round(ALG_FLOPS / (ms * 1e-3) / 1e12, 2),
             "mfma_frac_bf16_peak": round(ALG_FLOPS / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
     tf = os.path.join(ROOT, "profiles", "attn_kernel_config2_traffic.json")
     if os.path.exists(tf):   # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (calibrated)
-        roof["traffic"] = json.load(open(tf)).get("bytes_per_launch")
+        tj = json.load(open(tf))
+        if tj.get("kernel") == kname:
+            roof["traffic"] = tj.get("bytes_per_launch")
     cfg = {"workload": "BASELINE config 2: all-HBM sparse-MLA decode, B=64, H=128, ctx=32768/seq, top-2048, Row656 "
                        "rows, bf16 out + fp32 LSE; launches replayed from a HIP graph",
            "global_batch": B, "heads": H, "ctx": CTX, "topk": K, "row_bytes": ROWB, "idx_sets": a.idx_sets}
-    res = _line(METRIC, gbs, "GB/s", a, ms, "fp8e4m3 rows x bf16 q: bf16 MFMA (QK and PV), fp32 accumulate",
+    res = _line(METRIC, gbs, "GB/s", a, ms, "fp8e4m3 rows x bf16 q: bf16 MFMA (QK), f16 MFMA (PV), fp32 accumulate",
                 cfg, roof, step_us=round(ms * 1e3, 2), eager_step_us=round(eager_ms * 1e3, 2))
     if not a.no_cpu:
         res["cpu_baseline"] = _with_model(cpu_baseline(pool, q, idxs[0]))
@@ -480,7 +484,7 @@ def run_config5(a, dev):
     roof = {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None, "kernel": "spmla::attn::fwd_kernel"}
     res = _line("chunked prefill attention ms (8192 queries x 128 heads x top-2048) + cache write us", ms_a, "ms", a,
-                ms_a + ms_w, "bf16 MFMA (QK and PV), fp32 accumulate",
+                ms_a + ms_w, "f16 MFMA (QK latent and PV), bf16 MFMA (rope), fp32 accumulate",
                 {"workload": "BASELINE config 5: 8192 queries, 128 heads, top-2048 of <= 65536 prior rows; write "
                              "8192 rows at random slots of a paged cache (block 64)"}, roof, cpu, hib=False,
                 cache_write_us=round(ms_w * 1e3, 2),

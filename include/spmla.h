@@ -255,7 +255,10 @@ int spmla_compact_stage(const long long* rows, int tot, const int* sidx, long lo
  * opart == NULL (S == 1): out [T][H][512] bf16 (strides o_st, o_sh), lse [T][H] fp32 (stride lse_st).
  * opart != NULL (required for S > 1): the K entries are cut into S splits; opart [S][T][H][512] fp32 (normalized)
  * and lsepart [S][T][H] receive per-split partials for spmla_lse_merge (S = 1: one fp32 partial, e.g. per tier);
- * out / lse are not written then. ceil(ceil(K / S) / 32) * 32 <= 2048.
+ * out / lse are not written then. Any K. Two kernels serve it with the same results up to fp32 summation order:
+ * launches of at most 512 (token, split, 32-head group) work items run 32 heads per workgroup (decode batches),
+ * longer ones 128 heads per workgroup (prefill chunks; there ceil(ceil(K / S) / 32) * 32 > 2048 falls back to the
+ * first kernel).
  * Replaces LayerOffload.attend's decode kernels (oa2_v2_launch dotsnote/engine/arcstats_pkg/arcstats/csrc/
  * offload_attn2.cu:2021-2104, offload_split_launch csrc/offload_attn.cu:1155-1200, _sparse_mla_offload_split_kernel
  * sparse_offload.py:419-516) and triton_bf16_mla_sparse_interface (vllm_patch/.../ops/xpu_mla_sparse.py:182-278),
@@ -276,7 +279,8 @@ long long spmla_attn_ws_bytes(int T, int H, int S);
  * the bytes past them are scratch. So a workspace zero-filled once serves launches that run one after another,
  * except that a launch with a larger C than the previous launch on the same workspace needs the bytes from the
  * previous C to its own C zeroed first. Launches that may overlap need workspaces of their own. out 16-byte aligned
- * rows give 16-byte stores. S > 8: SPMLA_ELIMIT.
+ * rows give 16-byte stores. S > 8 or ceil(ceil(K / S) / 32) * 32 > 2048: SPMLA_ELIMIT. S = 1 is spmla_attn_splitk
+ * (ws unused).
  * Replaces the split-K decode launch with its partial combine (oa2_v2_launch dotsnote/engine/arcstats_pkg/arcstats/
  * csrc/offload_attn2.cu:2021-2104; _sparse_mla_offload_split_kernel + _combine_kernel sparse_offload.py:419-538). */
 int spmla_attn(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,

@@ -40,16 +40,18 @@ def _oracle_tokens(q, pool, idx, tokens, sm, kv_scale=1.0):
 
 def test_config2_full_size(dev):
     """B=64, 128 heads, top-2048 of 32768 rows per sequence over the 2,097,152-row pool (the last
-    sequence's rows sit at byte offsets up to 1.38e9); the default (in-kernel split-merge) launch vs the oracle on
-    the first, a middle and the last token, and vs the single-pass launch on every token."""
+    sequence's rows sit at byte offsets up to 1.38e9); the default launch (the head-group kernel, unsplit) vs the
+    oracle on the first, a middle and the last token, and vs the 128-head kernel with its in-kernel merge of 4 splits
+    on every token."""
     import bench
     from arcagi2_flashnext_dots3_amd import kernels
     pool, q, idxs = bench.build_inputs(dev, 1)
     idx = idxs[0]
     assert pool.shape[0] == 2097152 and int(idx.max()) >= 2097152 - 32768
     print("[fullsize] config 2: B=64, 2M-row pool", flush=True)
+    assert kernels.auto_split(64, 128, 2048) == 1
     out, lse = kernels.attend(q, pool, idx, bench.SM_SCALE)
-    o1, l1 = kernels.attend(q, pool, idx, bench.SM_SCALE, split=1)
+    o1, l1 = kernels.attend(q, pool, idx, bench.SM_SCALE, split=4)
     torch.cuda.synchronize()
     tokens = [0, 31, 63]
     o_ref, l_ref = _oracle_tokens(q, pool, idx, tokens, bench.SM_SCALE)
