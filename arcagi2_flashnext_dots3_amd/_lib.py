@@ -19,13 +19,13 @@ F = ctypes.c_float
 SIGNATURES = {
     "spmla_cache_write": [P, LL, P, LL, P, I, P, LL, I, LL, I, F, P],
     "spmla_index_key_write": [P, LL, P, I, P, LL, I, I, I, LL, I, P],
-    "spmla_index_logits": [P, LL, LL, P, LL, P, LL, I, LL, P, LL, I, P, P, I, I, I, I, I, I, I, P, LL, P],
-    "spmla_topk": [P, LL, P, I, I, I, P, LL, P],
+    "spmla_index_logits": [P, LL, LL, P, LL, P, LL, I, LL, P, LL, I, P, P, I, I, I, I, I, I, I, P, LL, I, P],
+    "spmla_topk": [P, LL, P, I, I, I, P, LL, I, P],
     "spmla_topk_ws_bytes": [I, I, I],
-    "spmla_topk_ws": [P, LL, P, I, I, I, P, LL, P, LL, P],
+    "spmla_topk_ws": [P, LL, P, I, I, I, P, LL, P, LL, I, P],
     "spmla_topk_scratch_bytes": [],
-    "spmla_topk_scratch": [P, LL, P, I, I, I, P, LL, P],
-    "spmla_topk_local": [P, LL, P, I, I, I, I, I, P, P],
+    "spmla_topk_scratch": [P, LL, P, I, I, I, P, LL, I, P],
+    "spmla_topk_local": [P, LL, P, I, I, I, I, I, P, I, P],
     "spmla_topk_merge": [P, I, I, I, I, I, P, LL, P],
     "spmla_rows_from_topk": [P, LL, P, P, LL, I, I, LL, I, I, P, LL, P, P],
     "spmla_gather": [P, LL, I, P, I, P, LL, P],

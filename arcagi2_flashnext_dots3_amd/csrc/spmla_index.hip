@@ -3,7 +3,8 @@
 // Logits (dotsnote/engine/arcstats_pkg/arcstats/shard_logits_v2.py:49-123, shard_indexer.py:63-91; torch statement
 // dotsnote/training/finetune/student.py:219-222):
 //   logit[row][j] = min(sum_h w[row][h] * relu(q[row][h] . kcode[j]) * ks[j], 60000) for positions j < ctx[row]
-//   (column j holds position j * P + rank of this rank's key store), -inf for j >= ctx (unless noinf).
+//   (column j holds position j * P + rank of this rank's key store), -inf for j >= ctx (unless noinf); stored as fp32,
+//   or rounded to fp16 (the reference's ARC_SHARD_F16OUT buffer, shard_indexer.py:28-29, :124).
 //   gfx950: each wave streams 8 tiles of 32 keys through a private LDS ring filled by LDS DMA (codes, scales and
 //   block-table entries; two tiles in flight); S = Q K^T on bf16 MFMA (32x32x16; e4m3 key codes convert exactly to
 //   bf16, two per instruction), 64 heads = 2 M blocks, keys as the B operand; the head reduction is in-lane plus
@@ -13,7 +14,8 @@
 // Top-k (dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:1-15, csrc/topk_select.cu:1-30 semantics):
 //   per row, the K largest values among columns j < n = min(ctx, Lc) by torch's order-preserving key
 //   (-0 < +0, NaN largest); equal keys -> lower column first; output positions sorted by (value desc, column asc),
-//   -1 where the value is +-inf and in slots >= n.
+//   -1 where the value is +-inf and in slots >= n. fp32 or fp16 logits: an fp16 key is the same order key of the
+//   16-bit pattern placed in the top half of the 32-bit key (low half zero), so one radix code serves both.
 //   gfx950: one 1024-thread workgroup per row, the row's keys in VGPRs (32 per thread, all loads in flight):
 //   11/11/10-bit radix levels with an LDS histogram; keys above the boundary bin are appended with one LDS atomic
 //   per wave; once the boundary bin holds at most TK_CAP keys the remaining levels run on those candidates alone;
@@ -39,7 +41,7 @@ struct LogitParams {
   const int* bt; long long bt_st; int bs;    // block table [req][...], block size (positions per block)
   const int* req; const int* ctx;            // per row
   int rows, Lc, P, rank, noinf;
-  float* out; long long out_st;
+  void* out; long long out_st;              // fp32, or fp16 (F16OUT); stride in elements
   int bs_sh, rpb_sh, p_sh;                   // log2 of bs, rpb, P when a power of two, else -1
   long long lim;                             // R_local * P (< 2^31): valid block-table positions lie below
   int clamp;                                 // 1: logits clamped at 60000 (shard kernels); 0: unclamped (paged)
@@ -75,7 +77,7 @@ constexpr int LG_WAVES = 4;
 // prefill gather: key j (column j) at store + j * k_st, scale kscale[j], valid for lo[row] <= j < ctx[row], no
 // block table (dsa_sm89.py:97-118).
 enum { LY_ROW = 0, LY_SHUF = 1, LY_FLAT = 2 };
-template <bool POW2, int LY>
+template <bool POW2, int LY, bool F16OUT = false>
 __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
   constexpr bool SHUF = LY == LY_SHUF, FLAT = LY == LY_FLAT;
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LG_WAVES * LG_WAVE];
@@ -86,12 +88,17 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
   const int half = lane >> 5, l32 = lane & 31;
   const int ctx = p.ctx[row];
   const int j_wv = blockIdx.y * LG_KPB + wv * LG_TPW * 32;   // first key of this wave
-  float* orow = p.out + (long long)row * p.out_st;
+  float* orow = (float*)p.out + (long long)row * p.out_st;            // fp32 output row
+  _Float16* hrow = (_Float16*)p.out + (long long)row * p.out_st;      // fp16 output row
+  auto put = [&](int j, float v) {
+    if constexpr (F16OUT) hrow[j] = (_Float16)v;                       // round to nearest even (+-inf kept)
+    else orow[j] = v;
+  };
   if (j_wv >= p.Lc) return;
   const int nt = min(LG_TPW, (p.Lc - j_wv + 31) >> 5);        // tiles of this wave (uniform)
   if ((long long)j_wv * p.P + p.rank >= ctx || p.lim == 0) {   // no key of this wave has a row
     if (!p.noinf)
-      for (int j = j_wv + lane; j < j_wv + 32 * nt && j < p.Lc; j += 64) orow[j] = -__builtin_inff();
+      for (int j = j_wv + lane; j < j_wv + 32 * nt && j < p.Lc; j += 64) put(j, -__builtin_inff());
     return;
   }
   const int* btr = FLAT ? nullptr : p.bt + (long long)p.req[row] * p.bt_st;
@@ -224,8 +231,8 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
     const int j = j_wv + 32 * t + l32;
     if (half == 0 && j < p.Lc) {
       const float lg = p.clamp ? fminf(part * sc, 60000.f) : part * sc;
-      if (ok0) orow[j] = lg;
-      else if (!p.noinf) orow[j] = -__builtin_inff();
+      if (ok0) put(j, lg);
+      else if (!p.noinf) put(j, -__builtin_inff());
     }
     ok0 = ok1;
     ok1 = ok2;
@@ -241,6 +248,28 @@ __device__ inline uint32_t okey(float v) {
   const uint32_t x = f2u(v);
   if (v != v) return 0xffffffffu;
   return (x & 0x80000000u) ? ~x : (x | 0x80000000u);
+}
+// the same key for an fp16 pattern, in the top 16 bits (low 16 bits zero; NaN largest)
+__device__ inline uint32_t okey16(uint32_t h) {
+  if ((h & 0x7fffu) > 0x7c00u) return 0xffff0000u;
+  return ((h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u)) << 16;
+}
+// key of logit j of a row (fp32 or fp16 elements)
+template <bool F16>
+__device__ inline uint32_t lkey(const void* x, long long j) {
+  if constexpr (F16) return okey16(((const uint16_t*)x)[j]);
+  else return okey(((const float*)x)[j]);
+}
+// keys of +inf and -inf
+template <bool F16>
+__device__ inline bool inf_key(uint32_t k) {
+  if constexpr (F16) return k == 0xfc000000u || k == 0x03ff0000u;
+  else return k == 0xff800000u || k == 0x007fffffu;
+}
+// row `row` of a logits matrix with element stride st
+template <bool F16>
+__device__ inline const void* lrow(const void* lg, int row, long long st) {
+  return (const uint8_t*)lg + (long long)row * st * (F16 ? 2 : 4);
 }
 
 // block-wide exclusive scan of a per-thread count (1024 threads = 16 waves)
@@ -392,10 +421,16 @@ __device__ inline void tk_sort_desc(unsigned long long* a, int n) {
   else if (np2 > 1) bitonic_desc(a, np2);
 }
 
-struct RowSrc {     // a logits row: candidate j = column j
-  const float* x; int n;
-  __device__ float val(int j) const { return x[j]; }
+template <bool F16>
+struct RowSrc {     // a logits row (fp32 or fp16): candidate j = column j
+  const void* x; int n;
+  __device__ uint32_t key(int j) const { return lkey<F16>(x, j); }
+  __device__ float val(int j) const {
+    if constexpr (F16) return (float)((const _Float16*)x)[j];
+    else return ((const float*)x)[j];
+  }
   __device__ int id(int j) const { return j; }
+  __device__ static bool inf(uint32_t k) { return inf_key<F16>(k); }
 };
 struct MergeSrc {   // all-gathered payloads [P][nrows][2 * kl] = [values | positions]: candidate c = (c / kl, c % kl)
   const float* allp; long long nrows; int row, kl, n;
@@ -405,7 +440,9 @@ struct MergeSrc {   // all-gathered payloads [P][nrows][2 * kl] = [values | posi
     return allp + ((long long)r * nrows + row) * 2 * kl;
   }
   __device__ float val(int c) const { int i; const float* b = seg(c, i); return b[i]; }
+  __device__ uint32_t key(int c) const { return okey(val(c)); }
   __device__ int id(int c) const { int i; const float* b = seg(c, i); return (int)f2u(b[kl + i]); }
+  __device__ static bool inf(uint32_t k) { return inf_key<false>(k); }
 };
 
 // Four copies of the 2048-bin histogram (lane & 3 picks one) split same-bin atomics of a wave four ways; a copy
@@ -474,7 +511,7 @@ __device__ inline void tk_load(const Src& src, int base, uint32_t (&k)[TK_KPT]) 
 #pragma unroll
   for (int i = 0; i < TK_KPT; ++i) {
     const int j = base + i * TK_NT + (int)threadIdx.x;
-    k[i] = j < src.n ? okey(src.val(j)) : 0u;
+    k[i] = j < src.n ? src.key(j) : 0u;
   }
 }
 
@@ -553,7 +590,7 @@ template <class Src>
 __device__ __forceinline__ int tk_select(const Src& src, int K, TopkLds& L) {
   const int tid = threadIdx.x, n = src.n;
   if (n <= K) {
-    for (int j = tid; j < n; j += TK_NT) L.sel[j] = tk_pack(okey(src.val(j)), j);
+    for (int j = tid; j < n; j += TK_NT) L.sel[j] = tk_pack(src.key(j), j);
     __syncthreads();
     return n;
   }
@@ -645,25 +682,25 @@ __device__ __forceinline__ void tk_emit_sorted(const Src& src, int nsel, int kou
       const unsigned long long e = L.sel[s];
       const uint32_t key = (uint32_t)(e >> 32);
       const int j = (int)(~(uint32_t)e);
-      const bool isinf = key == 0xff800000u || key == 0x007fffffu;   // +inf / -inf keys
-      if (!isinf) r = src.id(j);
+      if (!Src::inf(key)) r = src.id(j);                  // +-inf: no position
     }
     o[s] = r;
   }
 }
 
 struct TopkParams {
-  const float* lg; long long lg_st;
+  const void* lg; long long lg_st;                // fp32 or fp16 (the kernel's F16), stride in elements
   const int* ctx; int rows, Lc, K;
   int* out; long long out_st;
 };
 
+template <bool F16>
 __global__ void __launch_bounds__(TK_NT) topk_kernel(TopkParams p) {
   __shared__ TopkLds L;
   const int row = blockIdx.x;
   int n = p.ctx[row];
   n = n < 0 ? 0 : (n > p.Lc ? p.Lc : n);
-  const RowSrc src{p.lg + (long long)row * p.lg_st, n};
+  const RowSrc<F16> src{lrow<F16>(p.lg, row, p.lg_st), n};
   const int nsel = tk_select(src, p.K, L);
   tk_emit_sorted(src, nsel, p.K, p.out + (long long)row * p.out_st, L);
 }
@@ -710,7 +747,7 @@ __host__ inline TopkWs topk_ws_layout(int Lc) {
 }
 
 struct TopkWsParams {
-  const float* lg; long long lg_st;
+  const void* lg; long long lg_st;                // fp32 or fp16 (the kernels' F16), stride in elements
   const int* ctx; int rows, Lc, K;
   int* out; long long out_st;
   uint8_t* ws; TopkWs w;
@@ -728,6 +765,7 @@ __device__ inline TkwHdr tkw_state(const TopkWsParams& p, int row) {
   return p.w.hdr(p.ws, row)[p.level];
 }
 
+template <bool F16>
 __global__ void __launch_bounds__(TK_NT) topk_hist_kernel(TopkWsParams p) {
   __shared__ uint32_t hist[TK_HCOPY * TK_HSTR];
   const int row = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
@@ -739,14 +777,14 @@ __global__ void __launch_bounds__(TK_NT) topk_hist_kernel(TopkWsParams p) {
   const uint32_t prefix = (uint32_t)st.prefix, mask = (uint32_t)st.mask;
   for (int i = tid; i < TK_HCOPY * TK_HSTR; i += TK_NT) hist[i] = 0;
   __syncthreads();
-  const float* x = p.lg + (long long)row * p.lg_st;
+  const void* x = lrow<F16>(p.lg, row, p.lg_st);
   const int c0 = g * p.w.CL, c1 = min(c0 + p.w.CL, n);
   for (int base = c0; base < c1; base += 8 * TK_NT) {
     uint32_t k[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int j = base + i * TK_NT + tid;
-      k[i] = j < c1 ? okey(x[j]) : 0u;
+      k[i] = j < c1 ? lkey<F16>(x, j) : 0u;
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -763,6 +801,7 @@ __global__ void __launch_bounds__(TK_NT) topk_hist_kernel(TopkWsParams p) {
   }
 }
 
+template <bool F16>
 __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   __shared__ uint32_t wsum[17];
   __shared__ uint32_t sh[8];
@@ -825,14 +864,14 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   }
   unsigned long long* sel = p.w.sel(p.ws, row);
   unsigned long long* cand = p.w.cand(p.ws, row);
-  const float* x = p.lg + (long long)row * p.lg_st;
+  const void* x = lrow<F16>(p.lg, row, p.lg_st);
   const int c0 = g * p.w.CL, c1 = min(c0 + p.w.CL, n);
   for (int base = c0; base < c1; base += 8 * TK_NT) {
     uint32_t k[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int j = base + i * TK_NT + tid;
-      k[i] = j < c1 ? okey(x[j]) : 0u;
+      k[i] = j < c1 ? lkey<F16>(x, j) : 0u;
     }
     uint32_t selm = 0, candm = 0;
 #pragma unroll
@@ -868,11 +907,12 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   }
 }
 
+template <bool F16>
 __global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
   __shared__ TopkLds L;
   const int row = blockIdx.x, tid = threadIdx.x;
   const int n = tkw_n(p, row);
-  const RowSrc src{p.lg + (long long)row * p.lg_st, n};
+  const RowSrc<F16> src{lrow<F16>(p.lg, row, p.lg_st), n};
   int* o = p.out + (long long)row * p.out_st;
   int nsel = 0;
   bool full = n <= p.K;
@@ -904,18 +944,19 @@ __global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
 // pk[row] = [values fp32 | positions j * P + rank as int32 bits] in ascending column order; fewer than kl valid
 // columns: the rest is padded with -inf values and positions s * P + rank.
 struct LocalParams {
-  const float* lg; long long lg_st;
+  const void* lg; long long lg_st;                // fp32 or fp16 (the kernel's F16), stride in elements
   const int* ctx; int rows, rank, P, Lc, kl;
   float* pk;
 };
 
+template <bool F16>
 __global__ void __launch_bounds__(TK_NT) topk_local_kernel(LocalParams p) {
   __shared__ TopkLds L;
   const int row = blockIdx.x, tid = threadIdx.x;
   const int c = p.ctx[row];
   int n = c > p.rank ? (int)(((long long)c - p.rank + p.P - 1) / p.P) : 0;
   if (n > p.Lc) n = p.Lc;
-  const RowSrc src{p.lg + (long long)row * p.lg_st, n};
+  const RowSrc<F16> src{lrow<F16>(p.lg, row, p.lg_st), n};
   const int nsel = tk_select(src, p.kl, L);
   // ascending column order: sort descending on ~j (the low word of a selected entry)
   for (int i = tid; i < nsel; i += TK_NT) L.sel[i] = (unsigned long long)(uint32_t)L.sel[i] << 32;
@@ -1015,6 +1056,24 @@ int scratch_ptr(void** out) {
 }
 }  // namespace
 
+namespace spmla {
+namespace idx {
+// the passes of spmla_topk_ws on fp32 (F16 false) or fp16 logits
+template <bool F16>
+static void topk_ws_passes(TopkWsParams p, hipStream_t stream) {
+  p.level = 0;
+  hipLaunchKernelGGL(topk_hist_kernel<F16>, dim3(p.rows, p.w.G), dim3(TK_NT), 0, stream, p);
+  for (int level = 0; level < 2; ++level) {        // the level-1 histograms come from the level-0 collect
+    p.level = level;
+    hipLaunchKernelGGL(topk_collect_kernel<F16>, dim3(p.rows, p.w.G), dim3(TK_NT), 0, stream, p);
+  }
+  p.level = 2;                                      // header 2: the state after both levels
+  hipLaunchKernelGGL(topk_finish_kernel<F16>, dim3(p.rows), dim3(TK_NT), 0, stream, p);
+}
+
+}  // namespace idx
+}  // namespace spmla
+
 using namespace spmla;
 
 extern "C" {
@@ -1022,9 +1081,10 @@ extern "C" {
 int spmla_index_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
                        const void* store, long long R_local, int rows_per_block, long long block_stride,
                        const int* block_table, long long bt_st, int block_size, const int* req, const int* ctx,
-                       int rows, int H, int D, int Lc, int P, int rank, int noinf, float* out, long long out_st,
-                       void* stream) {
+                       int rows, int H, int D, int Lc, int P, int rank, int noinf, void* out, long long out_st,
+                       int out_dtype, void* stream) {
   if (rows < 0 || Lc < 0 || P <= 0 || rank < 0 || rank >= P || block_size <= 0 || rows_per_block <= 0) return SPMLA_EARG;
+  if (out_dtype != 0 && out_dtype != 1) return SPMLA_EARG;
   if (rows == 0 || Lc == 0) return SPMLA_OK;
   if (H != 64 || D != 128) return SPMLA_ELIMIT;
   if (R_local < 0 || R_local > (long long)INT_MAX / P) return SPMLA_ELIMIT;   // 32-bit row arithmetic
@@ -1042,10 +1102,14 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
   p.clamp = 1;
   p.lo = nullptr; p.kscale = nullptr; p.k_st = 0;
   dim3 grid(rows, (Lc + idx::LG_KPB - 1) / idx::LG_KPB);
-  if (p.bs_sh >= 0 && p.rpb_sh >= 0 && p.p_sh >= 0)
-    hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_ROW>), grid, dim3(256), 0, (hipStream_t)stream, p);
-  else
-    hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_ROW>), grid, dim3(256), 0, (hipStream_t)stream, p);
+  const bool pow2 = p.bs_sh >= 0 && p.rpb_sh >= 0 && p.p_sh >= 0;
+  if (out_dtype == 1) {
+    if (pow2) hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_ROW, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_ROW, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
+  } else {
+    if (pow2) hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_ROW>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_ROW>), grid, dim3(256), 0, (hipStream_t)stream, p);
+  }
   return (int)hipGetLastError();
 }
 
@@ -1103,15 +1167,16 @@ int spmla_mqa_logits(const void* q, long long q_st, long long q_sh, const float*
   return (int)hipGetLastError();
 }
 
-int spmla_topk(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
-               long long out_st, void* stream) {
-  if (rows < 0 || Lc < 0 || K <= 0) return SPMLA_EARG;
+int spmla_topk(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+               long long out_st, int dtype, void* stream) {
+  if (rows < 0 || Lc < 0 || K <= 0 || (dtype != 0 && dtype != 1)) return SPMLA_EARG;
   if (K > idx::TK_KMAX) return SPMLA_ELIMIT;
   if (rows == 0) return SPMLA_OK;
   if (!logits || !ctx || !out) return SPMLA_EARG;
   idx::TopkParams p;
   p.lg = logits; p.lg_st = lg_st; p.ctx = ctx; p.rows = rows; p.Lc = Lc; p.K = K; p.out = out; p.out_st = out_st;
-  hipLaunchKernelGGL(idx::topk_kernel, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  if (dtype == 1) hipLaunchKernelGGL(idx::topk_kernel<true>, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  else hipLaunchKernelGGL(idx::topk_kernel<false>, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 
@@ -1120,9 +1185,9 @@ long long spmla_topk_ws_bytes(int rows, int Lc, int K) {
   return (long long)rows * idx::topk_ws_layout(Lc).row_bytes;
 }
 
-int spmla_topk_ws(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
-                  long long out_st, void* ws, long long ws_bytes, void* stream) {
-  if (rows < 0 || Lc < 0 || K <= 0) return SPMLA_EARG;
+int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                  long long out_st, void* ws, long long ws_bytes, int dtype, void* stream) {
+  if (rows < 0 || Lc < 0 || K <= 0 || (dtype != 0 && dtype != 1)) return SPMLA_EARG;
   if (K > idx::TK_KMAX) return SPMLA_ELIMIT;
   if (rows == 0) return SPMLA_OK;
   if (!logits || !ctx || !out || !ws) return SPMLA_EARG;
@@ -1130,22 +1195,16 @@ int spmla_topk_ws(const float* logits, long long lg_st, const int* ctx, int rows
   idx::TopkWsParams p;
   p.lg = logits; p.lg_st = lg_st; p.ctx = ctx; p.rows = rows; p.Lc = Lc; p.K = K; p.out = out; p.out_st = out_st;
   p.ws = (uint8_t*)ws; p.w = idx::topk_ws_layout(Lc);
-  p.level = 0;
-  hipLaunchKernelGGL(idx::topk_hist_kernel, dim3(rows, p.w.G), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
-  for (int level = 0; level < 2; ++level) {        // the level-1 histograms come from the level-0 collect
-    p.level = level;
-    hipLaunchKernelGGL(idx::topk_collect_kernel, dim3(rows, p.w.G), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
-  }
-  p.level = 2;                                      // header 2: the state after both levels
-  hipLaunchKernelGGL(idx::topk_finish_kernel, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  if (dtype == 1) idx::topk_ws_passes<true>(p, (hipStream_t)stream);
+  else idx::topk_ws_passes<false>(p, (hipStream_t)stream);
   return (int)hipGetLastError();
 }
 
 long long spmla_topk_scratch_bytes(void) { return idx::TOPK_SCRATCH_BYTES; }
 
-int spmla_topk_scratch(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
-                       long long out_st, void* stream) {
-  if (rows < 0 || Lc < 0 || K <= 0) return SPMLA_EARG;
+int spmla_topk_scratch(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                       long long out_st, int dtype, void* stream) {
+  if (rows < 0 || Lc < 0 || K <= 0 || (dtype != 0 && dtype != 1)) return SPMLA_EARG;
   if (K > idx::TK_KMAX) return SPMLA_ELIMIT;
   if (rows == 0) return SPMLA_OK;
   if (!logits || !ctx || !out) return SPMLA_EARG;
@@ -1155,18 +1214,20 @@ int spmla_topk_scratch(const float* logits, long long lg_st, const int* ctx, int
   void* ws = nullptr;
   const int rc = scratch_ptr(&ws);
   if (rc != SPMLA_OK) return rc;
-  return spmla_topk_ws(logits, lg_st, ctx, rows, Lc, K, out, out_st, ws, need, stream);
+  return spmla_topk_ws(logits, lg_st, ctx, rows, Lc, K, out, out_st, ws, need, dtype, stream);
 }
 
-int spmla_topk_local(const float* logits, long long lg_st, const int* ctx, int rows, int rank, int P, int Lc, int kl,
-                     float* pk, void* stream) {
-  if (rows < 0 || Lc < 0 || kl <= 0 || P <= 0 || rank < 0 || rank >= P) return SPMLA_EARG;
+int spmla_topk_local(const void* logits, long long lg_st, const int* ctx, int rows, int rank, int P, int Lc, int kl,
+                     float* pk, int dtype, void* stream) {
+  if (rows < 0 || Lc < 0 || kl <= 0 || P <= 0 || rank < 0 || rank >= P || (dtype != 0 && dtype != 1))
+    return SPMLA_EARG;
   if (kl > idx::TK_KMAX) return SPMLA_ELIMIT;
   if (rows == 0) return SPMLA_OK;
   if (!logits || !ctx || !pk) return SPMLA_EARG;
   idx::LocalParams p;
   p.lg = logits; p.lg_st = lg_st; p.ctx = ctx; p.rows = rows; p.rank = rank; p.P = P; p.Lc = Lc; p.kl = kl; p.pk = pk;
-  hipLaunchKernelGGL(idx::topk_local_kernel, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  if (dtype == 1) hipLaunchKernelGGL(idx::topk_local_kernel<true>, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
+  else hipLaunchKernelGGL(idx::topk_local_kernel<false>, dim3(rows), dim3(idx::TK_NT), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 

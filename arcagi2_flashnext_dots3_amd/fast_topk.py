@@ -20,7 +20,7 @@ def enabled(level=1):
 
 
 def local(lg, ctx, rank, P, kl, pk=None, nt=None, agg=None):
-    """lg [rows, Lc] fp32 (column j = position j * P + rank; columns at or beyond the row's ctx are never read),
+    """lg [rows, Lc] fp32 or fp16 (column j = position j * P + rank; columns at or beyond the row's ctx are never read),
     ctx int32 [rows] -> pk [rows, 2 * kl] fp32 = [top-kl values | their positions (int32 bits)], selected columns in
     ascending column order; rows with fewer than kl valid columns padded with -inf (fast_topk.py:52-66).
     nt / agg (the reference's CTA-size knobs) are accepted and ignored."""

@@ -149,9 +149,15 @@ def mqa_logits(q, kv, weights, cu_seqlen_ks, cu_seqlen_ke):
 
 
 # ---------------------------------------------------------------------------------------------- indexer
-def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P=1, rank=0, noinf=False):
+# logits element types of the indexer kernels: the C-ABI's dtype argument
+_LG_DT = {torch.float32: 0, torch.float16: 1}
+
+
+def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P=1, rank=0, noinf=False,
+                 dtype=torch.float32):
     """q [rows, 64, 128] bf16, w [rows, 64] fp32, store [blocks, rpb, 132] uint8, block_table [nreq, cols] int32,
-    req / ctx [rows] int32 -> logits [rows, Lc] fp32 (column j = position j * P + rank)."""
+    req / ctx [rows] int32 -> logits [rows, Lc] (column j = position j * P + rank) in fp32, or in fp16 with
+    dtype=torch.float16 (each fp32 logit rounded to nearest even: the reference's ARC_SHARD_F16OUT)."""
     rows, H, D = q.shape
     _need(q.dtype == torch.bfloat16 and q.stride(2) == 1, "q bf16 with contiguous head dim")
     _need(w.dtype == torch.float32 and w.stride(1) == 1, "w fp32")
@@ -162,13 +168,13 @@ def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P
         R = store.shape[0]
         rpb, bstride = max(1, R), max(1, R) * KEYROW
     if out is None:
-        out = torch.empty(rows, max(Lc, 1), dtype=torch.float32, device=q.device)
-    _need(out.dtype == torch.float32 and out.stride(1) == 1 and out.shape[0] >= rows and out.shape[1] >= Lc,
-          "out fp32 [rows, >= Lc] with contiguous rows")
+        out = torch.empty(rows, max(Lc, 1), dtype=dtype, device=q.device)
+    _need(out.dtype in _LG_DT and out.stride(1) == 1 and out.shape[0] >= rows and out.shape[1] >= Lc,
+          "out fp32 / fp16 [rows, >= Lc] with contiguous rows")
     _lib.call("spmla_index_logits", q.data_ptr(), q.stride(0), q.stride(1), w.data_ptr(), w.stride(0),
               store.data_ptr(), R, rpb, bstride, block_table.data_ptr(), block_table.stride(0), block_size,
               req.data_ptr(), ctx.data_ptr(), rows, H, D, Lc, P, rank, int(bool(noinf)), out.data_ptr(),
-              out.stride(0), _stream(q))
+              out.stride(0), _LG_DT[out.dtype], _stream(q))
     return out
 
 
@@ -198,10 +204,10 @@ def _attn_counter_bytes(T, H):
 
 
 def topk(logits, ctx, K, out=None, single_pass=False):
-    """logits [rows, Lc] fp32, ctx [rows] int32 -> [rows, K] int32 positions (value desc, position asc; -1 pad).
-    Several workgroups per row (spmla_topk_ws) unless single_pass (spmla_topk, one workgroup per row)."""
+    """logits [rows, Lc] fp32 or fp16, ctx [rows] int32 -> [rows, K] int32 positions (value desc, position asc; -1
+    pad). Several workgroups per row (spmla_topk_ws) unless single_pass (spmla_topk, one workgroup per row)."""
     rows, Lc = logits.shape
-    _need(logits.dtype == torch.float32 and logits.stride(1) == 1, "fp32 logits with contiguous rows")
+    _need(logits.dtype in _LG_DT and logits.stride(1) == 1, "fp32 / fp16 logits with contiguous rows")
     _need(ctx.dtype == torch.int32 and ctx.is_contiguous(), "ctx int32")
     if out is None:
         out = torch.empty(rows, K, dtype=torch.int32, device=logits.device)
@@ -209,12 +215,12 @@ def topk(logits, ctx, K, out=None, single_pass=False):
           "out int32 [rows, >= K] with contiguous rows")
     if single_pass:
         _lib.call("spmla_topk", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
-                  out.stride(0), _stream(logits))
+                  out.stride(0), _LG_DT[logits.dtype], _stream(logits))
         return out
     nb = int(_lib.lib().spmla_topk_ws_bytes(rows, Lc, K))
     ws, _ = _workspace("topk", logits.device, nb)
     _lib.call("spmla_topk_ws", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
-              out.stride(0), ws.data_ptr(), ws.numel(), _stream(logits))
+              out.stride(0), ws.data_ptr(), ws.numel(), _LG_DT[logits.dtype], _stream(logits))
     return out
 
 
@@ -222,28 +228,28 @@ def topk_scratch(logits, ctx, K, out=None):
     """topk without a workspace or any allocation in the library (spmla_topk_scratch): the passes use the library's
     fixed per-GPU scratch. Calls that overlap on one GPU race. Sizes beyond the scratch raise (SPMLA_ELIMIT)."""
     rows, Lc = logits.shape
-    _need(logits.dtype == torch.float32 and logits.stride(1) == 1, "fp32 logits with contiguous rows")
+    _need(logits.dtype in _LG_DT and logits.stride(1) == 1, "fp32 / fp16 logits with contiguous rows")
     _need(ctx.dtype == torch.int32 and ctx.is_contiguous() and ctx.shape[0] >= rows, "ctx int32 [rows]")
     if out is None:
         out = torch.empty(rows, K, dtype=torch.int32, device=logits.device)
     _need(out.dtype == torch.int32 and out.stride(1) == 1 and out.shape[0] >= rows and out.shape[1] >= K,
           "out int32 [rows, >= K]")
     _lib.call("spmla_topk_scratch", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K,
-              out.data_ptr(), out.stride(0), _stream(logits))
+              out.data_ptr(), out.stride(0), _LG_DT[logits.dtype], _stream(logits))
     return out
 
 
 def topk_local(lg, ctx, rank, P, kl, pk=None):
-    """fast_topk.local: lg [rows, Lc] fp32 (column j = position j * P + rank), ctx [rows] int32 positions ->
+    """fast_topk.local: lg [rows, Lc] fp32 or fp16 (column j = position j * P + rank), ctx [rows] int32 positions ->
     pk [rows, 2 * kl] fp32 = [top-kl values | their positions as int32 bits], ascending column order, -inf padded."""
     rows, Lc = lg.shape
-    _need(lg.dtype == torch.float32 and lg.stride(1) == 1, "fp32 logits with contiguous rows")
+    _need(lg.dtype in _LG_DT and lg.stride(1) == 1, "fp32 / fp16 logits with contiguous rows")
     _need(ctx.dtype == torch.int32 and ctx.is_contiguous(), "ctx int32")
     if pk is None:
         pk = torch.empty(rows, 2 * kl, dtype=torch.float32, device=lg.device)
     _need(pk.dtype == torch.float32 and pk.is_contiguous() and pk.shape[-1] == 2 * kl, "pk [rows, 2 * kl] fp32")
     _lib.call("spmla_topk_local", lg.data_ptr(), lg.stride(0), ctx.data_ptr(), rows, rank, P, Lc, kl, pk.data_ptr(),
-              _stream(lg))
+              _LG_DT[lg.dtype], _stream(lg))
     return pk
 
 

@@ -83,11 +83,13 @@ class LayerOffload:
     """
 
     def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
-                 spill_rows=131072, overlap_fill=True, two_choice=False, cache_fmt="row656"):
+                 spill_rows=131072, overlap_fill=True, two_choice=False, cache_fmt="row656", packed=False):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         if cache_mode not in ("static", "ways"):
             raise ValueError("cache_mode must be 'static' or 'ways'")
+        if packed and (cache_mode != "static" or cache_fmt != "row656"):
+            raise ValueError("packed=True takes the static hot set with Row656 lines (or no cache)")
         self.R = int(num_host_rows)
         self.device = torch.device(device)
         self.key = key
@@ -105,6 +107,8 @@ class LayerOffload:
         self._ws = {}
         self.mode = cache_mode
         self.overlap_fill = bool(overlap_fill)
+        # request-packed MTP decode for ql > 1 (the reference's ARC_OFFLOAD_CUDA_PK, sparse_offload.py:1456-1515)
+        self.packed = bool(packed)
         self.wc = None
         if cache_mode == "ways":
             if self.C <= 0 or self.C % int(ways):
@@ -188,6 +192,36 @@ class LayerOffload:
             self._ws[name] = b
         return b[:n].view(shape)
 
+    def _attend_packed(self, q, idx, sm_scale, kv_scale, ql, out, lse, num_heads, return_lse):
+        """Request-packed MTP decode: the union of each request's rows (mtp_union, rows once each with token masks),
+        those rows staged in HBM -- hot rows copied from their cache lines, the others read over PCIe (decoded when the
+        host rows are Row400) --, then one packed attention per request (attend_packed)."""
+        T = q.shape[0]
+        u, mk, cnt = kernels.mtp_union(idx, ql=ql, R=self.R)
+        nreq, nmax = u.shape
+        N = nreq * nmax
+        uf = u.reshape(-1).to(torch.int64)
+        pos = torch.arange(N, dtype=torch.int64, device=q.device)
+        tiers = 2 if self.C else 1
+        staged = self._buf("pk_staged", (tiers * N, ROW), torch.uint8)
+        host_rows = uf
+        if self.C:
+            line = torch.where(uf >= 0, self.rowmap[uf.clamp(min=0)].to(torch.int64), torch.full_like(uf, -1))
+            hit = line >= 0
+            kernels.gather(self.cache, line, staged[:N])                    # hot rows from HBM (misses: zero rows)
+            host_rows = torch.where(hit, torch.full_like(uf, -1), uf)
+            su = torch.where(uf < 0, -1, torch.where(hit, pos, N + pos))
+        else:
+            su = torch.where(uf < 0, -1, pos)
+        hs = staged[N * (tiers - 1):]
+        if self.row_fmt == "e2m2":
+            kernels.row400_gather(self.host, host_rows, hs, pcie=True)
+        else:
+            kernels.gather(self.host, host_rows, hs, pcie=True)
+        su = su.to(torch.int32).view(nreq, nmax)
+        kernels.attend_packed(q, staged, idx, sm_scale, kv_scale, ql=ql, out=out, lse=lse, union=(su, mk, cnt))
+        return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+
     def _side(self, device):
         """Second stream (default priority) and the two events that order it against the caller's stream."""
         if getattr(self, "_side_sync", None) is None:
@@ -206,8 +240,9 @@ class LayerOffload:
                lse=None, return_lse=False):
         """q [T, H, 576] bf16, idx [T, K] int32 host rows (-1 / out of range = none) -> out [T, H, 512] bf16
         (reference LayerOffload.attend, sparse_offload.py:1350). return_lse: also the fp32 LSE [T, H]
-        (ln sum exp of the scaled scores; -inf for a token without rows). ql / mkey / slots are accepted for the
-        reference's signature (request packing and prefetch hints) and do not change the result."""
+        (ln sum exp of the scaled scores; -inf for a token without rows). ql: tokens per request; with packed=True and
+        ql > 1 the request-packed path runs (same result up to the fp32 summation order); mkey / slots (the
+        reference's prefetch hints) are accepted and do not change the result."""
         T, H, _ = q.shape
         K = idx.shape[1]
         num_heads = H if num_heads is None else num_heads
@@ -218,6 +253,8 @@ class LayerOffload:
         if T == 0:
             return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
         idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
+        if self.packed and ql is not None and 1 < int(ql) <= 6 and T % int(ql) == 0:
+            return self._attend_packed(q, idx, sm_scale, kv_scale, int(ql), out, lse, num_heads, return_lse)
         if self.wc is not None:
             return self._attend_ways(q, idx, sm_scale, kv_scale, out, lse, num_heads, return_lse)
         hbm = self._buf("hbm", (T, K), torch.int32)

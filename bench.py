@@ -364,13 +364,14 @@ def run_config4(a, dev):
         req = torch.arange(B, dtype=torch.int32, device=dev)
         ctx = torch.full((B,), L, dtype=torch.int32, device=dev)
         lg = torch.empty(B, L, dtype=torch.float32, device=dev)
+        lg16 = torch.empty(B, L, dtype=torch.float16, device=dev)
         out = torch.empty(B, K, dtype=torch.int32, device=dev)
 
-        def logits():
+        def logits(dst=lg):
             kernels._lib.call("spmla_index_logits", q.data_ptr(), q.stride(0), q.stride(1), w.data_ptr(),
                               w.stride(0), kc.data_ptr(), st.R_local, st.RPB, st.STRIDE_BLK, bt.data_ptr(),
                               bt.stride(0), bs, req.data_ptr(), ctx.data_ptr(), B, 64, 128, L, 1, 0, 1,
-                              lg.data_ptr(), lg.stride(0), kernels._stream(q))
+                              dst.data_ptr(), dst.stride(0), int(dst.dtype == torch.float16), kernels._stream(q))
 
         # eager (host dispatch from Python included) and from HIP graphs of 20 launches (the launches alone;
         # the top-k is four kernels per call)
@@ -378,6 +379,9 @@ def run_config4(a, dev):
         ms_t_eager = _timed(lambda: kernels.topk(lg, ctx, K, out=out), a.steps, a.warmup)
         ms_l = _graph_ms(logits, a.steps, a.warmup, reps=20)
         ms_t = _graph_ms(lambda: kernels.topk(lg, ctx, K, out=out), a.steps, a.warmup, reps=20)
+        # the reference's fp16 logits mode (ARC_SHARD_F16OUT): fp16 logits, top-k on fp16 keys
+        ms_l16 = _graph_ms(lambda: logits(lg16), a.steps, a.warmup, reps=20)
+        ms_t16 = _graph_ms(lambda: kernels.topk(lg16, ctx, K, out=out), a.steps, a.warmup, reps=20)
         key_bytes = B * L * 132
         alg = key_bytes + B * 64 * 128 * 2 + B * 64 * 4 + B * L * 4
         flops = B * L * 64 * 128 * 2
@@ -391,8 +395,11 @@ def run_config4(a, dev):
                            "logits_hbm_frac": round(alg / (ms_l * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                            "logits_tflops": round(flops / (ms_l * 1e-3) / 1e12, 1),
                            "topk_read_gbs": round(B * L * 4 / (ms_t * 1e-3) / 1e9, 1),
-                           "alg_bytes": alg, "cpu_baseline": cpu}
-        del kc, lg
+                           "alg_bytes": alg, "cpu_baseline": cpu,
+                           "f16_logits": {"step_us": round((ms_l16 + ms_t16) * 1e3, 2),
+                                          "logits_us": round(ms_l16 * 1e3, 2), "topk_us": round(ms_t16 * 1e3, 2),
+                                          "note": "the reference's ARC_SHARD_F16OUT mode: selection on fp16 logits"}}
+        del kc, lg, lg16
         torch.cuda.empty_cache()
     r = results["32768"]
     roof = {"bound": "hbm", "achieved": r["logits_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -689,6 +696,21 @@ def run_config1(a, dev):
                                            "lse": float((l.cpu() - el).abs().max())})
 
 
+def _child_variant(args, timeout=600):
+    """Run this script with `args` in a child process (a plain subprocess) and return the `detail` of the JSON line it
+    prints, or an error record; the primary line must still print."""
+    import subprocess
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__)] + args, capture_output=True, text=True,
+                           timeout=timeout)
+        lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+        if r.returncode != 0 or not lines:
+            return {"error": f"exit {r.returncode}: {(r.stderr or r.stdout)[-300:]}"}
+        return json.loads(lines[-1]).get("detail", {})
+    except Exception as e:
+        return {"error": repr(e)[:300]}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -729,18 +751,17 @@ def main():
     if a.config == 2:
         res = run_config2(a, dev)
         if not a.no_variant:
-            for key, fmt, cfmt in (("host_tier_variant", "row656", "row656"),
-                                   ("host_tier_compact_variant", "e2m2", "row656"),
-                                   ("host_tier_compact_cache_variant", "e2m2", "e2m2")):
-                try:
-                    res[key] = run_config3(a, dev, steps=min(a.steps, 20), row_fmt=fmt, cache_fmt=cfmt)
-                except Exception as e:   # the primary line must still print
-                    res[key] = {"error": repr(e)[:300]}
-            for key, two in (("host_tier_ways_variant", False), ("host_tier_ways_two_choice_variant", True)):
-                try:
-                    res[key] = run_config3_ways(a, dev, steps=min(a.steps, 20), row_fmt="e2m2", two=two)
-                except Exception as e:
-                    res[key] = {"error": repr(e)[:300]}
+            # each config-3 variant in a fresh child process (its own GPU context and pinned pool), so no variant
+            # inherits the allocator and pinned-memory state of the ones before it
+            st = str(min(a.steps, 20))
+            for key, extra in (("host_tier_variant", ["--host-rows", "row656"]),
+                               ("host_tier_compact_variant", ["--host-rows", "e2m2"]),
+                               ("host_tier_compact_cache_variant", ["--host-rows", "e2m2", "--cache-fmt", "e2m2"]),
+                               ("host_tier_ways_variant", ["--host-rows", "e2m2", "--cache", "ways"]),
+                               ("host_tier_ways_two_choice_variant",
+                                ["--host-rows", "e2m2", "--cache", "ways", "--two-choice"])):
+                print(f"[bench] {key}: child process", file=sys.stderr, flush=True)
+                res[key] = _child_variant(["--config", "3", "--steps", st, "--warmup", str(a.warmup)] + extra)
     elif a.config == 3:
         r = run_config3_ways(a, dev, row_fmt=a.host_rows, W=a.ways, two=a.two_choice) if a.cache == "ways" else \
             run_config3(a, dev, row_fmt=a.host_rows, cache_fmt=a.cache_fmt)

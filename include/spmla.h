@@ -49,23 +49,26 @@ int spmla_index_key_write(const void* k, long long k_st, const long long* slots,
 /* Indexer logits: out[row][j] = min(sum_h w[row][h] * relu(q[row][h] . kcode) * kscale, 60000) for the key at
  * position pos = j * P + rank < ctx[row] (located through block_table[req[row]][pos / block_size]), -inf for
  * pos >= ctx (columns j < Lc; noinf != 0 leaves tiles wholly beyond ctx unwritten). q [rows][H][D] bf16 with H = 64,
- * D = 128; w [rows][H] fp32; out [rows][Lc] fp32. ctx[row] <= block_size * (columns of the block table);
- * R_local * P <= 2^31 - 1 (SPMLA_ELIMIT otherwise).
+ * D = 128; w [rows][H] fp32; out [rows][Lc] fp32 (out_dtype 0) or fp16 (out_dtype 1: each fp32 logit rounded to
+ * nearest even, the reference's ARC_SHARD_F16OUT buffer, shard_indexer.py:28-29, :124; the 60000 clamp keeps it
+ * finite); out_st in elements. ctx[row] <= block_size * (columns of the block table); R_local * P <= 2^31 - 1
+ * (SPMLA_ELIMIT otherwise).
  * Replaces ShardStore.logits / _shard_logits_kernel and shard_logits_v2 'grp' / 'row8'
  * (dotsnote/engine/arcstats_pkg/arcstats/shard_indexer.py:63-91, :118-143; shard_logits_v2.py:15-138). */
 int spmla_index_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
                        const void* store, long long R_local, int rows_per_block, long long block_stride,
                        const int* block_table, long long bt_st, int block_size, const int* req, const int* ctx,
-                       int rows, int H, int D, int Lc, int P, int rank, int noinf, float* out, long long out_st,
-                       void* stream);
+                       int rows, int H, int D, int Lc, int P, int rank, int noinf, void* out, long long out_st,
+                       int out_dtype, void* stream);
 
-/* Exact top-K per row over columns j < min(ctx[row], Lc) of logits [rows][Lc] fp32: torch's order-preserving key
- * (-0 < +0, NaN largest), equal values -> lower column; out[row][0..K) = columns sorted by (value desc, column asc),
- * -1 where the value is +-inf and for slots beyond the valid columns. K <= 2048.
+/* Exact top-K per row over columns j < min(ctx[row], Lc) of logits [rows][Lc] (dtype 0: fp32, 1: fp16; lg_st in
+ * elements): torch's order-preserving key (-0 < +0, NaN largest), equal values -> lower column; out[row][0..K) =
+ * columns sorted by (value desc, column asc), -1 where the value is +-inf and for slots beyond the valid columns.
+ * K <= 2048. The dtype argument is topk_local_launch's (csrc/topk_select.cu:250-262).
  * Replaces fast_topk.local + fast_topk.merge at P = 1 (dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:52-78;
  * csrc/topk_select.cu:251-286) and the torch.topk path of sharded_topk (shard_indexer.py:194-221). */
-int spmla_topk(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
-               long long out_st, void* stream);
+int spmla_topk(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+               long long out_st, int dtype, void* stream);
 
 /* Bytes of workspace spmla_topk_ws needs for rows x Lc (0 for invalid sizes). */
 long long spmla_topk_ws_bytes(int rows, int Lc, int K);
@@ -76,8 +79,8 @@ long long spmla_topk_ws_bytes(int rows, int Lc, int K);
  * (every pass writes what the next reads); calls that share a workspace must not overlap. Same replacement as
  * spmla_topk (fast_topk.local + merge at P = 1, dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:52-78;
  * csrc/topk_select.cu:251-286; shard_indexer.py:194-221). */
-int spmla_topk_ws(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
-                  long long out_st, void* ws, long long ws_bytes, void* stream);
+int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                  long long out_st, void* ws, long long ws_bytes, int dtype, void* stream);
 
 /* spmla_topk_ws without a caller workspace and without any allocation: the passes use the library's own
  * fixed device scratch (a file-scope array of spmla_topk_scratch_bytes() = 16 MiB per GPU, held from library load
@@ -88,17 +91,18 @@ int spmla_topk_ws(const float* logits, long long lg_st, const int* ctx, int rows
  * particular initial contents. No counterpart in the reference: for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). */
 long long spmla_topk_scratch_bytes(void);
-int spmla_topk_scratch(const float* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
-                       long long out_st, void* stream);
+int spmla_topk_scratch(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                       long long out_st, int dtype, void* stream);
 
 /* fast_topk.local at rank `rank` of P: the row's valid columns are j < ceil((ctx[row] - rank) / P) (clipped to Lc);
  * the top kl of them by the same key and tie rule as spmla_topk go to pk[row] = [kl values fp32 | kl positions
  * j * P + rank as int32 bits] (pk row stride 2 * kl floats) in ascending column order; rows with fewer than kl valid
- * columns are padded with -inf values at positions s * P + rank. kl <= 2048.
+ * columns are padded with -inf values at positions s * P + rank. kl <= 2048. dtype 0: fp32 logits, 1: fp16 (the
+ * payload values are the fp16 values widened to fp32).
  * Replaces topk_local_launch (dotsnote/engine/arcstats_pkg/arcstats/csrc/topk_select.cu:251-270, binding
  * fast_topk.py:52-66). */
-int spmla_topk_local(const float* logits, long long lg_st, const int* ctx, int rows, int rank, int P, int Lc, int kl,
-                     float* pk, void* stream);
+int spmla_topk_local(const void* logits, long long lg_st, const int* ctx, int rows, int rank, int P, int Lc, int kl,
+                     float* pk, int dtype, void* stream);
 
 /* fast_topk.merge: allp [P][n][2 * kl] all-gathered local payloads (rank-major) -> out[row][0..kk) = positions of the
  * top kk of the P * kl candidates, ordered by (value desc, concatenation index asc), -1 where the value is +-inf;

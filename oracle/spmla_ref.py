@@ -69,7 +69,9 @@ PINS = {
                  " brute-force python loops on tiny cases; invariance under permutation of the selected rows",
     "lse_merge": "merge of disjoint splits == single-pass attention (exact math), single part == identity",
     "index_logits": "python triple loop on tiny cases; linearity in w; block-table indirection vs a flat store",
-    "topk": "torch.topk value sets; python sorted() with the (value desc, index asc) key on tiny / tie-heavy rows",
+    "topk": "torch.topk value sets; python sorted() with the (value desc, index asc) key on tiny / tie-heavy rows; "
+            "fp16 logits: widened exactly to fp32, whose order equals the fp16 order (python float comparison over "
+            "all 65536 fp16 patterns, NaN largest, -0 < +0)",
     "topk_local": "brute force python sort on tiny rows; at P = 1 the local + merge pair equals topk",
     "topk_merge": "python sorted() over concatenated candidates; merge(local(x)) == topk(x) at P = 1",
     "rows_from_topk": "python loop over the block table",
@@ -444,7 +446,8 @@ def okey(x):
 def topk(logits, ctx, K):
     """Per row: the K largest of columns j < min(ctx, Lc) (key okey, equal keys -> lower column), output sorted by
     (value desc, column asc), -1 for +-inf values and for missing slots (fast_topk.py:10-14 tie rule; merge
-    semantics csrc/topk_select.cu:13-15, :305-321; shard_indexer.py:212-221 maps +-inf to -1)."""
+    semantics csrc/topk_select.cu:13-15, :305-321; shard_indexer.py:212-221 maps +-inf to -1). fp16 logits (the
+    reference's fp16 key, csrc/topk_select.cu:26-31) are widened exactly to fp32, which keeps their order and ties."""
     logits = np.asarray(logits, dtype=np.float32)
     rows, Lc = logits.shape
     out = np.full((rows, K), -1, dtype=np.int32)

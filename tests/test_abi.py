@@ -48,16 +48,18 @@ def test_version():
       None, None), -2),
     (("spmla_attn_splitk", None, 0, 0, None, 0, None, 0, 4096, None, 1, 1, 1.0, 1.0, 1, None, 0, 0, None, 0, None,
       None, None), -2),
-    (("spmla_topk", None, 0, None, 1, 10, 5000, None, 0, None), -5),
-    (("spmla_topk", None, 0, None, 1, 10, 0, None, 0, None), -2),
-    (("spmla_topk_ws", None, 0, None, 1, 10, 5000, None, 0, None, 0, None), -5),
-    (("spmla_topk_ws", None, 0, None, 1, 10, 16, None, 0, None, 0, None), -2),
-    (("spmla_topk_scratch", None, 0, None, 1, 10, 5000, None, 0, None), -5),
-    (("spmla_topk_scratch", None, 0, None, -1, 10, 16, None, 0, None), -2),
+    (("spmla_topk", None, 0, None, 1, 10, 5000, None, 0, 0, None), -5),
+    (("spmla_topk", None, 0, None, 1, 10, 0, None, 0, 0, None), -2),
+    (("spmla_topk", 256, 16, 256, 1, 10, 16, 256, 16, 2, None), -2),          # dtype 0 (fp32) or 1 (fp16) only
+    (("spmla_topk_ws", None, 0, None, 1, 10, 5000, None, 0, None, 0, 0, None), -5),
+    (("spmla_topk_ws", None, 0, None, 1, 10, 16, None, 0, None, 0, 1, None), -2),
+    (("spmla_topk_scratch", None, 0, None, 1, 10, 5000, None, 0, 0, None), -5),
+    (("spmla_topk_scratch", None, 0, None, -1, 10, 16, None, 0, 1, None), -2),
     # 128 rows x 131072 columns need more workspace than the fixed 16 MiB scratch (placeholder pointers 256)
-    (("spmla_topk_scratch", 256, 131072, 256, 128, 131072, 2048, 256, 2048, None), -5),
-    (("spmla_topk_local", None, 0, None, 1, 0, 1, 100, 4096, None, None), -5),
-    (("spmla_topk_local", None, 0, None, 1, 2, 2, 100, 16, None, None), -2),
+    (("spmla_topk_scratch", 256, 131072, 256, 128, 131072, 2048, 256, 2048, 0, None), -5),
+    (("spmla_topk_local", None, 0, None, 1, 0, 1, 100, 4096, None, 0, None), -5),
+    (("spmla_topk_local", None, 0, None, 1, 2, 2, 100, 16, None, 0, None), -2),
+    (("spmla_topk_local", 256, 100, 256, 1, 0, 1, 100, 16, 256, 3, None), -2),
     (("spmla_topk_merge", None, 4, 2, 16, 33, 33, None, 0, None), -2),
     (("spmla_topk_merge", None, 4, 2, 2048, 4000, 4000, None, 0, None), -5),
     (("spmla_gather", None, 0, 650, None, 1, None, 0, None), -2),
@@ -83,7 +85,9 @@ def test_version():
     (("spmla_row400_copy", None, 0, None, None, 0, None, 1, 5, None), -2),
     (("spmla_row400_gather_tiers", None, 0, None, 4, None, 1, 4, None, 656, 3, None), -2),
     (("spmla_index_logits", None, 0, 0, None, 0, None, 0, 64, 0, None, 0, 64, None, None, 1, 32, 128, 10, 1, 0, 0,
-      None, 0, None), -5),
+      None, 0, 0, None), -5),
+    (("spmla_index_logits", 256, 64, 128, 256, 64, 256, 64, 16, 2112, 256, 8, 64, 256, 256, 1, 64, 128, 64, 1, 0, 0,
+      256, 64, 2, None), -2),                                               # out_dtype 0 (fp32) or 1 (fp16) only
     (("spmla_lse_merge", None, 0, 0, 0, 0, None, 0, 0, 0, 1, 1, None, 0, 0, None, None, 0, None), -2),
     # (pointer 256 below: a placeholder that the argument checks reject before anything is launched)
     (("spmla_topk_overlap", 256, 0, 0, 1, 1, 4096, 256, 256, None), -5),
@@ -104,7 +108,7 @@ def test_version():
     (("spmla_row576_gather", 256, 10, 256, 4, 256, 576, None), -3),
     # logits: local rows times P beyond 32-bit row arithmetic (R_local = INT_MAX / 4 + 1 with P = 4)
     (("spmla_index_logits", 256, 64, 128, 256, 64, 256, (2 ** 31 - 1) // 4 + 1, 16, 2112, 256, 8, 64, 256, 256, 1,
-      64, 128, 64, 4, 0, 0, 256, 64, None), -5),
+      64, 128, 64, 4, 0, 0, 256, 64, 0, None), -5),
     # the in-kernel split merge: a workspace is required, at most 8 splits
     (("spmla_attn", 256, 64, 64, 256, 100, 256, 8, 8, None, 1, 1, 1.0, 1.0, 4, 256, 512, 512, 256, 1, None, 0, None),
      -2),
@@ -140,7 +144,7 @@ def test_zero_sized_calls_are_noops():
     L = _lib.lib()
     assert L.spmla_attn_splitk(None, 0, 0, None, 0, None, 0, 0, None, 0, 1, 1.0, 1.0, 1, None, 0, 0, None, 0,
                                None, None, None) == 0
-    assert L.spmla_topk(None, 0, None, 0, 10, 16, None, 0, None) == 0
+    assert L.spmla_topk(None, 0, None, 0, 10, 16, None, 0, 0, None) == 0
     assert L.spmla_gather(None, 0, 656 - 656 % 16, None, 0, None, 0, None) == 0
 
 

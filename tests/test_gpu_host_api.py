@@ -104,12 +104,12 @@ def test_shard_store_and_sharded_topk(dev):
     assert np.array_equal(out.cpu().numpy(), ref.topk(glg, ctx.numpy(), K + 3))
 
 
-def _offload_layer(dev, R, C, seed):
+def _offload_layer(dev, R, C, seed, **kw):
     from arcagi2_flashnext_dots3_amd.sparse_offload import LayerOffload
     g = torch.Generator().manual_seed(seed)
     kv = torch.randn(R, 512, generator=g).to(torch.bfloat16)
     pe = torch.randn(R, 1, 64, generator=g).to(torch.bfloat16)
-    lo = LayerOffload(R, dev, key="model.layers.3.self_attn.indexer.k_cache", cache_rows=C)
+    lo = LayerOffload(R, dev, key="model.layers.3.self_attn.indexer.k_cache", cache_rows=C, **kw)
     slots = torch.randperm(R, generator=g)
     lo.store(kv.to(dev), pe.to(dev), slots.to(dev))
     torch.cuda.synchronize()
@@ -166,6 +166,37 @@ def test_offload_attend_tiers(dev, C):
     e_o, e_l = _attn_err(o.float().cpu().numpy(), lse.cpu().numpy(), eo, el)
     print(f"[offload attend] err o {e_o:.2e} lse {e_l:.2e}", flush=True)
     assert e_o <= 1e-2 and e_l <= 1e-3
+
+
+@pytest.mark.parametrize("C", [0, 1500])
+def test_offload_attend_packed_mtp(dev, C):
+    """packed=True with ql = 4 (the reference's request-packed MTP decode through LayerOffload.attend): the union rows
+    staged from both tiers, each token's softmax over its own rows; vs the fp64 oracle per token, and vs the
+    per-token path (ql = 1) of the same layer."""
+    R, ql, nreq, H, K = 4000, 4, 3, 64, 512
+    T = ql * nreq
+    lo, pool = _offload_layer(dev, R, C, 6, packed=True)
+    if C:
+        lo.set_hot_rows(torch.arange(0, 2 * C, 2, dtype=torch.int64, device=dev))
+    q = make_q(T, H, seed=7)
+    g = torch.Generator().manual_seed(8)
+    idx = torch.empty(T, K, dtype=torch.int32)
+    for r in range(nreq):                          # the tokens of a request share most of their rows
+        base = torch.randperm(R, generator=g)[: K + 64]
+        for j in range(ql):
+            idx[r * ql + j] = base[torch.randperm(K + 64, generator=g)[:K]].to(torch.int32)
+    idx[1, 200:] = -1                              # a short row
+    idx[5, :] = torch.arange(0, 2 * K, 2)          # all hits when cached
+    print(f"[offload packed] C={C} ql={ql} T={T}", flush=True)
+    o, lse = lo.attend(q.to(dev), idx.to(dev), SM, 1.0, H, ql=ql, return_lse=True)
+    o1, l1 = lo.attend(q.to(dev), idx.to(dev), SM, 1.0, H, ql=1, return_lse=True)
+    torch.cuda.synchronize()
+    eo, el = ref.attention(q.float().numpy(), pool, idx.numpy(), SM)
+    e_o, e_l = _attn_err(o.float().cpu().numpy(), lse.cpu().numpy(), eo, el)
+    print(f"[offload packed] err o {e_o:.2e} lse {e_l:.2e}", flush=True)
+    assert e_o <= 1e-2 and e_l <= 1e-3
+    d_o, d_l = _attn_err(o.float().cpu().numpy(), lse.cpu().numpy(), o1.float().cpu().numpy(), l1.cpu().numpy())
+    assert d_o <= 1e-2 and d_l <= 1e-4
 
 
 def _paged_setup(dev, nreq, bs, nb, ctx_len, seed):

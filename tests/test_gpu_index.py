@@ -143,3 +143,94 @@ def test_logits_then_topk_end_to_end(dev):
         gap = srt[2047] - srt[2048]
         if gap > 1e-5 * max(1.0, abs(srt[2047])) * 4:
             assert set(sel[r].tolist()) == set(np.argsort(-exp[r], kind="stable")[:2048].tolist())
+
+
+# ---- fp16 logits (the reference's ARC_SHARD_F16OUT buffer) and top-k over fp16 keys
+def test_index_logits_f16_is_the_rounded_f32(dev):
+    """fp16 logits bit for bit equal to the fp32 launch's logits rounded to nearest even (numpy's float32 -> float16),
+    -inf where the fp32 launch has -inf; the fp16 values also within half an fp16 ulp (plus the fp32 bound) of the
+    fp64 oracle."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    rows, L, bs = 6, 5000, 64
+    nbp = (L + bs - 1) // bs
+    nb = rows * nbp + 3
+    store = _keys(nb, bs, 40)
+    g = torch.Generator().manual_seed(41)
+    bt = torch.randperm(nb, generator=g)[: rows * nbp].reshape(rows, nbp).to(torch.int32)
+    q = torch.randn(rows, 64, 128, generator=g).to(torch.bfloat16)
+    w = torch.rand(rows, 64, generator=g) * 400.0                      # logits up to the 60000 clamp
+    req = torch.arange(rows, dtype=torch.int32)
+    ctx = torch.randint(L // 2, L + 1, (rows,), generator=g).to(torch.int32)
+    ctx[0] = L
+    args = (q.to(dev), w.to(dev), torch.from_numpy(store).to(dev).view(nb, bs, 132), bt.to(dev), bs, req.to(dev),
+            ctx.to(dev), L)
+    print(f"[logits f16] rows={rows} L={L}", flush=True)
+    l32 = kernels.index_logits(*args).cpu().numpy()
+    l16 = kernels.index_logits(*args, dtype=torch.float16)
+    torch.cuda.synchronize()
+    assert l16.dtype == torch.float16
+    l16 = l16.cpu().numpy()
+    assert np.array_equal(l16.view(np.uint16), l32.astype(np.float16).view(np.uint16))
+    assert (l32 == 60000.0).any()                                     # the clamp is exercised
+    exp = ref.index_logits(q.float().numpy(), w.numpy(), store, bt.numpy(), bs, req.numpy(), ctx.numpy(), L)
+    fin = np.isfinite(exp)
+    assert np.array_equal(np.isinf(l16), ~fin)
+    ulp = np.spacing(np.abs(exp[fin]).astype(np.float16)).astype(np.float64)
+    assert (np.abs(l16[fin].astype(np.float64) - exp[fin]) <= 0.5 * ulp + 2e-5 * np.maximum(1.0, np.abs(exp[fin]))).all()
+
+
+def _topk16_check(dev, lg16, ctx, K):
+    """All fp16 top-k entry points (workspace, one workgroup per row, fixed scratch, local payload) against the oracle
+    on the same values widened to fp32 (exact: the fp16 order equals the fp32 order of the widened values)."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    exp = ref.topk(lg16.astype(np.float32), ctx, K)
+    d16, dctx = torch.from_numpy(lg16).to(dev), torch.from_numpy(ctx).to(dev)
+    for name, fn in (("ws", lambda: kernels.topk(d16, dctx, K)),
+                     ("single", lambda: kernels.topk(d16, dctx, K, single_pass=True)),
+                     ("scratch", lambda: kernels.topk_scratch(d16, dctx, K))):
+        got = fn().cpu().numpy()
+        bad = np.where((got != exp).any(1))[0]
+        assert bad.size == 0, f"fp16 {name}: rows {bad[:8]} differ"
+    pk = kernels.topk_local(d16, dctx, 0, 1, K).cpu().numpy()
+    assert np.array_equal(pk.view(np.uint32), ref.topk_local(lg16.astype(np.float32), ctx, 0, 1, K).view(np.uint32))
+
+
+def test_topk_f16_ties_and_specials(dev):
+    """fp16 keys: heavy ties (every value is one of a few thousand fp16 numbers), signed zeros, NaN, +-inf, short
+    rows, and indexer-like concentrated values whose boundary bin needs the second level."""
+    g = np.random.default_rng(7)
+    rows, L = 12, 40000
+    lg = (280.0 + 56.0 * g.standard_normal((rows, L))).astype(np.float16)
+    lg[1] = g.standard_normal(L).astype(np.float16)
+    lg[2] = np.where(g.standard_normal(L) > 0, 0.0, -0.0).astype(np.float16)
+    lg[3, 100:30000] = -np.inf
+    lg[4, :] = -np.inf
+    lg[4, :10] = 3.0
+    lg[5, 7] = np.nan
+    lg[6, ::5] = np.inf
+    lg[7] = np.float16(60000.0)
+    ctx = np.full(rows, L, dtype=np.int32)
+    ctx[8], ctx[9], ctx[10] = 0, 2047, 2049
+    print("[topk f16] ties and specials", flush=True)
+    _topk16_check(dev, lg, ctx, 2048)
+
+
+def test_logits_f16_then_topk(dev):
+    """The reference's fp16 mode end to end: fp16 logits of the GPU, then top-k on them, bit-exact vs the oracle's
+    top-k of the same fp16 values."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    rows, L, bs = 4, 8192, 64
+    nbp = L // bs
+    store = _keys(rows * nbp, bs, 50)
+    g = torch.Generator().manual_seed(51)
+    bt = torch.arange(rows * nbp, dtype=torch.int32).reshape(rows, nbp)
+    q = torch.randn(rows, 64, 128, generator=g).to(torch.bfloat16)
+    w = torch.rand(rows, 64, generator=g)
+    req = torch.arange(rows, dtype=torch.int32)
+    ctx = torch.full((rows,), L, dtype=torch.int32)
+    ctx[1] = L - 1000
+    print("[logits f16 + topk]", flush=True)
+    lg = kernels.index_logits(q.to(dev), w.to(dev), torch.from_numpy(store).to(dev).view(-1, bs, 132), bt.to(dev),
+                              bs, req.to(dev), ctx.to(dev), L, dtype=torch.float16)
+    sel = kernels.topk(lg, ctx.to(dev), 2048).cpu().numpy()
+    assert np.array_equal(sel, ref.topk(lg.cpu().numpy().astype(np.float32), ctx.numpy(), 2048))

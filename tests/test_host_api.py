@@ -128,3 +128,13 @@ def test_host_pool_capacity_guard(monkeypatch):
     monkeypatch.setattr(so, "host_memory_available", lambda: 1 << 20)   # the constructor checks before pinning
     with pytest.raises(RuntimeError, match="host pool"):
         so.LayerOffload(1 << 20, "cpu")
+
+
+def test_packed_option_rejects_caches_it_cannot_stage():
+    """packed=True (request-packed MTP decode) stages union rows from the static hot set's Row656 lines or the host
+    pool; the W-way cache and compact cache lines are refused before anything is allocated."""
+    from arcagi2_flashnext_dots3_amd import sparse_offload as so
+    with pytest.raises(ValueError, match="packed"):
+        so.LayerOffload(1024, "cpu", cache_rows=64, cache_mode="ways", ways=16, packed=True)
+    with pytest.raises(ValueError, match="packed"):
+        so.LayerOffload(1024, "cpu", cache_rows=64, row_fmt="e2m2", cache_fmt="e2m2", packed=True)

@@ -317,3 +317,36 @@ def test_tier_split_and_gather_hand_example():
     assert host[0, :2].tolist() == [0, 2] and sc[0] == 2 and np.all(host[0, 2:] == -1)
     src = np.arange(12, dtype=np.uint8).reshape(3, 4)
     assert ref.gather(src, np.array([2, -1, 0, 3])).tolist() == [[8, 9, 10, 11], [0] * 4, [0, 1, 2, 3], [0] * 4]
+
+
+def test_topk_fp16_order_is_the_widened_fp32_order():
+    """The oracle selects on fp16 logits by widening them to fp32: over all 65536 fp16 patterns, the fp32 order key
+    of the widened value orders and ties them exactly as python's float comparison does (NaN largest, -0 below +0),
+    i.e. as the reference's 16-bit key does."""
+    import functools
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = h.view(np.float16).astype(np.float64)
+
+    def cmp(a, b):                                  # NaN largest, then value, then -0 < +0
+        na, nb = np.isnan(f[a]), np.isnan(f[b])
+        if na or nb:
+            return int(na) - int(nb)
+        if f[a] != f[b]:
+            return -1 if f[a] < f[b] else 1
+        sa, sb = np.signbit(f[a]), np.signbit(f[b])
+        return int(sb) - int(sa)
+    k = ref.okey(h.view(np.float16).astype(np.float32)).astype(np.int64)
+    g = np.random.default_rng(9)
+    a, b = g.integers(0, 65536, 20000), g.integers(0, 65536, 20000)
+    for x, y in zip(a, b):
+        c = cmp(x, y)
+        assert (k[x] < k[y]) == (c < 0 and not (np.isnan(f[x]) and np.isnan(f[y])))
+        assert (k[x] == k[y]) == (c == 0 or (np.isnan(f[x]) and np.isnan(f[y])))
+    srt = sorted(range(0, 65536, 7), key=functools.cmp_to_key(cmp))
+    assert (np.diff(k[srt]) >= 0).all()
+    # the widened row gives the same selection as brute force on the fp16 values
+    row = g.standard_normal(300).astype(np.float16)
+    row[::7] = 0.5
+    row[3] = np.float16(-0.0)
+    exp = sorted(range(300), key=lambda j: (-float(row[j]), j))[:64]
+    assert list(ref.topk(row[None].astype(np.float32), np.array([300]), 64)[0]) == exp
