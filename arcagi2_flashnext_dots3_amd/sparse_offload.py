@@ -25,6 +25,7 @@ import os
 import torch
 
 from . import kernels
+from .diagnostics import AttnTimer
 
 ROW = kernels.ROW656
 HOST_ROW = {"row656": kernels.ROW656, "e2m2": kernels.ROW400}
@@ -83,7 +84,8 @@ class LayerOffload:
     """
 
     def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
-                 spill_rows=131072, overlap_fill=True, two_choice=False, cache_fmt="row656", packed=False):
+                 spill_rows=131072, overlap_fill=True, two_choice=False, cache_fmt="row656", packed=False,
+                 time_every=None):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         if cache_mode not in ("static", "ways"):
@@ -109,6 +111,10 @@ class LayerOffload:
         self.overlap_fill = bool(overlap_fill)
         # request-packed MTP decode for ql > 1 (the reference's ARC_OFFLOAD_CUDA_PK, sparse_offload.py:1456-1515)
         self.packed = bool(packed)
+        # GPU-event timing of every attend call, printed every N calls (ARC_OFFLOAD_ATTN2_TIME=N; 0: off)
+        if time_every is None:
+            time_every = int(os.environ.get("ARC_OFFLOAD_ATTN2_TIME", "0") or 0)
+        self.timer = AttnTimer(time_every)
         self.wc = None
         if cache_mode == "ways":
             if self.C <= 0 or self.C % int(ways):
@@ -242,7 +248,17 @@ class LayerOffload:
         (reference LayerOffload.attend, sparse_offload.py:1350). return_lse: also the fp32 LSE [T, H]
         (ln sum exp of the scaled scores; -inf for a token without rows). ql: tokens per request; with packed=True and
         ql > 1 the request-packed path runs (same result up to the fp32 summation order); mkey / slots (the
-        reference's prefetch hints) are accepted and do not change the result."""
+        reference's prefetch hints) are accepted and do not change the result. With time_every set, the call is
+        timed with GPU events (arm: packed / ways / tiers / host)."""
+        e0 = self.timer.begin(q.device)
+        res = self._attend(q, idx, sm_scale, kv_scale, num_heads, ql, out, lse, return_lse)
+        if e0 is not None:
+            packed = self.packed and ql is not None and 1 < int(ql) <= 6 and q.shape[0] % int(ql) == 0
+            arm = "packed" if packed else ("ways" if self.wc is not None else ("tiers" if self.C else "host"))
+            self.timer.end(e0, arm, q.shape[0], q.device)
+        return res
+
+    def _attend(self, q, idx, sm_scale, kv_scale, num_heads, ql, out, lse, return_lse):
         T, H, _ = q.shape
         K = idx.shape[1]
         num_heads = H if num_heads is None else num_heads

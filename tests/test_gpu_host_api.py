@@ -243,6 +243,62 @@ def test_portable_impl_paged_decode(dev):
     assert e_o <= 1e-2
 
 
+def test_portable_impl_offload_verify(dev):
+    """verify=True (ARC_OFFLOAD_VERIFY): both caches are written, the offload output is checked against the paged
+    one on every step and the paged one is returned; on agreeing paths no token is reported."""
+    from arcagi2_flashnext_dots3_amd.dsa import (CommonAttentionMetadata, DecodeMetadata, IndexerMetadata,
+                                                 PortableSparseBackend)
+    nreq, bs, nb, L, H, K = 3, 64, 64, 1000, 64, 256
+    Impl, bt, slots, kv, pe = _paged_setup(dev, nreq, bs, nb, L, 16)
+    cache = torch.zeros(nb, bs, 656, dtype=torch.uint8, device=dev)
+    g = torch.Generator().manual_seed(17)
+    topk = torch.stack([torch.randperm(L, generator=g)[:K] for _ in range(nreq)]).to(torch.int32)
+    impl = Impl(H, 576, SM, 1, None, None, "fp8_ds_mla", None, "decoder", None, topk_indices_buffer=topk.to(dev),
+                offload=True, cache_rows=500, verify=True)
+    impl.do_kv_cache_update(kv.to(dev), pe.to(dev), cache, slots.to(dev), "fp8_ds_mla", 1.0)
+    impl._off.set_hot_rows(slots[::2][:500].to(dev))
+    builder = PortableSparseBackend.get_builder_cls()(bs, K, 16, dev)
+    cam = CommonAttentionMetadata(query_start_loc=torch.arange(nreq + 1, dtype=torch.int32, device=dev),
+                                  num_reqs=nreq, num_actual_tokens=nreq, max_query_len=1, max_seq_len=L,
+                                  slot_mapping=slots[:nreq].to(dev), block_table_tensor=bt.to(dev))
+    md = builder.build(0, cam)
+    md.indexer = IndexerMetadata(num_decode_tokens=nreq, num_decodes=nreq, num_prefill_tokens=0,
+                                 decode=DecodeMetadata(block_table=bt.to(dev), seq_lens=torch.full((nreq,), L, device=dev),
+                                                       decode_lens=torch.ones(nreq, device=dev)))
+    q = make_q(nreq, H, seed=18)
+    print("[offload verify]", flush=True)
+    out, _ = impl.forward_mqa(q.to(dev), cache, md, None)
+    torch.cuda.synchronize()
+    st = impl.verify_stats
+    print(f"[offload verify] {st}", flush=True)
+    assert st["calls"] == 1 and st["tokens"] == nreq and st["bad"] == 0 and st["max_rel"] < 2e-2
+    flat = np.zeros((nb * bs, 656), dtype=np.uint8)
+    ref.cache_write_656(bf16_bits(kv), bf16_bits(pe.reshape(-1, 64)), slots.numpy(), flat)
+    assert np.array_equal(cache.cpu().numpy().reshape(-1, 656), flat)      # the paged cache was written too
+    rows = ref.rows_from_topk(topk.numpy(), np.arange(nreq), bt.numpy(), bs)
+    eo, el = ref.attention(q.float().numpy(), flat, rows, SM)
+    assert np.max(np.abs(out.float().cpu().numpy() - eo) / np.maximum(1.0, np.abs(eo))) <= 1e-2
+
+
+def test_offload_attend_timer(dev):
+    """time_every (ARC_OFFLOAD_ATTN2_TIME): every attend call is bracketed by GPU events, read back later without
+    a synchronization in the loop; the arm of each call is recorded."""
+    R, C, T, H, K = 3000, 800, 4, 64, 256
+    lines = []
+    lo, _ = _offload_layer(dev, R, C, 19, time_every=3)
+    lo.timer.log = lines.append
+    lo.set_hot_rows(torch.arange(0, 2 * C, 2, dtype=torch.int64, device=dev))
+    q = make_q(T, H, seed=20).to(dev)
+    idx = distinct_idx(T, K, R, seed=21).to(dev)
+    print("[offload timer]", flush=True)
+    for _ in range(5):
+        lo.attend(q, idx, SM, 1.0, H)
+    assert len(lo.timer.queue) == 5                # nothing read back yet (no wait in the loop)
+    stats = lo.timer.drain()
+    assert stats["tiers"][0] == 5 and stats["tiers"][1] > 0 and stats["tiers"][2] == 5 * T
+    assert lines and lines[0].startswith("[attn time] tiers: n=5")
+
+
 def test_portable_impl_offload_decode_and_prefill(dev):
     """Offload mode: decode tokens via LayerOffload.attend, one prefill chunk via staged (compacted) rows; both
     against the oracle over the same rows."""

@@ -138,3 +138,35 @@ def test_packed_option_rejects_caches_it_cannot_stage():
         so.LayerOffload(1024, "cpu", cache_rows=64, cache_mode="ways", ways=16, packed=True)
     with pytest.raises(ValueError, match="packed"):
         so.LayerOffload(1024, "cpu", cache_rows=64, row_fmt="e2m2", cache_fmt="e2m2", packed=True)
+
+
+def test_verify_outputs_reports_bad_tokens():
+    """ARC_OFFLOAD_VERIFY's comparison: per token max |a - b| / max(max |b|, 1e-3); a planted error on one token is
+    reported, agreeing tokens are not, and the statistics accumulate over calls."""
+    from arcagi2_flashnext_dots3_amd.diagnostics import verify_outputs
+    g = torch.Generator().manual_seed(0)
+    ref_o = torch.randn(5, 4, 16, generator=g)
+    test_o = ref_o + 1e-4 * torch.randn(5, 4, 16, generator=g)
+    test_o[2, 1, 3] += 0.5 * ref_o[2].abs().max()                       # token 2 off by half its largest value
+    lines, st = [], {}
+    rel = verify_outputs(test_o, ref_o, st, label="L3", log=lines.append)
+    assert (rel > 0.1).nonzero().flatten().tolist() == [2]
+    assert st["calls"] == 1 and st["tokens"] == 5 and st["bad"] == 1 and 0.49 < st["max_rel"] < 0.51
+    assert len(lines) == 1 and "bad=1" in lines[0] and "first=[2]" in lines[0]
+    verify_outputs(ref_o, ref_o, st, log=lines.append)
+    assert st["calls"] == 2 and st["bad"] == 1 and len(lines) == 1
+
+
+def test_topk_check_recall():
+    """ARC_SHARD_CHECK's statistic: recall of a selection against torch.topk over the row's first ctx columns."""
+    from arcagi2_flashnext_dots3_amd.diagnostics import TopkCheck
+    lg = torch.arange(20, dtype=torch.float32).flip(0).repeat(2, 1)      # column j holds 19 - j
+    lg[1, 3] = float("-inf")
+    ctx = torch.tensor([20, 10])
+    lines = []
+    chk = TopkCheck(every=2, log=lines.append)
+    got = torch.tensor([[0, 1, 2, 3], [0, 1, 2, 5]], dtype=torch.int32)
+    r = chk.check(lg, ctx, got, 4)
+    # row 0: exact; row 1: reference {0, 1, 2, 4} (column 3 is -inf), got {0, 1, 2, 5}: 3 of 4
+    assert abs(r - (1.0 + 0.75) / 2) < 1e-9 and chk.min_recall == 0.75
+    assert lines and "mean recall=0.87500" in lines[0]
