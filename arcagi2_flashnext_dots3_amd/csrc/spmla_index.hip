@@ -710,8 +710,10 @@ __global__ void __launch_bounds__(TK_NT) topk_kernel(TopkParams p) {
 //   hist:    the histogram of the level-0 11-bit digit over each chunk's keys;
 //   collect: every workgroup sums the G histograms of the level and finds the boundary bin b of the row's
 //            remaining need; it writes its chunk's keys above b (and in b when that completes the need) to the row's
-//            winner list, and the keys in b to the candidate list when the bin holds at most TK_CAP keys, at offsets
-//            given by the histograms of the chunks before it (no atomics; the lists are unordered). Otherwise the
+//            winner list, and the keys in b to the candidate list when the bin holds at most TK_CAP keys. A chunk's
+//            entries start at the offset the histograms of the chunks before it give; inside the chunk each wave
+//            takes its slots with one LDS atomic per pass, so the lists are unordered (the finishing pass orders
+//            by key and column, so the result does not depend on it). Otherwise the
 //            next level narrows the prefix to b, and this pass also builds its chunk's histogram of that level
 //            (into the other half of the histogram buffer, which no workgroup of the row is reading).
 // A finishing pass (one workgroup per row) resolves the candidates' remaining levels, sorts the K winners and
@@ -806,6 +808,7 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   __shared__ uint32_t wsum[17];
   __shared__ uint32_t sh[8];
   __shared__ uint32_t nh[TK_HCOPY * TK_HSTR];       // the next level's histogram of this chunk (when narrowing)
+  __shared__ uint32_t wcnt;                         // slots taken in the chunk: winners (low 16 bits), candidates
   const int row = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
   const int n = tkw_n(p, row);
   if (n <= p.K) return;
@@ -841,8 +844,10 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   (void)block_excl_scan(mine, wsum, &sum);
   if ((uint32_t)b0 == b) sh[4] = q0;
   if ((uint32_t)b1 == b) sh[4] = q1;
+  if (tid == 0) wcnt = 0u;
   __syncthreads();
-  uint32_t sb = (uint32_t)st.sb + sum, cb = sh[4];
+  const uint32_t sb = (uint32_t)st.sb + sum, cb = sh[4];   // this chunk's first winner / candidate slot
+  const int lane = tid & 63;
   const bool narrow = !whole && !fits && p.level + 1 < 2;   // uniform per row: the next level runs on bin b
   const int nshift = tk_shift(p.level + 1);
   if (narrow) {
@@ -881,11 +886,20 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
       selm |= (uint32_t)(in && (d > b || (whole && d == b))) << i;
       candm |= (uint32_t)(in && fits && d == b) << i;
     }
-    uint32_t tt;
-    const uint32_t off = block_excl_scan((uint32_t)__popc(selm) | ((uint32_t)__popc(candm) << 16), wsum, &tt);
+    // the lane's slots: an exclusive scan of the counts over the wave, after the wave's block of the chunk's slots
+    // (one LDS atomic; both counts stay below 2^16: at most K winners and TK_CAP candidates per chunk)
+    const uint32_t cntv = (uint32_t)__popc(selm) | ((uint32_t)__popc(candm) << 16);
+    uint32_t inc = cntv;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t t = __shfl_up(inc, o, 64);
+      if (lane >= o) inc += t;
+    }
+    uint32_t wb = 0u;
+    if (lane == 63) wb = atomicAdd(&wcnt, inc);
+    wb = __shfl(wb, 63, 64);
+    const uint32_t off = wb + inc - cntv;
     uint32_t so = sb + (off & 0xffffu), co = cb + (off >> 16);
-    sb += tt & 0xffffu;
-    cb += tt >> 16;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int j = base + i * TK_NT + tid;
