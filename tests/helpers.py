@@ -1,5 +1,5 @@
 """Seeded input generators shared by the tests and bench.py (synthetic data with the shapes of BASELINE.json's
-configs). Nothing here computes a result: oracle/ does that."""
+configs), and the attention output bar. Nothing here computes a result: oracle/ does that."""
 import numpy as np
 import torch
 
@@ -31,3 +31,17 @@ def make_q(T, H, seed=0, scale=1.0):
 def distinct_idx(T, K, R, seed=2):
     g = torch.Generator().manual_seed(seed)
     return torch.stack([torch.randperm(R, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+
+
+def half_ulp_bf16(x):
+    """Half a bf16 ulp of |x| (2^(e - 8) for |x| in [2^e, 2^(e + 1))), 0 for x = 0."""
+    a = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    return np.where(a > 0, 2.0 ** (e - 8), 0.0)
+
+
+def attn_excess(o, o_ref, tol=1e-2):
+    """Largest amount by which |o - o_ref| exceeds the attention output bar tol + half a bf16 ulp of o_ref (the
+    rounding of the bf16 output itself); <= 0 passes."""
+    o, o_ref = np.asarray(o, dtype=np.float64), np.asarray(o_ref, dtype=np.float64)
+    return float((np.abs(o - o_ref) - (tol + half_ulp_bf16(o_ref))).max()) if o.size else 0.0

@@ -1,13 +1,12 @@
 """GPU parity of spmla_attn_splitk / spmla_lse_merge against the CPU oracle (fp64), through the C-ABI.
-Tolerances (north star): max |out - ref| <= 1e-2 on the bf16 output, max |lse - ref| <= 1e-3 against the fp64 oracle.
-Stress cases whose outputs exceed 1 in magnitude (peaked softmax, few rows) are held to |out - ref| <= 1e-2 * max(1,
-|ref|): the bf16 rounding of the output alone is up to 2^-9 |ref|."""
+Tolerances (north star): |out - ref| <= 1e-2 + half a bf16 ulp of ref (the rounding of the bf16 output itself) on
+every element, max |lse - ref| <= 1e-3 against the fp64 oracle."""
 import numpy as np
 import pytest
 import torch
 
 from oracle import spmla_ref as ref
-from tests.helpers import distinct_idx, make_pool_656, make_q
+from tests.helpers import attn_excess, distinct_idx, make_pool_656, make_q
 
 pytestmark = pytest.mark.gpu
 OUT_TOL, LSE_TOL = 1e-2, 1e-3
@@ -31,11 +30,11 @@ def _check(dev, T, H, R, K, idx=None, split=1, kcount=None, seed=0, sm_scale=192
     l = lse.cpu().numpy()
     fin = np.isfinite(l_ref)
     assert np.array_equal(fin, np.isfinite(l)), "lse -inf pattern differs"
-    err_o = (np.abs(o - o_ref) / np.maximum(1.0, np.abs(o_ref))).max()
+    err_o = attn_excess(o, o_ref, OUT_TOL)
     err_l = np.abs(l[fin] - l_ref[fin]).max() if fin.any() else 0.0
-    print(f"[attn] max|o-ref|/max(1,|ref|) {err_o:.3e} max|lse-ref| {err_l:.3e} max|ref| {np.abs(o_ref).max():.2f}",
-          flush=True)
-    assert err_o <= OUT_TOL and err_l <= LSE_TOL
+    print(f"[attn] max|o-ref| {np.abs(o - o_ref).max():.3e} (excess over the bar {err_o:.3e}) max|lse-ref| "
+          f"{err_l:.3e} max|ref| {np.abs(o_ref).max():.2f}", flush=True)
+    assert err_o <= 0 and err_l <= LSE_TOL
     assert np.all(o[~fin] == 0)
     return err_o, err_l
 
@@ -105,7 +104,7 @@ def test_attend_merge_two_tiers(dev):
     o, l = out.float().cpu().numpy(), lse.cpu().numpy()
     fin = np.isfinite(l_ref)
     assert np.array_equal(fin, np.isfinite(l)) and not fin[3].any() and np.all(o[3] == 0)
-    assert (np.abs(o - o_ref) / np.maximum(1.0, np.abs(o_ref))).max() <= OUT_TOL
+    assert attn_excess(o, o_ref, OUT_TOL) <= 0
     assert np.abs(l[fin] - l_ref[fin]).max() <= LSE_TOL
     assert np.abs(o - o_m.float().cpu().numpy()).max() <= 2.0 ** -7 * max(1.0, np.abs(o).max())
     assert np.abs(l[fin] - l_m.cpu().numpy()[fin]).max() <= 1e-5

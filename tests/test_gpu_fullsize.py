@@ -9,22 +9,16 @@ import pytest
 import torch
 
 from oracle import spmla_ref as ref
+from tests.helpers import attn_excess
 
 pytestmark = pytest.mark.gpu
-
-
-def _half_ulp_bf16(x):
-    """Half a bf16 ulp of |x| (2^(e - 8) for |x| in [2^e, 2^(e + 1))), 0 for x = 0."""
-    a = np.abs(np.asarray(x, dtype=np.float64))
-    e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
-    return np.where(a > 0, 2.0 ** (e - 8), 0.0)
 
 
 def _check_rows(o, l, o_ref, l_ref, what):
     fin = np.isfinite(l_ref)
     assert np.array_equal(fin, np.isfinite(l)), f"{what}: lse -inf pattern"
-    viol = np.abs(o - o_ref) - (1e-2 + _half_ulp_bf16(o_ref))
-    assert viol.max() <= 0, f"{what}: output {viol.max():.3e} beyond the bar"
+    viol = attn_excess(o, o_ref)
+    assert viol <= 0, f"{what}: output {viol:.3e} beyond the bar"
     if fin.any():
         assert np.abs(l[fin] - l_ref[fin]).max() <= 1e-3, f"{what}: lse"
 
