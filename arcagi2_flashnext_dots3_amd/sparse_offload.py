@@ -85,13 +85,15 @@ class LayerOffload:
 
     def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
                  spill_rows=131072, overlap_fill=True, two_choice=False, cache_fmt="row656", packed=False,
-                 time_every=None):
+                 time_every=None, host_direct=False):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         if cache_mode not in ("static", "ways"):
             raise ValueError("cache_mode must be 'static' or 'ways'")
         if packed and (cache_mode != "static" or cache_fmt != "row656"):
             raise ValueError("packed=True takes the static hot set with Row656 lines (or no cache)")
+        if host_direct and (cache_mode != "static" or row_fmt != "row656" or cache_fmt != "row656"):
+            raise ValueError("host_direct=True takes Row656 host rows and the static hot set")
         self.R = int(num_host_rows)
         self.device = torch.device(device)
         self.key = key
@@ -111,6 +113,9 @@ class LayerOffload:
         self.overlap_fill = bool(overlap_fill)
         # request-packed MTP decode for ql > 1 (the reference's ARC_OFFLOAD_CUDA_PK, sparse_offload.py:1456-1515)
         self.packed = bool(packed)
+        # host-tier rows read by the attention in place over PCIe (the reference's loaders fetch misses inside the
+        # attention, csrc/offload_attn2.cu:177-208), instead of a staging copy into HBM first
+        self.host_direct = bool(host_direct)
         # GPU-event timing of every attend call, printed every N calls (ARC_OFFLOAD_ATTN2_TIME=N; 0: off)
         if time_every is None:
             time_every = int(os.environ.get("ARC_OFFLOAD_ATTN2_TIME", "0") or 0)
@@ -295,6 +300,9 @@ class LayerOffload:
             torch.where((host >= 0) & (host < self.R), ar, torch.full_like(ar, -1), out=sidx)
             kernels.attend(q, staged, sidx, sm_scale, kv_scale, out=out, lse=lse)
             return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+        if self.host_direct:
+            return self._attend_host_direct(q, idx, sm_scale, kv_scale, out, lse, num_heads, return_lse, hbm, hcnt,
+                                            host, mcnt)
         # the host list of token t is compacted (its mcnt[t] valid rows first): staged rows t * K + k, k < mcnt[t];
         # the attention's per-token count masks the rest, so the index map is the fixed identity
         sidx = self._identity(T, K, q.device)
@@ -323,6 +331,24 @@ class LayerOffload:
             ev_hbm.record(side)
         main.wait_event(ev_hbm)
         kernels.attend_merge(q, staged, sidx, sm_scale, kv_scale, op[0], lp[0], out=out, lse=lse, kcount=mcnt)
+        return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+
+    def _attend_host_direct(self, q, idx, sm_scale, kv_scale, out, lse, num_heads, return_lse, hbm, hcnt, host, mcnt):
+        """Two tiers, no staging copy: the HBM-tier attention (second stream) runs beside an attention that reads
+        each token's host rows in place from the pinned pool over PCIe; the two partials are then merged."""
+        T, H, _ = q.shape
+        op = self._buf("opart2", (2, T, H, kernels.D_LAT), torch.float32)
+        lp = self._buf("lpart2", (2, T, H), torch.float32)
+        main = torch.cuda.current_stream(q.device)
+        side, ev_split, ev_hbm = self._side(q.device)
+        ev_split.record(main)
+        side.wait_event(ev_split)
+        with torch.cuda.stream(side):
+            kernels.attend_partial(q, self.cache[:self.C], hbm, sm_scale, kv_scale, op[0:1], lp[0:1], kcount=hcnt)
+            ev_hbm.record(side)
+        kernels.attend_partial(q, self.host, host, sm_scale, kv_scale, op[1:2], lp[1:2], kcount=mcnt, R=self.R)
+        main.wait_event(ev_hbm)
+        kernels.lse_merge(op, lp, out=out, lse=lse)
         return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
 
     def _attend_ways(self, q, idx, sm_scale, kv_scale, out, lse, num_heads, return_lse):

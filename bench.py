@@ -226,14 +226,14 @@ def zipf_selections(nseq, K, R, seed, s=1.1, perm=None, device="cpu"):
     return out
 
 
-def run_config3(a, dev, steps=None, row_fmt="row656", cache_fmt="row656"):
+def run_config3(a, dev, steps=None, row_fmt="row656", cache_fmt="row656", host_direct=False):
     import torch
     from arcagi2_flashnext_dots3_amd import kernels
     from arcagi2_flashnext_dots3_amd.sparse_offload import HOST_ROW, LayerOffload, hot_rows_by_frequency
     steps = steps or a.steps
     C = R3 // 4
     compact = row_fmt == "e2m2"
-    lo = LayerOffload(R3, dev, cache_rows=C, row_fmt=row_fmt, cache_fmt=cache_fmt)
+    lo = LayerOffload(R3, dev, cache_rows=C, row_fmt=row_fmt, cache_fmt=cache_fmt, host_direct=host_direct)
     _cache_fill(lo.host, R3, 1, dev, fmt=2 if compact else 0)
     perm = torch.randperm(R3, generator=torch.Generator().manual_seed(3))
     warm = zipf_selections(64 * B, K, R3, seed=4, perm=perm, device=dev)   # 64 warm-up steps of B sequences
@@ -270,13 +270,15 @@ def run_config3(a, dev, steps=None, row_fmt="row656", cache_fmt="row656"):
            "ms_per_step": round(ms, 4), "hit_rate": round(hit, 4), "host_rows_per_step": int(round((1 - hit) * B * K)),
            "pcie_bytes_per_step": int(miss_bytes), "pcie_gbs_achieved": round(miss_bytes / (ms * 1e-3) / 1e9, 2),
            "h2d_copy_gbs": round(h2d, 2), "max_abs_diff_vs_single_tier": {"out": d_o, "lse": d_l},
-           "host_row_format": row_fmt, "cache_line_format": cache_fmt,
+           "host_row_format": row_fmt, "cache_line_format": cache_fmt, "host_rows_read_in_place": host_direct,
            "workload": "BASELINE config 3: B=64, H=128, top-2048 Zipf(1.1) rows of a 2,097,152-row "
                        + ("compact Row400 (e2m2b32)" if compact else "Row656") +
                        " pool in pinned host memory, HBM hot set = 524,288 most frequent rows over 64 warm-up steps "
                        + ("(compact Row400 lines in HBM, decoded into Row656 staging each step)" if cache_fmt == "e2m2"
                           else "(Row656 in HBM)") + "; tier split -> HBM-tier attention + host rows gathered over PCIe"
-                       + (" and decoded" if compact else "") + " -> host-tier attention -> LSE merge"}
+                       + (" and decoded" if compact else "") + " -> host-tier attention -> LSE merge"
+                       + (" (host_direct: no staging copy, the host-tier attention reads the pinned rows over PCIe)"
+                          if host_direct else "")}
     del lo, hb, db, staged
     torch.cuda.empty_cache()
     return res
@@ -727,6 +729,9 @@ def main():
     ap.add_argument("--two-choice", action="store_true", help="config 3 --cache ways: two-choice set placement")
     ap.add_argument("--cache-fmt", default="row656", choices=["row656", "e2m2"],
                     help="config 3 static cache with --host-rows e2m2: Row656 lines, or compact Row400 lines in HBM")
+    ap.add_argument("--host-direct", action="store_true",
+                    help="config 3 static cache, Row656 host rows: the host-tier attention reads the pinned rows in "
+                         "place over PCIe instead of a staging copy into HBM")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
                     help="only run 5 plain device-to-device copies of BYTES bytes (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -764,7 +769,7 @@ def main():
                 res[key] = _child_variant(["--config", "3", "--steps", st, "--warmup", str(a.warmup)] + extra)
     elif a.config == 3:
         r = run_config3_ways(a, dev, row_fmt=a.host_rows, W=a.ways, two=a.two_choice) if a.cache == "ways" else \
-            run_config3(a, dev, row_fmt=a.host_rows, cache_fmt=a.cache_fmt)
+            run_config3(a, dev, row_fmt=a.host_rows, cache_fmt=a.cache_fmt, host_direct=a.host_direct)
         res = _line("offload split-K decode step us (host tier + HBM hot rows), B=64 top2048", r["ms_per_step"] * 1e3,
                     "us", a, r["ms_per_step"], "bf16 MFMA, fp32 accumulate", {"workload": r["workload"]},
                     {"bound": "pcie", "achieved": r["pcie_gbs_achieved"], "peak": r["h2d_copy_gbs"], "unit": "GB/s",

@@ -175,6 +175,29 @@ def test_offload_attend_tiers(dev, C):
     assert e_o <= 0 and e_l <= 1e-3
 
 
+def test_offload_attend_host_direct(dev):
+    """host_direct=True: the host-tier attention reads the pinned rows in place over PCIe (no staging copy), its
+    partial merged with the HBM tier's; vs the fp64 oracle and vs the staged path of the same rows."""
+    R, C, T, H, K = 4000, 1500, 3, 64, 512
+    lo, pool = _offload_layer(dev, R, C, 4, host_direct=True)
+    lo.set_hot_rows(torch.arange(0, 2 * C, 2, dtype=torch.int64, device=dev))
+    q = make_q(T, H, seed=4)
+    idx = distinct_idx(T, K, R, seed=5)
+    idx[1, 100:] = -1                       # a short row
+    idx[2, :] = torch.arange(0, 2 * K, 2)   # all hits
+    print("[offload host direct]", flush=True)
+    o, lse = lo.attend(q.to(dev), idx.to(dev), SM, 1.0, H, return_lse=True)
+    lo.host_direct = False
+    o2, l2 = lo.attend(q.to(dev), idx.to(dev), SM, 1.0, H, return_lse=True)
+    torch.cuda.synchronize()
+    eo, el = ref.attention(q.float().numpy(), pool, idx.numpy(), SM)
+    e_o, e_l = _attn_err(o.float().cpu().numpy(), lse.cpu().numpy(), eo, el)
+    print(f"[offload host direct] excess {e_o:.2e} lse {e_l:.2e}", flush=True)
+    assert e_o <= 0 and e_l <= 1e-3
+    d_o, d_l = _gpu_diff(o.float().cpu().numpy(), lse.cpu().numpy(), o2.float().cpu().numpy(), l2.cpu().numpy())
+    assert d_o <= 1e-2 and d_l <= 1e-5
+
+
 @pytest.mark.parametrize("C", [0, 1500])
 def test_offload_attend_packed_mtp(dev, C):
     """packed=True with ql = 4 (the reference's request-packed MTP decode through LayerOffload.attend): the union rows
