@@ -322,17 +322,27 @@ __device__ inline void bitonic_desc(unsigned long long* a, int n) {
   __syncthreads();
 }
 
-// Lane-xor exchange of a 64-bit value: ds_swizzle (bit mode, xor within 32 lanes) for masks below 32, one
-// ds_bpermute with a precomputed address for 32.
+// Lane-xor exchange of a 64-bit value. Masks 1 and 2 are DPP quad permutations and 32 is v_permlane32_swap, all on
+// the SIMD's own VALU; 4, 8 and 16 go through the LDS crossbar (ds_swizzle, bit mode). The sort's stages are bound by
+// the LDS pipe that the CU's 16 waves share, so every exchange moved to the VALU shortens them.
 template <int M>
 __device__ inline unsigned long long xchg64(unsigned long long v, int perm32) {
+  (void)perm32;
+  const int vlo = (int)(uint32_t)v, vhi = (int)(uint32_t)(v >> 32);
   int lo, hi;
-  if constexpr (M < 32) {
-    lo = __builtin_amdgcn_ds_swizzle((int)(uint32_t)v, (M << 10) | 0x1f);
-    hi = __builtin_amdgcn_ds_swizzle((int)(uint32_t)(v >> 32), (M << 10) | 0x1f);
+  if constexpr (M == 1 || M == 2) {
+    constexpr int ctl = M == 1 ? 0xB1 : 0x4E;          // quad_perm [1, 0, 3, 2] / [2, 3, 0, 1]
+    lo = __builtin_amdgcn_mov_dpp(vlo, ctl, 0xF, 0xF, false);
+    hi = __builtin_amdgcn_mov_dpp(vhi, ctl, 0xF, 0xF, false);
+  } else if constexpr (M == 32) {
+    const auto a = __builtin_amdgcn_permlane32_swap((uint32_t)vlo, (uint32_t)vlo, false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap((uint32_t)vhi, (uint32_t)vhi, false, false);
+    const bool up = (__lane_id() & 32) != 0;
+    lo = (int)(up ? a[0] : a[1]);
+    hi = (int)(up ? b[0] : b[1]);
   } else {
-    lo = __builtin_amdgcn_ds_bpermute(perm32, (int)(uint32_t)v);
-    hi = __builtin_amdgcn_ds_bpermute(perm32, (int)(uint32_t)(v >> 32));
+    lo = __builtin_amdgcn_ds_swizzle(vlo, (M << 10) | 0x1f);
+    hi = __builtin_amdgcn_ds_swizzle(vhi, (M << 10) | 0x1f);
   }
   return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
 }
