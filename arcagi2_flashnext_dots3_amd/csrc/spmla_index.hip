@@ -529,7 +529,7 @@ __device__ inline void tk_load(const Src& src, int base, uint32_t (&k)[TK_KPT]) 
 // radix levels lvl..2 on the candidates held in registers; equal final keys go to the lowest columns. sb = entries
 // already in L.sel.
 __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, uint32_t prefix, uint32_t mask,
-                                                 uint32_t need, uint32_t sb) {
+                                                 uint32_t need, uint32_t sb, int ncols) {
   const int tid = threadIdx.x;
   unsigned long long e[TK_EPT];
   uint32_t vm = 0;                                   // bit i: e[i] is a candidate
@@ -572,11 +572,49 @@ __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, ui
     mask |= dm << shift;
     need -= above;
     if (level == 2) {
-      // binc candidates carry the final key; the need lowest columns win: sort them by column ascending
+      // binc candidates carry the final key; the need lowest columns win
       uint32_t eqm = 0;
 #pragma unroll
       for (int i = 0; i < TK_EPT; ++i)
         eqm |= (uint32_t)(((vm >> i) & 1u) && (uint32_t)(e[i] >> 32) == prefix) << i;
+      constexpr int BM_WPT = 8;                    // bitmap words per thread: TK_NT * 8 words in the histogram space
+      static_assert(TK_NT * BM_WPT <= TK_HCOPY * TK_HSTR, "bitmap fits the histogram space");
+      if (ncols <= 32 * TK_NT * BM_WPT) {
+        // a bitmap of the tied columns in the histogram space (free after the last level), then each column's rank
+        // among them from prefix sums of per-word bit counts: the need lowest are taken, no sort (the final output
+        // sort orders every winner anyway)
+        const int words = (ncols + 31) >> 5;
+        __syncthreads();
+        for (int w = tid; w < words; w += TK_NT) L.hist[w] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TK_EPT; ++i)
+          if ((eqm >> i) & 1u) {
+            const uint32_t j = ~(uint32_t)e[i];
+            atomicOr(&L.hist[j >> 5], 1u << (j & 31u));
+          }
+        __syncthreads();
+        const int w0 = tid * BM_WPT;
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int k = 0; k < BM_WPT; ++k)
+          if (w0 + k < words) cnt += (uint32_t)__popc(L.hist[w0 + k]);
+        uint32_t tot;
+        uint32_t r = block_excl_scan(cnt, L.wsum, &tot);   // ranks of this thread's first tied column
+#pragma unroll
+        for (int k = 0; k < BM_WPT; ++k) {
+          uint32_t bits = w0 + k < words ? L.hist[w0 + k] : 0u;
+          while (bits && r < need) {
+            const uint32_t j = 32u * (uint32_t)(w0 + k) + (uint32_t)(__ffs(bits) - 1);
+            bits &= bits - 1u;
+            L.sel[sb + r] = (((unsigned long long)prefix) << 32) | (uint32_t)~j;
+            ++r;
+          }
+        }
+        __syncthreads();
+        return;
+      }
+      // wider rows: sort the tied candidates by column ascending
       __syncthreads();                             // every thread has read its candidates: L.cand is free
       uint32_t cb2 = 0, sb2 = 0;
       tk_slots(0u, __popc(eqm), L, sb2, cb2, so, co);
@@ -653,7 +691,7 @@ __device__ __forceinline__ int tk_select(const Src& src, int K, TopkLds& L) {
     __syncthreads();
     if (whole) return K;
     if (fits) {
-      tk_resolve_cands(L, (int)binc, level + 1, prefix | (b << shift), mask | (dm << shift), need - above, sb);
+      tk_resolve_cands(L, (int)binc, level + 1, prefix | (b << shift), mask | (dm << shift), need - above, sb, n);
       return K;
     }
     prefix |= b << shift;
@@ -957,7 +995,7 @@ __global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
     __syncthreads();
     if (st.state == TKW_CANDS)
       tk_resolve_cands(L, st.binc, st.lvl, (uint32_t)st.prefix, (uint32_t)st.mask, (uint32_t)st.need,
-                       (uint32_t)st.sb);
+                       (uint32_t)st.sb, n);
     nsel = p.K;
   }
   tk_emit_sorted(src, nsel, p.K, o, L);
