@@ -471,6 +471,7 @@ def run_config5(a, dev):
     pe = torch.randn(NQ, 64, generator=g9, device=dev).to(torch.bfloat16)
     posn = torch.arange(pos0, CTXMAX, device=dev)
     slots = bt[0, posn // bs].long() * bs + posn % bs
+    _settle(lambda: kernels.cache_write(kv, pe, slots, cache))
     ms_w = _timed(lambda: kernels.cache_write(kv, pe, slots, cache), a.steps, a.warmup)
     g8 = torch.Generator().manual_seed(8)
     tk = torch.stack([torch.randperm(min(p + 1, CTXMAX), generator=g8)[:K] for p in range(pos0, CTXMAX)])
@@ -480,6 +481,7 @@ def run_config5(a, dev):
     out = torch.empty(NQ, H, 512, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(NQ, H, dtype=torch.float32, device=dev)
     flat = cache.view(-1, ROWB)
+    _settle(lambda: kernels.attend(q, flat, rows, SM_SCALE, out=out, lse=lse))
     ms_a = _timed(lambda: kernels.attend(q, flat, rows, SM_SCALE, out=out, lse=lse), max(3, a.steps // 20),
                   max(1, a.warmup // 10))
     flops = NQ * H * K * (2 * 576 + 2 * 512)
