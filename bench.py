@@ -179,12 +179,12 @@ def run_config2(a, dev):
         launch(cur[0] % len(idxs))
         cur[0] += 1
 
-    eager_ms = _timed(step, a.steps, a.warmup)
     n = len(idxs)
     replay = _graphed(lambda: [launch(i) for i in range(n)], 1)
     reps = max(1, a.steps // n)
     _settle(replay)
     ms = _timed(replay, reps, max(1, a.warmup // n)) / n
+    eager_ms = _timed(step, a.steps, a.warmup)          # right after, at the same settled clocks
     gbs = ALG_BYTES / (ms * 1e-3) / 1e9
     # unsplit decode launches run the head-group kernel, split ones the 128-head kernel with its in-kernel merge
     kname = "spmla::pk::attn_kernel<false>" if split == 1 else "spmla::attn::fwd_kernel"
