@@ -963,13 +963,8 @@ static int attn_launch(const void* q, long long q_st, long long q_sh, const void
   const long long nwork = (long long)T * S * p.HG;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)attn::fwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       attn::L_TOTAL);
-    if (e != hipSuccess) return (int)e;
-    attr = true;
-  }
+  static DynLds lds_attr;
+  if (const int e = lds_attr.ensure((const void*)attn::fwd_kernel, attn::L_TOTAL)) return e;
   hipLaunchKernelGGL(attn::fwd_kernel, dim3(grid), dim3(256), attn::L_TOTAL, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }

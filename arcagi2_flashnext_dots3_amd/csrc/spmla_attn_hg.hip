@@ -580,13 +580,8 @@ int launch_tokens(const void* q, long long q_st, long long q_sh, const void* poo
   const long long nwork = (long long)T * S * p.HGN;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)attn_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       L_TOTAL);
-    if (e != hipSuccess) return (int)e;
-    attr = true;
-  }
+  static DynLds lds_attr;
+  if (const int e = lds_attr.ensure((const void*)attn_kernel<false>, L_TOTAL)) return e;
   hipLaunchKernelGGL(attn_kernel<false>, dim3(grid), dim3(256), L_TOTAL, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
@@ -627,13 +622,8 @@ int spmla_attn_packed(const void* q, long long q_st, long long q_sh, const void*
   const long long nwork = (long long)nreq * S * p.HGN;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute((const void*)pk::attn_kernel<true>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, pk::L_TOTAL);
-    if (e != hipSuccess) return (int)e;
-    attr = true;
-  }
+  static DynLds lds_attr;
+  if (const int e = lds_attr.ensure((const void*)pk::attn_kernel<true>, pk::L_TOTAL)) return e;
   hipLaunchKernelGGL(pk::attn_kernel<true>, dim3(grid), dim3(256), pk::L_TOTAL, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }

@@ -3,6 +3,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <atomic>
+#include <mutex>
 
 namespace spmla {
 
@@ -146,5 +148,27 @@ __device__ inline void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
   asm volatile("" ::: "memory");
 }
+
+// ---- host: the dynamic-LDS limit of a kernel, raised once per device ---------------------------------------
+// hipFuncSetAttribute applies to the current device, so each kernel keeps one bit per device (ids 0..63) of where
+// it is set; the first launch on a device sets it under a mutex, later launches only read the bit. Safe to call
+// from several host threads.
+struct DynLds {
+  std::atomic<uint64_t> done{0};
+  std::mutex m;
+  int ensure(const void* fn, int bytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    const uint64_t bit = dev >= 0 && dev < 64 ? 1ull << dev : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return SPMLA_OK;
+    std::lock_guard<std::mutex> g(m);
+    if (bit && (done.load(std::memory_order_relaxed) & bit)) return SPMLA_OK;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return (int)e;
+    done.fetch_or(bit, std::memory_order_release);
+    return SPMLA_OK;
+  }
+};
 
 }  // namespace spmla

@@ -180,22 +180,48 @@ def index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=None, P
 
 _WS = {}
 _WS_CNT = {}      # attention workspaces: counter bytes of the last launch (the bytes known to be zero)
+_WS_KEEP = []     # every workspace ever handed out: a HIP graph captured with one keeps its address for good
 
 
 def _workspace(kind, device, nbytes, zero=False):
     """Device workspace of one kind of call, per (device, current stream): calls queued on one stream run in order,
-    so they can share it; calls on other streams get their own. Grown on demand; a replaced buffer returns to
-    torch's caching allocator under its stream, which hands it only to later work of that stream. zero: allocated
-    zero-filled (the attention's counters)."""
+    so they can share it; calls on other streams get their own. Grown on demand (at least doubling); a replaced
+    buffer stays allocated, so graphs captured with it stay valid. zero: allocated zero-filled (the attention's
+    counters). Under HIP graph capture nothing is allocated (a buffer allocated there would hold its contents only
+    after the first replay): the device's largest workspace of this kind from an eager call serves every capture, so
+    graphs that use it must be replayed one at a time, and a capture needing more raises. Returns (buffer, key);
+    key is None under capture."""
     dev = torch.device(device)
+    if torch.cuda.is_current_stream_capturing():
+        have = [b for (k, d, _), b in _WS.items() if k == kind and d == dev]
+        b = max(have, key=lambda t: t.numel(), default=None)
+        _need(b is not None and b.numel() >= nbytes,
+              f"{kind} workspace of {nbytes} bytes needed under HIP graph capture: pass one explicitly, or make an "
+              f"eager call of at least this size (reserve_workspace) before capturing")
+        return b, None
     key = (kind, dev, torch.cuda.current_stream(dev).cuda_stream)
     b = _WS.get(key)
     if b is None or b.numel() < nbytes:
-        n = max(nbytes, 256)
+        n = max(nbytes, 256, 2 * b.numel() if b is not None else 0)
         b = torch.zeros(n, dtype=torch.uint8, device=dev) if zero else torch.empty(n, dtype=torch.uint8, device=dev)
         _WS[key] = b
+        _WS_KEEP.append(b)
         _WS_CNT[key] = n if zero else 0
     return b, key
+
+
+def fused_max_tokens(H, cus=256):
+    """The most tokens for which auto_split picks the in-kernel split merge (H heads): below it attend needs a
+    workspace."""
+    return max(0, -(-cus * 3 // (8 * ((H + 31) // 32))) - 1)
+
+
+def reserve_workspace(device, H, T=None, split=8):
+    """Allocate now (eagerly) the attention workspace that attend's split merge needs for up to T tokens of H heads
+    (default: every size auto_split sends there), so that later HIP graph captures find it. No-op when present."""
+    T = fused_max_tokens(H) if T is None else T
+    if T > 0:
+        _workspace("attn", device, int(_lib.lib().spmla_attn_ws_bytes(T, H, split)), zero=True)
 
 
 def _attn_counter_bytes(T, H):
@@ -519,18 +545,24 @@ def attention_ok(q, idx):
             and idx.dtype == torch.int32 and idx.stride(1) == 1)
 
 
+ATTN_SPLIT_ROWS = 2048      # rows of one (token, split) in spmla_attn's split merge, rounded up to 32-row tiles
+
+
 def auto_split(T, H, K, cus=256):
     """Row splits per token. 1 when the unsplit launch has at least cus * 3 / 8 workgroups of 32 heads (the
     head-group kernel: a workgroup of 32 heads over all K rows takes as long as one of 128 heads over K / 4 rows, so
     a partly filled unsplit launch still beats a split one with its merge); else the in-kernel split merge over
     128-head workgroups, doubled while that launch has fewer workgroups than compute units and every split keeps
-    at least 8 tiles of 32 rows (at most 8 splits)."""
+    at least 8 tiles of 32 rows (at most 8 splits). 1 as well when a split would hold more than ATTN_SPLIT_ROWS
+    rows (the split kernel's limit; the head-group kernel takes any K)."""
     if T * ((H + 31) // 32) * 8 >= cus * 3:
         return 1
     n = T * ((H + 127) // 128)
     s = 1
     while s < 8 and n * s < cus and K >= 2 * s * 256:
         s *= 2
+    if -(-(-(-K // s)) // 32) * 32 > ATTN_SPLIT_ROWS:
+        return 1
     return s
 
 
@@ -543,8 +575,8 @@ def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None,
     """q [T, H, 576] bf16, pool [R, 656] uint8 Row656 rows (or a mapped host address with R given), idx [T, K]
     int32 rows -> (out [T, H, 512] bf16, lse [T, H] fp32). split > 1 (at most 8) cuts K into partials that the
     kernel merges (spmla_attn; ws: a uint8 workspace of attn_ws_bytes whose leading counter bytes are zero -- the
-    kernel leaves them so --, else a cached one per stream; under HIP graph capture pass ws, or the capture stream's
-    new workspace is zero-filled by every replay); None: auto_split."""
+    kernel leaves them so --, else a cached one per stream; under HIP graph capture either ws or a workspace reserved
+    by an earlier eager call, see reserve_workspace); None: auto_split."""
     T, H, _ = q.shape
     K = idx.shape[1]
     if split is None:
@@ -567,9 +599,12 @@ def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None,
     if ws is None:
         ws, key = _workspace("attn", q.device, nb, zero=True)
         cnt = _attn_counter_bytes(T, H)
-        if cnt > _WS_CNT[key]:            # counter bytes the previous launch used as scratch: cleared by a fill kernel
-            ws[_WS_CNT[key]:cnt].zero_()
-        _WS_CNT[key] = cnt
+        if key is None:                   # captured: replays come in any order, so every replay clears its counters
+            ws[:cnt].zero_()
+        else:
+            if cnt > _WS_CNT[key]:        # counter bytes the previous launch used as scratch: cleared by a fill kernel
+                ws[_WS_CNT[key]:cnt].zero_()
+            _WS_CNT[key] = cnt
     _need(ws.dtype == torch.uint8 and ws.numel() >= nb, "attend: workspace too small")
     _lib.call("spmla_attn", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(), idx.stride(0), K,
               _ptr(kcount), T, H, float(sm_scale), float(kv_scale), split, out.data_ptr(), out.stride(0),
@@ -683,19 +718,21 @@ def topk_overlap(sets):
     return hits, nvalid
 
 
-def mtp_union(idx, ql=None, cu=None, R=None, nmax=None):
+def mtp_union(idx, ql=None, cu=None, R=None, nmax=None, max_query_len=None):
     """The union of each request's MTP top-k rows with token masks: idx [T, topk] int32 rows, requests of ql tokens
-    (or boundaries cu [nreq + 1]) -> (u [nreq, nmax] int32 (-1 padded), mk [nreq, nmax] uint8, cnt [nreq] int32),
-    rows ordered by mask descending then first occurrence (the request-packed decode's row list)."""
+    (or boundaries cu [nreq + 1] on the device, with max_query_len, the host-known largest request, at most 6: the
+    boundaries themselves are not read back) -> (u [nreq, nmax] int32 (-1 padded), mk [nreq, nmax] uint8, cnt [nreq]
+    int32), rows ordered by mask descending then first occurrence (the request-packed decode's row list). A request
+    longer than 6 tokens is a caller error the kernel does not see: it uses the first 6."""
     T, topk = idx.shape
     _need(idx.dtype == torch.int32 and idx.stride(1) == 1, "idx int32 [T, topk]")
     _need(R is not None, "mtp_union: R (rows of the pool) is required")
     if cu is not None:
+        _need(max_query_len is not None, "mtp_union: cu needs max_query_len (the largest request, host-known)")
+        _need(0 <= int(max_query_len) <= 6, "mtp_union: at most 6 tokens per request")
         cu = cu.to(torch.int32).contiguous()
         nreq, ql_ = cu.shape[0] - 1, 0
         gmax = 6
-        if nreq > 0:   # the kernels take at most 6 tokens of a request: a longer request is an error, not a cut
-            _need(int((cu[1:] - cu[:-1]).max().item()) <= 6, "mtp_union: at most 6 tokens per request")
     else:
         _need(ql is not None and 0 < ql <= 6, "mtp_union: ql (1 .. 6) or cu")
         nreq, ql_ = (T + ql - 1) // ql, int(ql)
@@ -711,19 +748,20 @@ def mtp_union(idx, ql=None, cu=None, R=None, nmax=None):
 
 
 def attend_packed(q, pool, idx, sm_scale, kv_scale=1.0, ql=None, cu=None, out=None, lse=None, split=1, tpg=None,
-                  union=None):
+                  union=None, max_query_len=None):
     """Request-packed MTP decode (the reference's ARC_OFFLOAD_CUDA_PK path): the tokens of a request (ql tokens each,
     or boundaries cu) attend over the union of their top-k rows (mtp_union), each union row loaded and converted once
     per request and head group, each token's softmax kept to its own rows. Same result as attend per token up to the
-    fp32 summation order. q [T, H, 576] bf16, pool Row656 rows, idx [T, K] int32 -> (out [T, H, 512] bf16, lse)."""
+    fp32 summation order. q [T, H, 576] bf16, pool Row656 rows, idx [T, K] int32 -> (out [T, H, 512] bf16, lse).
+    With cu, max_query_len is the host-known largest request (at most 6)."""
     T, H, _ = q.shape
     _need(attention_ok(q, idx), "attend_packed: q must be bf16 [T, H, 576] with 16-byte aligned rows, idx int32")
     R = int(pool.shape[0])
     _need(cu is not None or (ql is not None and 0 < ql <= 6), "attend_packed: ql (1 .. 6) or cu")
-    u, mk, cnt = union if union is not None else mtp_union(idx, ql=ql, cu=cu, R=R)
+    u, mk, cnt = union if union is not None else mtp_union(idx, ql=ql, cu=cu, R=R, max_query_len=max_query_len)
     nreq, nmax = u.shape
     if tpg is None:
-        g = min(int(ql), 6) if cu is None else 6
+        g = min(int(ql), 6) if cu is None else min(int(max_query_len or 6), 6)
         tpg = 1 if g <= 1 else (2 if g <= 2 else (4 if g <= 4 else 8))
     if out is None:
         out = torch.empty(T, H, D_LAT, dtype=torch.bfloat16, device=q.device)

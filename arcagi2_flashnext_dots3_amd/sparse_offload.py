@@ -273,6 +273,8 @@ class LayerOffload:
             lse = torch.empty((T, H), dtype=torch.float32, device=q.device)
         if T == 0:
             return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+        if not torch.cuda.is_current_stream_capturing():    # the split merge's workspace, found by later captures
+            kernels.reserve_workspace(q.device, H)
         idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
         if self.packed and ql is not None and 1 < int(ql) <= 6 and T % int(ql) == 0:
             return self._attend_packed(q, idx, sm_scale, kv_scale, int(ql), out, lse, num_heads, return_lse)

@@ -121,3 +121,46 @@ def test_workspace_reuse_larger_counter_region(dev):
     bar = 2.0 ** -7 * o1.abs() + 2.0 ** -9 * o1.abs().amax(dim=-1, keepdim=True) + 1e-5
     assert bool(torch.isfinite(o).all()) and float(((o - o1).abs() - bar).max()) <= 0
     assert float((lse - l1).abs().max()) <= 1e-5
+
+
+def test_graph_capture_ascending_batches(dev):
+    """Two decode batches captured in ascending size without an explicit workspace (the serving path's calls): both
+    captures use the workspace reserved by an earlier eager call, so neither frees or swaps the other's buffer. Each
+    graph is replayed three times, alternating, with eager launches between the replays; every replay equals the
+    eager result bit for bit (same kernel, same split, same fixed merge order)."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    R, H, K = 4096, 128, 2048
+    pool = torch.from_numpy(make_pool_656(R, seed=61)[0]).to(dev)
+    sm = 192 ** -0.5
+    kernels.reserve_workspace(dev, H)
+    Ts = (4, 16)
+    assert all(kernels.auto_split(T, H, K) > 1 for T in Ts)
+    qs = [make_q(T, H, seed=62 + T).to(dev) for T in Ts]
+    ids = [distinct_idx(T, K, R, seed=63 + T).to(dev) for T in Ts]
+    print(f"[fused] graph capture of T={Ts} (splits {[kernels.auto_split(T, H, K) for T in Ts]})", flush=True)
+    eager = [kernels.attend(q, pool, i, sm) for q, i in zip(qs, ids)]
+    torch.cuda.synchronize()
+    graphs, outs = [], []
+    for q, i in zip(qs, ids):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            kernels.attend(q, pool, i, sm)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(kernels.attend(q, pool, i, sm))
+        torch.cuda.synchronize()
+        graphs.append(g)
+    for rep in range(3):
+        for n in (0, 1):
+            outs[n][0].fill_(7.0)
+            outs[n][1].fill_(7.0)
+            graphs[n].replay()
+            torch.cuda.synchronize()
+            assert torch.equal(outs[n][0], eager[n][0]), f"replay {rep} of T={Ts[n]}: output differs from eager"
+            assert torch.equal(outs[n][1], eager[n][1]), f"replay {rep} of T={Ts[n]}: lse differs from eager"
+            o, l = kernels.attend(qs[1 - n], pool, ids[1 - n], sm)       # eager work between the replays
+            torch.cuda.synchronize()
+            assert torch.equal(o, eager[1 - n][0]) and torch.equal(l, eager[1 - n][1])

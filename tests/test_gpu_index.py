@@ -121,8 +121,10 @@ def test_topk_ctx_lengths_fixture(dev):
 
 
 def test_logits_then_topk_end_to_end(dev):
-    """Indices bit-exact against the oracle's top-k of the GPU's own logits; against the fp64 oracle logits, the
-    selected sets agree wherever the gap at the k-th value exceeds the logits tolerance."""
+    """Indices bit-exact against the oracle's top-k of the GPU's own logits; against the fp64 oracle logits, on every
+    row, each position whose logit clears the k-th value by more than the logits tolerance is selected and none that
+    falls short of it by more is; rows whose gap at the k-th value exceeds the tolerance select exactly the oracle's
+    set (at least one such row is required)."""
     from arcagi2_flashnext_dots3_amd import kernels
     rows, L, bs = 4, 8192, 64
     nbp = L // bs
@@ -138,11 +140,19 @@ def test_logits_then_topk_end_to_end(dev):
     sel = kernels.topk(lg, ctx.to(dev), 2048).cpu().numpy()
     assert np.array_equal(sel, ref.topk(lg.cpu().numpy(), ctx.numpy(), 2048))
     exp = ref.index_logits(q.float().numpy(), w.numpy(), store, bt.numpy(), bs, req.numpy(), ctx.numpy(), L)
+    exact = 0
     for r in range(rows):
         srt = np.sort(exp[r])[::-1]
-        gap = srt[2047] - srt[2048]
-        if gap > 1e-5 * max(1.0, abs(srt[2047])) * 4:
-            assert set(sel[r].tolist()) == set(np.argsort(-exp[r], kind="stable")[:2048].tolist())
+        kth, tol = srt[2047], 4e-5 * max(1.0, abs(srt[2047]))
+        s = set(sel[r].tolist())
+        must, never = np.nonzero(exp[r] > kth + tol)[0], np.nonzero(exp[r] < kth - tol)[0]
+        assert len(must) >= 1900, f"row {r}: only {len(must)} positions clear the k-th value"
+        assert set(must.tolist()) <= s and not (set(never.tolist()) & s), f"row {r}: selection off the oracle's order"
+        if srt[2047] - srt[2048] > tol:
+            assert s == set(np.argsort(-exp[r], kind="stable")[:2048].tolist())
+            exact += 1
+    print(f"[index] end to end: {exact} of {rows} rows with a clear gap matched the oracle's set", flush=True)
+    assert exact >= 1
 
 
 # ---- fp16 logits (the reference's ARC_SHARD_F16OUT buffer) and top-k over fp16 keys

@@ -43,14 +43,17 @@ def test_mtp_union_boundaries(dev):
     T, topk, R = 9, 256, 2000
     idx = np.stack([g.choice(R, topk, replace=False) for _ in range(T)]).astype(np.int32)
     cu = np.array([0, 2, 2, 8], dtype=np.int32)                        # an empty request; one of 6 tokens
-    u, mk, cnt = kernels.mtp_union(torch.from_numpy(idx).to(dev), cu=torch.from_numpy(cu).to(dev), R=R)
+    u, mk, cnt = kernels.mtp_union(torch.from_numpy(idx).to(dev), cu=torch.from_numpy(cu).to(dev), R=R,
+                                   max_query_len=6)
     torch.cuda.synchronize()
     eu, emk, ecnt = ref.mtp_union(idx, T, None, cu, 3, R, nmax=u.shape[1])
     assert np.array_equal(cnt.cpu().numpy(), ecnt) and np.array_equal(u.cpu().numpy(), eu)
-    # a request of 7 tokens is refused (the kernels take at most 6), not cut to its first 6
+    # a host-declared request of 7 tokens is refused (the kernels take at most 6), as is cu without its maximum
     with pytest.raises(ValueError, match="at most 6"):
         kernels.mtp_union(torch.from_numpy(idx).to(dev), cu=torch.tensor([0, 2, 9], dtype=torch.int32, device=dev),
-                          R=R)
+                          R=R, max_query_len=7)
+    with pytest.raises(ValueError, match="max_query_len"):
+        kernels.mtp_union(torch.from_numpy(idx).to(dev), cu=torch.from_numpy(cu).to(dev), R=R)
 
 
 def _mtp_inputs(B, ql, H, R, K, shared, seed):
@@ -105,7 +108,7 @@ def test_attend_packed_variable_requests(dev):
     pd = torch.from_numpy(pool).to(dev)
     out = torch.full((10, H, 512), 7.0, dtype=torch.bfloat16, device=dev)
     lse = torch.full((10, H), 7.0, dtype=torch.float32, device=dev)
-    kernels.attend_packed(q.to(dev), pd, idx.to(dev), sm, cu=cu.to(dev), out=out, lse=lse)
+    kernels.attend_packed(q.to(dev), pd, idx.to(dev), sm, cu=cu.to(dev), out=out, lse=lse, max_query_len=6)
     torch.cuda.synchronize()
     o_ref, l_ref = ref.attention(q.float().numpy(), pool, idx.numpy(), sm)
     o = out.float().cpu().numpy()
@@ -114,4 +117,4 @@ def test_attend_packed_variable_requests(dev):
     assert np.abs(l - l_ref).max() <= 1e-3
     with pytest.raises(ValueError, match="at most 6"):
         kernels.attend_packed(q.to(dev), pd, idx.to(dev), sm, cu=torch.tensor([0, 3, 10], dtype=torch.int32,
-                                                                               device=dev))
+                                                                               device=dev), max_query_len=7)

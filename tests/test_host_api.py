@@ -170,3 +170,44 @@ def test_topk_check_recall():
     # row 0: exact; row 1: reference {0, 1, 2, 4} (column 3 is -inf), got {0, 1, 2, 5}: 3 of 4
     assert abs(r - (1.0 + 0.75) / 2) < 1e-9 and chk.min_recall == 0.75
     assert lines and "mean recall=0.87500" in lines[0]
+
+
+def test_auto_split_respects_the_split_kernel_row_limit():
+    """auto_split never picks a split whose rows per split pass the split kernel's limit (2048 rows, whole tiles of
+    32): the unsplit head-group kernel takes any K."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    assert kernels.ATTN_SPLIT_ROWS == 2048
+    for T in (1, 2, 7, 23):
+        for K in (64, 256, 2048, 4096, 16384, 16385, 20000, 65536):
+            s = kernels.auto_split(T, 128, K)
+            assert 1 <= s <= 8
+            if s > 1:
+                assert -(-(-(-K // s)) // 32) * 32 <= kernels.ATTN_SPLIT_ROWS
+    assert kernels.auto_split(1, 128, 16384) == 8 and kernels.auto_split(1, 128, 16385) == 1
+    assert kernels.auto_split(1, 128, 20000) == 1
+    # below fused_max_tokens tokens auto_split may take the split merge (needs a workspace), never at or above it
+    for H in (16, 64, 128):
+        Tm = kernels.fused_max_tokens(H)
+        assert kernels.auto_split(Tm, H, 4096) > 1 and kernels.auto_split(Tm + 1, H, 4096) == 1
+
+
+def test_workspace_under_capture_reuses_the_eager_one(monkeypatch):
+    """Under HIP graph capture the workspace cache allocates nothing: it hands out the device's largest eager
+    workspace of the kind and raises when there is none or it is too small (a buffer allocated inside a capture holds
+    its contents only after the first replay). Grown buffers stay referenced, so captured graphs keep valid ones."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    monkeypatch.setattr(kernels, "_WS", {})
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    d0, d1 = torch.device("cuda:0"), torch.device("cuda:1")
+    with pytest.raises(ValueError, match="graph capture"):
+        kernels._workspace("attn", d0, 1000)
+    small, big, other = torch.empty(512, dtype=torch.uint8), torch.empty(4096, dtype=torch.uint8), \
+        torch.empty(1 << 20, dtype=torch.uint8)
+    kernels._WS[("attn", d0, 1)] = small
+    kernels._WS[("attn", d0, 2)] = big
+    kernels._WS[("attn", d1, 1)] = other          # another device's buffer is never used
+    kernels._WS[("topk", d0, 1)] = other          # nor another kind's
+    b, key = kernels._workspace("attn", d0, 1000)
+    assert b is big and key is None
+    with pytest.raises(ValueError, match="graph capture"):
+        kernels._workspace("attn", d0, 5000)
