@@ -46,6 +46,7 @@ SIGNATURES = {
     "spmla_wcache_split": [P, LL, I, I, P, I, P, P, LL, P, P, LL, P, P],
     "spmla_compact_stage": [P, I, P, LL, I, I, P, P, P, P, LL, P],
     "spmla_attn_splitk": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, I, P, LL, LL, P, LL, P, P, P],
+    "spmla_attn576": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, I, P, LL, LL, P, LL, P, P, P],
     "spmla_attn": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, I, P, LL, LL, P, LL, P, LL, P],
     "spmla_attn_ws_bytes": [I, I, I],
     "spmla_attn_merge": [P, LL, LL, P, LL, P, LL, I, P, I, I, F, F, P, LL, LL, P, LL, P, LL, LL, P, LL, P],

@@ -906,7 +906,7 @@ int launch_tokens(const void* q, long long q_st, long long q_sh, const void* poo
                   long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale, int S,
                   void* out, long long o_st, long long o_sh, float* lse, long long lse_st, float* opart,
                   float* lsepart, const float* prior_o, long long po_st, long long po_sh, const float* prior_lse,
-                  long long pl_st, void* stream);
+                  long long pl_st, void* stream, bool r576);
 }  // namespace pk
 }  // namespace spmla
 
@@ -937,7 +937,8 @@ static int attn_launch(const void* q, long long q_st, long long q_sh, const void
   const bool kfit = ((K + S - 1) / S + attn::TR - 1) / attn::TR * attn::TR <= attn::KMAX;
   if (!fused && (!kfit || (long long)T * S * ((H + 31) / 32) <= attn::HG_TOKENS_MAX))
     return pk::launch_tokens(q, q_st, q_sh, pool, R, idx, idx_st, K, kcount, T, H, sm_scale, kv_scale, S, out, o_st,
-                             o_sh, lse, lse_st, opart, lsepart, prior_o, po_st, po_sh, prior_lse, pl_st, stream);
+                             o_sh, lse, lse_st, opart, lsepart, prior_o, po_st, po_sh, prior_lse, pl_st, stream,
+                             false);
   if (!kfit) return SPMLA_ELIMIT;
   attn::Params p;
   p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh;
@@ -991,6 +992,23 @@ int spmla_attn(const void* q, long long q_st, long long q_sh, const void* pool, 
                void* stream) {
   return attn_launch(q, q_st, q_sh, pool, R, idx, idx_st, K, kcount, T, H, sm_scale, kv_scale, S, out, o_st, o_sh, lse,
                      lse_st, nullptr, nullptr, nullptr, 0, 0, nullptr, 0, S > 1 ? ws : nullptr, ws_bytes, stream);
+}
+
+int spmla_attn576(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
+                  long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale, int S,
+                  void* out, long long o_st, long long o_sh, float* lse, long long lse_st, float* opart,
+                  float* lsepart, void* stream) {
+  if (T < 0 || H <= 0 || K < 0 || S <= 0 || R < 0) return SPMLA_EARG;
+  if (T == 0) return SPMLA_OK;
+  if (!q || !idx || (R > 0 && !pool)) return SPMLA_EARG;
+  const bool f32part = opart != nullptr;
+  if (f32part ? !lsepart : (S != 1 || !out || !lse)) return SPMLA_EARG;
+  if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)pool & 15)) return SPMLA_EALIGN;
+  if (out && (((uintptr_t)out & 7) || (o_st & 3) || (o_sh & 3))) return SPMLA_EALIGN;
+  if (f32part && ((uintptr_t)opart & 15)) return SPMLA_EALIGN;
+  return pk::launch_tokens(q, q_st, q_sh, pool, R, idx, idx_st, K, kcount, T, H, sm_scale, kv_scale, S, out, o_st,
+                           o_sh, lse, lse_st, f32part ? opart : nullptr, lsepart, nullptr, 0, 0, nullptr, 0, stream,
+                           true);
 }
 
 int spmla_attn_merge(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,

@@ -7,10 +7,14 @@
 //     item = request, columns = tokens x heads; a column's softmax keeps only the rows its token selected (per-row
 //     token masks, ballots). Reference: dotsnote/engine/arcstats_pkg/arcstats/csrc/offload_attn.cu:700-1153
 //     (pk_attn_kernel).
+//   * attn_kernel<false, true>, the same decode over Row576 rows (spmla_attn576: 512 + 64 e4m3 codes, one
+//     per-tensor kv_scale): no per-group scales, so the latent MFMAs run as one chain into S (no scale combine), P'
+//     is P itself in f16 for every group, and the rope codes are widened to bf16 (exact) in registers.
 //
 // Math (reference: dotsnote/kaggle/runtime_dataset/bench_offload_attn2.py:77-93 and
 // dotsnote/engine/vllm_patch/vllm/v1/attention/ops/xpu_mla_sparse.py:77-161):
-//   latent_d = e4m3(code_d) * scale[d / 128], rope bf16; s = sm_scale * kv_scale * (q . row) (fp32);
+//   latent_d = e4m3(code_d) * scale[d / 128], rope bf16 (Row576: latent_d = e4m3(code_d), rope e4m3, no scales);
+//   s = sm_scale * kv_scale * (q . row) (fp32);
 //   p = exp2(s * log2e - m), o = kv_scale * sum p latent / sum p, lse = ln sum exp(s).
 //
 // gfx950 mapping (per wave): S^T (32 rows x 32 columns) on bf16 MFMA (32x32x16) with the codes converted exactly to
@@ -112,7 +116,7 @@ __device__ inline void scale_acc(f32x16 (&O)[16], float a) {
 
 struct Params {
   const uint16_t* q; long long q_st, q_sh;        // q[t][h][576] bf16 (last dim contiguous)
-  const uint8_t* pool; long long R;               // Row656 rows
+  const uint8_t* pool; long long R;               // Row656 rows (Row576 in attn_kernel<false, true>)
   const int* idx; long long idx_st; int K;        // idx[t][k]
   const int* kcount;                              // optional per-token count of leading valid entries
   int T, H, S, HGN;                               // tokens, heads, splits, head groups
@@ -134,8 +138,10 @@ struct Params {
 // Source of invalid and padding rows: zero codes, zero scales, zero rope (their P is 0, and 0 * 0 stays 0 in PV).
 __device__ __attribute__((aligned(16))) uint8_t zero_row[ROW656];
 
-template <bool PK>
+template <bool PK, bool R5 = false>
 __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
+  constexpr int RB = R5 ? ROW576 : ROW656;      // row bytes
+  constexpr int NRP = R5 ? 2 : 4;               // 16-byte rope pieces per lane: e4m3 (32 B) or bf16 (64 B)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_generic[];
   SPMLA_LDS uint8_t* lds = (SPMLA_LDS uint8_t*)smem_generic;
 
@@ -214,15 +220,24 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   }
   const int ntw = ntile > w ? (ntile - w + NW - 1) / NW : 0;   // tiles w, w + 4, ...
   SPMLA_LDS uint8_t* mybuf = lds + L_TILES + w * NBUF * TILE;
-  u32x4 rp[4];
+  // rope of this lane's row: Row656, dims 16 ks + 8 half .. + 7 of MFMA ks (bf16); Row576, the 32 e4m3 codes of
+  // dims 32 half .. 32 half + 31, MFMA ks taking dims 32 half + 8 ks .. + 7 (the query rope is read to match)
+  u32x4 rp[NRP];
+  auto load_rope = [&](const uint8_t* src) {
+#pragma unroll
+    for (int ks = 0; ks < NRP; ++ks)
+      rp[ks] = R5 ? *(const u32x4*)(src + D_LAT + 32 * half + 16 * ks)
+                  : *(const u32x4*)(src + ROPE_OFF + ks * 32 + half * 16);
+  };
   if (ntw > 0) {
-    const uint8_t* src = rcur >= 0 ? p.pool + (long long)rcur * ROW656 : zero_row;
+    const uint8_t* src = rcur >= 0 ? p.pool + (long long)rcur * RB : zero_row;
 #pragma unroll
     for (int i = 0; i < 16; ++i) dma16(src + (2 * i + half) * 16, mybuf + i * 1024);
-    dma4(src + SC_OFF + half * 4, mybuf + T_SCT);
-    dma4(src + SC_OFF + (2 + half) * 4, mybuf + T_SCT + 256);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(src + ROPE_OFF + ks * 32 + half * 16);
+    if constexpr (!R5) {
+      dma4(src + SC_OFF + half * 4, mybuf + T_SCT);
+      dma4(src + SC_OFF + (2 + half) * 4, mybuf + T_SCT + 256);
+    }
+    load_rope(src);
   }
   // latent query fragments of groups 0, 1 (bf16 B operands), k-pair kp (32 dims = chunks 2kp, 2kp + 1): lane half
   // h holds the dims of chunk 2kp + h; MFMA 2kp + e uses its bytes 8e .. 8e + 7 (the K operand is read the same
@@ -266,7 +281,8 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     // ---- first LDS reads of the tile: query rope, K group 0, the row ids of this and of the next tile
     u32x4 qr[4], kr[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qr[ks] = *(SPMLA_LDS u32x4*)(qrope + l32 * QRS + (16 * ks + 8 * half) * 2);
+    for (int ks = 0; ks < 4; ++ks)
+      qr[ks] = *(SPMLA_LDS u32x4*)(qrope + l32 * QRS + (R5 ? 32 * half + 8 * ks : 16 * ks + 8 * half) * 2);
 #pragma unroll
     for (int kq = 0; kq < 4; ++kq) kr[kq] = *(SPMLA_LDS u32x4*)(tb + (2 * kq + half) * 512 + l32 * 16);
     const bool more = j + 1 < ntw;
@@ -281,12 +297,23 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     f32x16 S;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 a = __builtin_bit_cast(bf16x8, rp[ks]), b = __builtin_bit_cast(bf16x8, qr[ks]);
-      S = ks == 0 ? qk_first(a, b) : (ks == 3 ? qk_last(a, b, S) : qk_next(a, b, S));
+      bf16x8 a;
+      if constexpr (R5) {                          // 8 e4m3 rope codes -> bf16 (exact)
+        const uint32_t w0 = rp[ks >> 1][2 * (ks & 1)], w1 = rp[ks >> 1][2 * (ks & 1) + 1];
+        i32x4 x;
+        x[0] = (int)fp8lo_bf16x2(w0); x[1] = (int)fp8hi_bf16x2(w0);
+        x[2] = (int)fp8lo_bf16x2(w1); x[3] = (int)fp8hi_bf16x2(w1);
+        a = __builtin_bit_cast(bf16x8, x);
+      } else {
+        a = __builtin_bit_cast(bf16x8, rp[ks]);
+      }
+      const bf16x8 b = __builtin_bit_cast(bf16x8, qr[ks]);
+      // Row576: the chain goes on through the latent groups (no scales to combine)
+      S = ks == 0 ? qk_first(a, b) : ((ks == 3 && !R5) ? qk_last(a, b, S) : qk_next(a, b, S));
     }
     const unsigned vmask = (unsigned)__ballot(rcur >= 0);  // rows of the tile that exist
     // the next tile's copy is issued in four parts, one per latent group, between that group's MFMAs
-    const uint8_t* nsrc = rnxt >= 0 ? p.pool + (long long)rnxt * ROW656 : zero_row;
+    const uint8_t* nsrc = rnxt >= 0 ? p.pool + (long long)rnxt * RB : zero_row;
     SPMLA_LDS uint8_t* nbuf = mybuf + ((j + 1) & 1) * TILE;
 
     // ---- latent part of S^T: group g = chunks 8g .. 8g + 7; group g + 1's K is read while group g's MFMAs run
@@ -301,10 +328,11 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
 #pragma unroll
         for (int i = 4 * g; i < 4 * g + 4; ++i) dma16(nsrc + (2 * i + half) * 16, nbuf + i * 1024);
         if (g == 3) {
-          dma4(nsrc + SC_OFF + half * 4, nbuf + T_SCT);
-          dma4(nsrc + SC_OFF + (2 + half) * 4, nbuf + T_SCT + 256);
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) rp[ks] = *(const u32x4*)(nsrc + ROPE_OFF + ks * 32 + half * 16);
+          if constexpr (!R5) {
+            dma4(nsrc + SC_OFF + half * 4, nbuf + T_SCT);
+            dma4(nsrc + SC_OFF + (2 + half) * 4, nbuf + T_SCT + 256);
+          }
+          load_rope(nsrc);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -327,14 +355,22 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
           b0 = __builtin_bit_cast(bf16x8, *(const SPMLA_LDS u32x4*)qp);
           b1 = __builtin_bit_cast(bf16x8, *(const SPMLA_LDS u32x4*)(qp + 16));
         }
-        acc = kq == 0 ? qk_first(__builtin_bit_cast(bf16x8, a0), b0) : qk_next(__builtin_bit_cast(bf16x8, a0), b0, acc);
-        acc = kq == 3 ? qk_last(__builtin_bit_cast(bf16x8, a1), b1, acc) : qk_next(__builtin_bit_cast(bf16x8, a1), b1, acc);
+        if constexpr (R5) {
+          S = qk_next(__builtin_bit_cast(bf16x8, a0), b0, S);
+          S = (g == 3 && kq == 3) ? qk_last(__builtin_bit_cast(bf16x8, a1), b1, S)
+                                  : qk_next(__builtin_bit_cast(bf16x8, a1), b1, S);
+        } else {
+          acc = kq == 0 ? qk_first(__builtin_bit_cast(bf16x8, a0), b0) : qk_next(__builtin_bit_cast(bf16x8, a0), b0, acc);
+          acc = kq == 3 ? qk_last(__builtin_bit_cast(bf16x8, a1), b1, acc) : qk_next(__builtin_bit_cast(bf16x8, a1), b1, acc);
+        }
       }
+      if constexpr (!R5) {
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x4 sg = *(SPMLA_LDS f32x4*)(tb + T_SCT + (g * 32 + 8 * qd + 4 * half) * 4);
+        for (int qd = 0; qd < 4; ++qd) {
+          const f32x4 sg = *(SPMLA_LDS f32x4*)(tb + T_SCT + (g * 32 + 8 * qd + 4 * half) * 4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S[4 * qd + e] = __builtin_fmaf(acc[4 * qd + e], sg[e], S[4 * qd + e]);
+          for (int e = 0; e < 4; ++e) S[4 * qd + e] = __builtin_fmaf(acc[4 * qd + e], sg[e], S[4 * qd + e]);
+        }
       }
       if (g < 3) {
 #pragma unroll
@@ -346,9 +382,12 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     f32x4 ps[4];
     i32x2 tv[8];
     // 2 of the tile's 128 scales ([group][row]) per lane, for the range check of P' below
-    const f32x2 sc2 = *(SPMLA_LDS f32x2*)(tb + T_SCT + lane * 8);
+    f32x2 sc2 = {};
+    if constexpr (!R5) {
+      sc2 = *(SPMLA_LDS f32x2*)(tb + T_SCT + lane * 8);
 #pragma unroll
-    for (int qd = 0; qd < 4; ++qd) ps[qd] = *(SPMLA_LDS f32x4*)(tb + T_SCT + (8 * qd + 4 * half) * 4);
+      for (int qd = 0; qd < 4; ++qd) ps[qd] = *(SPMLA_LDS f32x4*)(tb + T_SCT + (8 * qd + 4 * half) * 4);
+    }
 #pragma unroll
     for (int f8 = 0; f8 < 8; ++f8)
       tv[f8] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((SPMLA_LDS i32x2*)(tb + (f8 >> 1) * 1024 + (f8 & 1) * 256 + tr_off));
@@ -389,7 +428,7 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     // that P' < 2^TAU * 2^9 = 2^15 while every row scale of the tile is below 2^(9 + eps). eps is set by the first
     // tile with a positive scale and rises (an exact power-of-two rescale of O and l_run) when a
     // later tile's largest such scale passes 2^(9 + eps) -- rare: scales sit near amax / 448 of their rows.
-    if (__ballot(fmaxf(sc2[0], sc2[1]) > elim)) {     // (a missing row's scales are the zero row's)
+    if (!R5 && __ballot(fmaxf(sc2[0], sc2[1]) > elim)) {     // (a missing row's scales are the zero row's)
       float wm = fmaxf(sc2[0], sc2[1]);
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) wm = fmaxf(wm, __shfl_xor(wm, o, 64));
@@ -429,14 +468,28 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
       }
     };
     f16x8 pb[2];
-    p_scaled(ps, pb);
+    if constexpr (R5) {                                  // P' = P (P <= 2^TAU), the same for every group
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float* pp = P + 8 * ks;
+        i32x4 o;
+        o[0] = (int)pk_f16(pp[0], pp[1]); o[1] = (int)pk_f16(pp[2], pp[3]);
+        o[2] = (int)pk_f16(pp[4], pp[5]); o[3] = (int)pk_f16(pp[6], pp[7]);
+        pb[ks] = __builtin_bit_cast(f16x8, o);
+      }
+    } else {
+      p_scaled(ps, pb);
+    }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       f32x4 pn[4];
       i32x2 vn[8];
       if (g < 3) {
+        if constexpr (!R5) {
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) pn[qd] = *(SPMLA_LDS f32x4*)(tb + T_SCT + ((g + 1) * 32 + 8 * qd + 4 * half) * 4);
+          for (int qd = 0; qd < 4; ++qd)
+            pn[qd] = *(SPMLA_LDS f32x4*)(tb + T_SCT + ((g + 1) * 32 + 8 * qd + 4 * half) * 4);
+        }
 #pragma unroll
         for (int f8 = 0; f8 < 8; ++f8)
           vn[f8] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
@@ -452,11 +505,13 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
         a[0] = (int)fp8lo_f16x2((uint32_t)raw[0]); a[1] = (int)fp8hi_f16x2((uint32_t)raw[0]);
         a[2] = (int)fp8lo_f16x2((uint32_t)raw[1]); a[3] = (int)fp8hi_f16x2((uint32_t)raw[1]);
         O[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), pb[ks], O[mt], 0, 0, 0);
-        if (f8 == 3 && g < 3) p_scaled(pn, pbn);          // next group's P', behind four MFMAs
+        if (!R5 && f8 == 3 && g < 3) p_scaled(pn, pbn);  // next group's P', behind four MFMAs
       }
       if (g < 3) {
-        pb[0] = pbn[0];
-        pb[1] = pbn[1];
+        if constexpr (!R5) {
+          pb[0] = pbn[0];
+          pb[1] = pbn[1];
+        }
 #pragma unroll
         for (int f8 = 0; f8 < 8; ++f8) tv[f8] = vn[f8];
       }
@@ -558,14 +613,15 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   }
 }
 
-// Per-token launch of attn_kernel<false>: the arguments of spmla_attn_splitk / spmla_attn_merge, already checked by
-// the caller (spmla_attn.hip, which chooses this kernel for launches with few tokens). Any K: row ids are read from
-// global memory a tile ahead, not staged.
+// Per-token launch of attn_kernel<false> (r576: attn_kernel<false, true> over Row576 rows): the arguments of
+// spmla_attn_splitk / spmla_attn_merge / spmla_attn576, already checked by the caller (spmla_attn.hip, which chooses
+// this kernel for launches with few tokens, and for every Row576 launch). Any K: row ids are read from global memory
+// a tile ahead, not staged.
 int launch_tokens(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
                   long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale, int S,
                   void* out, long long o_st, long long o_sh, float* lse, long long lse_st, float* opart,
                   float* lsepart, const float* prior_o, long long po_st, long long po_sh, const float* prior_lse,
-                  long long pl_st, void* stream) {
+                  long long pl_st, void* stream, bool r576) {
   Params p;
   p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh;
   p.pool = (const uint8_t*)pool; p.R = R;
@@ -580,9 +636,15 @@ int launch_tokens(const void* q, long long q_st, long long q_sh, const void* poo
   const long long nwork = (long long)T * S * p.HGN;
   if (nwork > (1ll << 30)) return SPMLA_ELIMIT;
   const int grid = (int)((nwork + 7) / 8 * 8);
-  static DynLds lds_attr;
-  if (const int e = lds_attr.ensure((const void*)attn_kernel<false>, L_TOTAL)) return e;
-  hipLaunchKernelGGL(attn_kernel<false>, dim3(grid), dim3(256), L_TOTAL, (hipStream_t)stream, p);
+  if (r576) {
+    static DynLds lds_attr5;
+    if (const int e = lds_attr5.ensure((const void*)attn_kernel<false, true>, L_TOTAL)) return e;
+    hipLaunchKernelGGL((attn_kernel<false, true>), dim3(grid), dim3(256), L_TOTAL, (hipStream_t)stream, p);
+  } else {
+    static DynLds lds_attr;
+    if (const int e = lds_attr.ensure((const void*)attn_kernel<false>, L_TOTAL)) return e;
+    hipLaunchKernelGGL(attn_kernel<false>, dim3(grid), dim3(256), L_TOTAL, (hipStream_t)stream, p);
+  }
   return (int)hipGetLastError();
 }
 

@@ -566,21 +566,37 @@ def auto_split(T, H, K, cus=256):
     return s
 
 
+def auto_split576(T, H, K, cus=256):
+    """Row splits per token of a Row576 launch (one kernel, 32 heads per workgroup; split partials in fp32, merged by
+    spmla_lse_merge): doubled while the launch has fewer than cus * 3 / 8 workgroups and every split keeps at least
+    8 tiles of 32 rows (at most 8 splits)."""
+    n = T * ((H + 31) // 32)
+    s = 1
+    while s < 8 and n * s * 8 < cus * 3 and K >= 2 * s * 256:
+        s *= 2
+    return s
+
+
 def attn_ws_bytes(T, H, split):
     """Bytes of the workspace attend needs for T tokens, H heads and `split` splits (0 for split 1)."""
     return int(_lib.lib().spmla_attn_ws_bytes(T, H, split))
 
 
-def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None, kcount=None, ws=None, R=None):
+def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None, kcount=None, ws=None, R=None,
+           row_bytes=None):
     """q [T, H, 576] bf16, pool [R, 656] uint8 Row656 rows (or a mapped host address with R given), idx [T, K]
-    int32 rows -> (out [T, H, 512] bf16, lse [T, H] fp32). split > 1 (at most 8) cuts K into partials that the
+    int32 rows -> (out [T, H, 512] bf16, lse [T, H] fp32). Row576 rows (pool [..., 576], or row_bytes=576: the
+    per-tensor fp8 cache, every code times kv_scale) go to spmla_attn576, whose splits merge through fp32 partials
+    (split None: auto_split576). For Row656, split > 1 (at most 8) cuts K into partials that the
     kernel merges (spmla_attn; ws: a uint8 workspace of attn_ws_bytes whose leading counter bytes are zero -- the
     kernel leaves them so --, else a cached one per stream; under HIP graph capture either ws or a workspace reserved
     by an earlier eager call, see reserve_workspace); None: auto_split."""
     T, H, _ = q.shape
     K = idx.shape[1]
+    rb = int(row_bytes) if row_bytes is not None else (int(pool.shape[-1]) if torch.is_tensor(pool) else ROW656)
+    _need(rb in (ROW656, ROW576), "attend: Row656 or Row576 rows")
     if split is None:
-        split = auto_split(T, H, K)
+        split = auto_split576(T, H, K) if rb == ROW576 else auto_split(T, H, K)
     _need(attention_ok(q, idx), "attend: q must be bf16 [T, H, 576] with 16-byte aligned rows, idx int32")
     if out is None:
         out = torch.empty(T, H, D_LAT, dtype=torch.bfloat16, device=q.device)
@@ -589,6 +605,19 @@ def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None,
     Rv = int(R if R is not None else pool.shape[0])
     pptr = pool.data_ptr() if torch.is_tensor(pool) else int(pool)
     st = _stream(q)
+    if rb == ROW576:
+        _need(1 <= split <= 8, "attend: split must be 1 .. 8")
+        if split == 1:
+            _lib.call("spmla_attn576", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(),
+                      idx.stride(0), K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), 1, out.data_ptr(),
+                      out.stride(0), out.stride(1), lse.data_ptr(), lse.stride(0), None, None, st)
+            return out, lse
+        opart = torch.empty(split, T, H, D_LAT, dtype=torch.float32, device=q.device)
+        lpart = torch.empty(split, T, H, dtype=torch.float32, device=q.device)
+        _lib.call("spmla_attn576", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(), idx.stride(0),
+                  K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), split, None, 0, 0, None, 0,
+                  opart.data_ptr(), lpart.data_ptr(), st)
+        return lse_merge(opart, lpart, out=out, lse=lse)
     if split == 1:
         _lib.call("spmla_attn_splitk", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(),
                   idx.stride(0), K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), 1, out.data_ptr(),

@@ -103,7 +103,7 @@ def _line(metric, value, unit, a, ms, dtype, config, roofline, cpu=None, hib=Tru
 
 def _cache_fill(pool_u8, nrows, seed, dev, fmt=0):
     """Rows 0..nrows of pool_u8 (device or pinned host) written from seeded N(0,1) bf16 latents / ropes by the
-    library's cache-write kernel (fmt 0 = Row656, 2 = compact Row400 with kv_scale 1)."""
+    library's cache-write kernel (fmt 0 = Row656, 1 = Row576 and 2 = compact Row400, both with kv_scale 1)."""
     import torch
     from arcagi2_flashnext_dots3_amd import kernels
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -208,7 +208,33 @@ def run_config2(a, dev):
         res["cpu_baseline"] = _with_model(cpu_baseline(pool, q, idxs[0]))
     del pool
     torch.cuda.empty_cache()
+    if not a.no_variant:
+        res["row576_variant"] = run_row576(a, dev, q, idxs, out, lse)
     return res
+
+
+def run_row576(a, dev, q, idxs, out, lse):
+    """Config 2's step over the plugin's per-tensor fp8 cache (Row576 rows: 512 + 64 e4m3 codes, kv_scale 1, written
+    by the library from the same seeded latents), attended in place by spmla_attn576; timed like the main line."""
+    import torch
+    from arcagi2_flashnext_dots3_amd import kernels
+    R = B * CTX
+    pool = torch.empty(R, 576, dtype=torch.uint8, device=dev)
+    _cache_fill(pool, R, 1, dev, fmt=1)
+    n = len(idxs)
+    replay = _graphed(lambda: [kernels.attend(q, pool, idxs[i], SM_SCALE, out=out, lse=lse, split=1)
+                               for i in range(n)], 1)
+    _settle(replay)
+    ms = _timed(replay, max(1, a.steps // n), max(1, a.warmup // n)) / n
+    alg = ALG_BYTES - B * K * (ROWB - 576)
+    gbs = alg / (ms * 1e-3) / 1e9
+    del pool
+    torch.cuda.empty_cache()
+    return {"step_us": round(ms * 1e3, 2), "gbs": round(gbs, 2), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "alg_bytes_per_launch": alg, "kernel": "spmla::pk::attn_kernel<false, true>",
+            "mfma_tflops": round(ALG_FLOPS / (ms * 1e-3) / 1e12, 2),
+            "workload": "config 2 (B=64, H=128, top-2048 of 32768 rows per sequence) over Row576 rows (the plugin's "
+                        "fp8 cache: 576 B/row, per-tensor scale), one launch per step from a HIP graph"}
 
 
 # ------------------------------------------------------------------------------------------------ config 3

@@ -272,6 +272,17 @@ int spmla_attn_splitk(const void* q, long long q_st, long long q_sh, const void*
                       float kv_scale, int S, void* out, long long o_st, long long o_sh, float* lse,
                       long long lse_st, float* opart, float* lsepart, void* stream);
 
+/* spmla_attn_splitk over Row576 rows, the plugin's per-tensor "fp8" cache: pool [R] rows of 512 latent + 64 rope
+ * e4m3 codes (no per-group scales), every code times the tensor's kv_scale. Same arguments, outputs and results
+ * (o = kv_scale * softmax(s) codes_latent, s = sm_scale * kv_scale * q . codes); S > 1 needs opart / lsepart (the
+ * fp32 partials for spmla_lse_merge). Any K; one kernel (32 heads per workgroup) serves every launch.
+ * Replaces triton_bf16_mla_sparse_interface over the fp8 per-tensor rows (PortableSparseImpl._run,
+ * dotsnote/engine/arcstats_pkg/arcstats/dsa_sm89.py:379-391, kernel vllm_patch/.../ops/xpu_mla_sparse.py:77-161). */
+int spmla_attn576(const void* q, long long q_st, long long q_sh, const void* pool, long long R, const int* idx,
+                  long long idx_st, int K, const int* kcount, int T, int H, float sm_scale, float kv_scale, int S,
+                  void* out, long long o_st, long long o_sh, float* lse, long long lse_st, float* opart,
+                  float* lsepart, void* stream);
+
 /* Bytes of the workspace spmla_attn needs for T tokens, H heads and S splits (0 for S = 1; -1 for bad sizes). */
 long long spmla_attn_ws_bytes(int T, int H, int S);
 

@@ -23,6 +23,18 @@ def make_pool_656(R, seed=1, scale=1.0, device=None):
     return pool, kv, pe
 
 
+def make_pool_576(R, seed=1, scale=1.0, kv_scale=1.0):
+    """R Row576 rows (the per-tensor fp8 cache) from N(0, scale^2) latent / rope, written by the oracle's writer with
+    kv_scale. Returns pool uint8 numpy [R, 576]."""
+    from oracle import spmla_ref as ref
+    g = torch.Generator().manual_seed(seed)
+    kv = bf16_bits(torch.randn(R, D_LAT, generator=g) * scale)
+    pe = bf16_bits(torch.randn(R, D_ROPE, generator=g) * scale)
+    pool = np.zeros((R, D_QK), dtype=np.uint8)
+    ref.cache_write_576(kv, pe, np.arange(R), pool, kv_scale)
+    return pool
+
+
 def make_q(T, H, seed=0, scale=1.0):
     g = torch.Generator().manual_seed(seed)
     return (torch.randn(T, H, D_QK, generator=g) * scale).to(torch.bfloat16)

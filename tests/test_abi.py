@@ -109,6 +109,13 @@ def test_version():
     # logits: local rows times P beyond 32-bit row arithmetic (R_local = INT_MAX / 4 + 1 with P = 4)
     (("spmla_index_logits", 256, 64, 128, 256, 64, 256, (2 ** 31 - 1) // 4 + 1, 16, 2112, 256, 8, 64, 256, 256, 1,
       64, 128, 64, 4, 0, 0, 256, 64, 0, None), -5),
+    # Row576 attention: S > 1 needs the fp32 partials; q rows 16-byte aligned; H > 0
+    (("spmla_attn576", 256, 576, 576, 256, 100, 256, 8, 8, None, 1, 1, 1.0, 1.0, 2, 256, 512, 512, 256, 1, None, None,
+      None), -2),
+    (("spmla_attn576", 264, 576, 576, 256, 100, 256, 8, 8, None, 1, 1, 1.0, 1.0, 1, 256, 512, 512, 256, 1, None, None,
+      None), -3),
+    (("spmla_attn576", 256, 576, 576, 256, 100, 256, 8, 8, None, 1, 0, 1.0, 1.0, 1, 256, 512, 512, 256, 1, None, None,
+      None), -2),
     # the in-kernel split merge: a workspace is required, at most 8 splits
     (("spmla_attn", 256, 64, 64, 256, 100, 256, 8, 8, None, 1, 1, 1.0, 1.0, 4, 256, 512, 512, 256, 1, None, 0, None),
      -2),

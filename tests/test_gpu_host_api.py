@@ -376,9 +376,9 @@ def test_portable_impl_offload_decode_and_prefill(dev):
 
 def test_portable_impl_paged_decode_row576(dev):
     """The reference's deployed cache: 576-byte per-tensor fp8 rows ("fp8", dsa_sm89.py:551-562) written with a
-    k_scale and attended with the layer's _k_scale_float (dsa_sm89.py:379-391), against the fp64 oracle over the same
-    Row576 rows; the Row576 -> Row656 staging gather byte-checked (codes as stored, scales 1.0, rope widened: torch's
-    float8_e4m3fn -> bfloat16 conversion)."""
+    k_scale and attended in place with the layer's _k_scale_float (dsa_sm89.py:379-391), against the fp64 oracle over
+    the same Row576 rows; the Row576 -> Row656 gather (kernels.row576_gather) byte-checked too (codes as stored,
+    scales 1.0, rope widened: torch's float8_e4m3fn -> bfloat16 conversion)."""
     from types import SimpleNamespace
     from arcagi2_flashnext_dots3_amd import kernels
     from arcagi2_flashnext_dots3_amd.dsa import CommonAttentionMetadata, PortableSparseBackend
