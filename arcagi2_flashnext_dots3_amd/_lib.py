@@ -36,11 +36,12 @@ SIGNATURES = {
     "spmla_row576_gather": [P, LL, P, I, P, LL, P],
     "spmla_row400_copy": [P, LL, P, P, LL, P, I, I, P],
     "spmla_row400_gather_tiers": [P, LL, P, LL, P, I, I, P, LL, I, P],
+    "spmla_row400_decode_tiers": [P, LL, P, LL, P, I, I, P, LL, I, P],
     "spmla_tier_split": [P, LL, I, I, P, LL, P, LL, P, P, LL, P, P],
     "spmla_wcache_step": [P, LL, I, I, LL, P, I, I, P, P, P, P, P, P, P, P, I, I, P, LL, P],
     "spmla_wcache_place": [P, LL, I, I, LL, P, I, I, P, P, P, P, P, P, P, P, I, I, P],
     "spmla_wcache_resolve": [P, LL, I, I, LL, P, I, I, P, P, P, P, P, P, P, P, I, I, P, LL, P],
-    "spmla_wcache_fill": [P, LL, I, P, P, P, I, P, LL, P],
+    "spmla_wcache_fill": [P, LL, I, I, P, P, P, I, P, LL, P],
     "spmla_wcache_invalidate": [P, I, LL, P, I, I, I, P],
     "spmla_split_res": [P, LL, P, LL, I, I, P, LL, P, P, LL, P, P],
     "spmla_wcache_split": [P, LL, I, I, P, I, P, P, LL, P, P, LL, P, P],

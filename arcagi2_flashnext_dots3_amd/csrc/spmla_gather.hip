@@ -405,6 +405,107 @@ __global__ void remap_kernel(const int* sidx, long long s_st, int M, int K, int 
   sidx2[(long long)m * s2_st + k] = (p >= 0 && p < tot) ? (int)rank_of(bits, woff, p) : -1;
 }
 
+// ---- Row400 -> GPU rows from HBM, 16 lanes per row: lane q of a row's group decodes latent block q (32 values, one
+// block exponent k), so a row's decode is spread over 16 lanes and a wave decodes 4 rows at once; every thread
+// decodes one block, and the grid covers all rows (occupancy, not a per-wave pipeline, hides the memory latency).
+// For -4 <= k <= 6 (every block the writer produces from values up to 448 with amax / 7 >= 2^-5) the e4m3 code of
+// magnitude nibble m is a byte table T_k[m]: 0, (k + 5) << 3, (k + 6) << 3, ((k + 6) << 3) | 4 for m = 0 .. 3 (the
+// e2m2 subnormals) and (m << 1) + ((k + 6) << 3) for m >= 4 (exponent and 2 mantissa bits moved over); the lookup of
+// 4 nibbles takes two v_perm_b32 over the 16-byte table and a byte select. Other blocks go through e2m2_to_e4m3 per
+// value. The sign bit is ORed in after (-0 -> 0x80, as e2m2_to_e4m3).
+__device__ inline uint32_t r4_lut4(uint32_t x, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  const uint32_t s7 = x & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(t1, t0, s7), hi = __builtin_amdgcn_perm(t3, t2, s7);
+  // selector 12 gives byte 0x00, 13 gives 0xff: the mask of the nibbles with bit 3 set
+  const uint32_t mask = __builtin_amdgcn_perm(0u, 0u, ((x >> 3) & 0x01010101u) | 0x0c0c0c0cu);
+  return (hi & mask) | (lo & ~mask);
+}
+// bits 0..3 of t -> bit 7 of bytes 0..3 (four shifted copies of t; no two of them overlap)
+__device__ inline uint32_t r4_sign4(uint32_t t) { return ((t << 7) * 0x204081u) & 0x80808080u; }
+
+// Entry i of the launch: rows64 (n entries, dst row i), or the token lists rows32 [T][r_st] with counts (dst row
+// t * K + k for k < counts[t], later entries skipped; no counts: every entry).
+struct DecodeList {
+  const long long* rows64; int n;
+  const int* rows32; long long r_st; const int* counts; int T, K;
+};
+
+__global__ void __launch_bounds__(256) decode400_kernel(const uint8_t* __restrict__ src, long long R, DecodeList L,
+                                                        uint8_t* __restrict__ dst, long long dst_stride, int fmt) {
+  const long long g = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long i = g >> 4;
+  const int q = (int)(g & 15);
+  long long r;
+  if (L.rows64) {
+    if (i >= L.n) return;
+    r = L.rows64[i];
+  } else {
+    if (i >= (long long)L.T * L.K) return;
+    const int t = (int)(i / L.K), k = (int)(i - (long long)t * L.K);
+    if (L.counts && k >= L.counts[t]) return;
+    r = L.rows32[(long long)t * L.r_st + k];
+  }
+  const bool ok = r >= 0 && r < R;
+  const uint8_t* s = src + (ok ? r : 0) * ROW400;
+  u32x4 nib = {0u, 0u, 0u, 0u};
+  uint32_t sg = 0u;
+  int k = 0;
+  u32x4 rp = {0u, 0u, 0u, 0u};
+  if (ok) {
+    nib = *(const u32x4*)(s + 16 * q);
+    sg = *(const uint32_t*)(s + R4_SIGN + 4 * q);
+    k = (int)(int8_t)s[R4_K + q];
+    if (fmt == 1 ? q < 4 : q < 8) {
+      if (fmt == 1) rp = *(const u32x4*)(s + R4_ROPE + 16 * q);
+      else { const uint2 v = *(const uint2*)(s + R4_ROPE + 8 * q); rp[0] = v.x; rp[1] = v.y; }
+    }
+  }
+  uint8_t* d = dst + i * dst_stride;
+  uint32_t c[8];
+  if (k >= -4 && k <= 6) {
+    const uint32_t kb = (uint32_t)(k + 6) << 3;             // 16 .. 96
+    const uint32_t k4 = kb * 0x01010101u;
+    const uint32_t t0 = (k4 & 0xffffff00u) + 0x03fff800u;    // 0, kb - 8, kb, kb + 4
+    const uint32_t t1 = k4 + 0x0e0c0a08u, t2 = k4 + 0x16141210u, t3 = k4 + 0x1e1c1a18u;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {                            // values 8w .. 8w + 7
+      const uint32_t ce = r4_lut4(nib[w] & 0x0f0f0f0fu, t0, t1, t2, t3);          // values 8w + 0, 2, 4, 6
+      const uint32_t co = r4_lut4((nib[w] >> 4) & 0x0f0f0f0fu, t0, t1, t2, t3);   // values 8w + 1, 3, 5, 7
+      c[2 * w] = __builtin_amdgcn_perm(co, ce, 0x05010400u) | r4_sign4((sg >> (8 * w)) & 15u);
+      c[2 * w + 1] = __builtin_amdgcn_perm(co, ce, 0x07030602u) | r4_sign4((sg >> (8 * w + 4)) & 15u);
+    }
+  } else {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      uint32_t x = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = 4 * w + e;
+        const uint32_t code = ((nib[j >> 3] >> (4 * (j & 7))) & 15u) | (((sg >> j) & 1u) << 4);
+        x |= (uint32_t)e2m2_to_e4m3(code, k) << (8 * e);
+      }
+      c[w] = x;
+    }
+  }
+  *(u32x4*)(d + 32 * q) = u32x4{c[0], c[1], c[2], c[3]};
+  *(u32x4*)(d + 32 * q + 16) = u32x4{c[4], c[5], c[6], c[7]};
+  if (fmt == 1) {
+    if (q < 4) *(u32x4*)(d + D_LAT + 16 * q) = rp;
+  } else {
+    if (q < 4) *(float*)(d + SC_OFF + 4 * q) = ok ? 1.0f : 0.0f;
+    if (q < 8) {
+      uint32_t b[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint8_t x = (uint8_t)(rp[e >> 2] >> (8 * (e & 3)));
+        b[e] = (x & 0x7fu) == 0x7fu ? 0x7fc0u : f2u(e4m3_to_f32(x)) >> 16;
+      }
+      *(u32x4*)(d + ROPE_OFF + 16 * q) = u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
+                                               b[6] | (b[7] << 16)};
+    }
+  }
+}
+
 }  // namespace gth
 }  // namespace spmla
 
@@ -445,16 +546,23 @@ int spmla_gather_tiers(const void* src, long long R, int row_bytes, const int* r
   return (int)hipGetLastError();
 }
 
-// ---- the W-way row cache's fill: every miss m < state[1] with miss_dst[m] >= 0 gets its host row (Row656 bytes, or a
-// Row400 row decoded to Row656) at pool row miss_dst[m]; spmla_wcache_step produced the list
-int spmla_wcache_fill(const void* host, long long R, int host_fmt, const long long* miss_rows, const long long* miss_dst,
-                      const int* state, int n_max, void* pool, long long R_pool, void* stream) {
+// ---- the W-way row cache's fill: every miss m < state[1] with miss_dst[m] >= 0 gets its host row (Row656 bytes, a
+// Row400 row decoded to Row656, or Row400 bytes into Row400 lines) at pool row miss_dst[m]; spmla_wcache_step
+// produced the list
+int spmla_wcache_fill(const void* host, long long R, int host_fmt, int pool_fmt, const long long* miss_rows,
+                      const long long* miss_dst, const int* state, int n_max, void* pool, long long R_pool,
+                      void* stream) {
   if (R < 0 || n_max < 0 || R_pool < 0 || (host_fmt != 0 && host_fmt != 2)) return SPMLA_EARG;
+  if (pool_fmt != 0 && !(pool_fmt == 2 && host_fmt == 2)) return SPMLA_EARG;
   if (n_max == 0) return SPMLA_OK;
   if (!host || !miss_rows || !miss_dst || !state || !pool) return SPMLA_EARG;
   if (((uintptr_t)host & 15) || ((uintptr_t)pool & 15)) return SPMLA_EALIGN;
   const unsigned grid = (unsigned)min(64, (n_max + 3) / 4);
-  if (host_fmt == 0)
+  if (pool_fmt == 2)
+    hipLaunchKernelGGL(gth::gather_kernel<gth::CopyRow>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)host, R, ROW400, miss_rows, n_max, (uint8_t*)pool, (long long)ROW400, miss_dst,
+                       R_pool, gth::CopyRow{ROW400 / 16}, state + 1);
+  else if (host_fmt == 0)
     hipLaunchKernelGGL(gth::gather_kernel<gth::CopyRow>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                        (const uint8_t*)host, R, ROW656, miss_rows, n_max, (uint8_t*)pool, (long long)ROW656, miss_dst,
                        R_pool, gth::CopyRow{ROW656 / 16}, state + 1);
@@ -475,8 +583,16 @@ int spmla_row400_gather(const void* src, long long R, const long long* rows, int
   if (n == 0) return SPMLA_OK;
   if (!src || !rows || !dst) return SPMLA_EARG;
   if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < db) return SPMLA_EALIGN;
+  if (!pcie) {                      // HBM source: 16 lanes per row, every row's blocks in flight at once
+    if ((long long)n * 16 > (1ll << 31) - 256) return SPMLA_ELIMIT;
+    const gth::DecodeList L{rows, n, nullptr, 0, nullptr, 0, 0};
+    hipLaunchKernelGGL(gth::decode400_kernel, dim3((unsigned)(((long long)n * 16 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint8_t*)src, R, L, (uint8_t*)dst, dst_stride, dst_fmt);
+    return (int)hipGetLastError();
+  }
+  // pinned host source: a wave per row on 64 workgroups (PCIe-bound; see the gathers above)
   unsigned grid = (unsigned)((n + 3) / 4);
-  if (pcie && grid > 64u) grid = 64u;
+  if (grid > 64u) grid = 64u;
   hipLaunchKernelGGL(gth::gather_kernel<gth::DecodeRow400>, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      (const uint8_t*)src, R, ROW400, rows, n, (uint8_t*)dst, dst_stride, (const long long*)nullptr,
                      0ll, gth::DecodeRow400{dst_fmt});
@@ -518,6 +634,20 @@ int spmla_row400_gather_tiers(const void* src, long long R, const int* rows, lon
   hipLaunchKernelGGL(gth::gather_tiers_kernel<gth::DecodeRow400>, dim3(64), dim3(256), 0, (hipStream_t)stream,
                      (const uint8_t*)src, R, ROW400, rows, r_st, counts, T, K, (uint8_t*)dst, dst_stride,
                      gth::DecodeRow400{dst_fmt});
+  return (int)hipGetLastError();
+}
+
+int spmla_row400_decode_tiers(const void* src, long long R, const int* rows, long long r_st, const int* counts, int T,
+                              int K, void* dst, long long dst_stride, int dst_fmt, void* stream) {
+  const int db = row400_dst_bytes(dst_fmt);
+  if (T < 0 || K < 0 || R < 0 || r_st < K || db == 0) return SPMLA_EARG;
+  if (T == 0 || K == 0) return SPMLA_OK;
+  if (!src || !rows || !dst) return SPMLA_EARG;
+  if (((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || (dst_stride & 15) || dst_stride < db) return SPMLA_EALIGN;
+  if ((long long)T * K * 16 > (1ll << 31) - 256) return SPMLA_ELIMIT;
+  const gth::DecodeList L{nullptr, 0, rows, r_st, counts, T, K};
+  hipLaunchKernelGGL(gth::decode400_kernel, dim3((unsigned)(((long long)T * K * 16 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)src, R, L, (uint8_t*)dst, dst_stride, dst_fmt);
   return (int)hipGetLastError();
 }
 

@@ -379,6 +379,18 @@ def row400_gather_tiers(src, rows, counts, out, R=None):
     return out
 
 
+def row400_decode_tiers(src, rows, counts, out, R=None):
+    """out row t * K + k = the GPU row (out's format: Row656 / Row576) of compact Row400 row src[rows[t, k]] in HBM
+    for k < counts[t] (counts None: every k; zero row when outside [0, R)); other out rows untouched."""
+    T, K = rows.shape
+    _need(rows.dtype == torch.int32 and rows.stride(1) == 1, "int32 rows")
+    _need(counts is None or counts.dtype == torch.int32, "int32 counts")
+    _need(out.shape[0] >= T * K, "out holds T * K rows")
+    _lib.call("spmla_row400_decode_tiers", src.data_ptr(), int(R if R is not None else src.shape[0]), rows.data_ptr(),
+              rows.stride(0), _ptr(counts), T, K, out.data_ptr(), out.stride(0), _dst_fmt(out), _stream(out))
+    return out
+
+
 def copy_rows(src, src_rows, dst, dst_rows, R_src=None):
     n = src_rows.shape[0]
     _lib.call("spmla_copy_rows", src.data_ptr() if torch.is_tensor(src) else int(src),
@@ -388,13 +400,15 @@ def copy_rows(src, src_rows, dst, dst_rows, R_src=None):
 
 class RowCache:
     """Device state of a dynamic W-way HBM row cache (spmla_wcache_*): C lines in S = C / W sets plus `cap` spill rows,
-    both in one Row656 pool [C + cap, 656] that the attention reads; tags, round-robin pointers, pins, and per host row
-    the epoch of its last miss and that miss's pool row. Everything is zero-initialized once (tags -1); no buffer is
-    cleared between steps. two=True: two-choice placement (a row may also live in a second, hashed set; every step
-    and invalidation of this cache then uses both sets)."""
+    both in one pool [C + cap, row_bytes] (Row656 lines that the attention reads, or compact Row400 lines that are
+    decoded for it); tags, round-robin pointers, pins, and per host row the epoch of its last miss and that miss's
+    pool row. Everything is zero-initialized once (tags -1); no buffer is cleared between steps. two=True: two-choice
+    placement (a row may also live in a second, hashed set; every step and invalidation of this cache then uses
+    both sets)."""
 
-    def __init__(self, C, W, cap, device, two=False):
+    def __init__(self, C, W, cap, device, two=False, row_bytes=ROW656):
         _need(C > 0 and W > 0 and C % W == 0 and cap >= 0, "RowCache: C a positive multiple of W, cap >= 0")
+        _need(row_bytes in (ROW656, ROW400), "RowCache: Row656 or Row400 lines")
         self.C, self.W, self.S, self.cap = int(C), int(W), int(C) // int(W), int(cap)
         self.two = bool(two)
         self.device = torch.device(device)
@@ -404,7 +418,7 @@ class RowCache:
         self.cnt = torch.zeros(self.S, **i32)
         self.pin = torch.zeros(self.C, **i32)
         self.state = torch.zeros(4, **i32)              # epoch, misses, spill rows used, hits (of the last step)
-        self.pool = torch.zeros((self.C + self.cap, ROW656), dtype=torch.uint8, device=self.device)
+        self.pool = torch.zeros((self.C + self.cap, int(row_bytes)), dtype=torch.uint8, device=self.device)
         self.n = 0
         self.R = 0
 
@@ -470,11 +484,13 @@ def wcache_resolve(cache, idx, R, res=None):
 
 
 def wcache_fill(cache, host, R, host_fmt, n):
-    """The step's row copies from the host pool (Row656 = host_fmt 0, compact Row400 = 2) into cache.pool; n = the
-    step's entry count (bounds the miss list)."""
+    """The step's row copies from the host pool (Row656 = host_fmt 0, compact Row400 = 2) into cache.pool (Row656
+    lines, or compact Row400 lines that take Row400 rows as they are); n = the step's entry count (bounds the miss
+    list)."""
+    pool_fmt = 2 if cache.pool.shape[1] == ROW400 else 0
     _lib.call("spmla_wcache_fill", host.data_ptr() if torch.is_tensor(host) else int(host), int(R), int(host_fmt),
-              cache.ml.data_ptr(), cache.mdst.data_ptr(), cache.state.data_ptr(), int(n), cache.pool.data_ptr(),
-              cache.pool.shape[0], _stream(cache.pool))
+              pool_fmt, cache.ml.data_ptr(), cache.mdst.data_ptr(), cache.state.data_ptr(), int(n),
+              cache.pool.data_ptr(), cache.pool.shape[0], _stream(cache.pool))
 
 
 def wcache_invalidate(cache, slots, R):
@@ -641,9 +657,11 @@ def attend(q, pool, idx, sm_scale, kv_scale=1.0, out=None, lse=None, split=None,
     return out, lse
 
 
-def attend_partial(q, pool, idx, sm_scale, kv_scale=1.0, opart=None, lpart=None, split=1, kcount=None, R=None):
+def attend_partial(q, pool, idx, sm_scale, kv_scale=1.0, opart=None, lpart=None, split=1, kcount=None, R=None,
+                   row_bytes=None):
     """Like attend, but the result stays as `split` normalized fp32 partials (opart [split, T, H, 512], lpart
-    [split, T, H]) for a later lse_merge (tier partials use split = 1)."""
+    [split, T, H]) for a later lse_merge (tier partials use split = 1). Row576 pools (pool [..., 576] or
+    row_bytes=576) go to spmla_attn576."""
     T, H, _ = q.shape
     K = idx.shape[1]
     _need(attention_ok(q, idx), "attend_partial: q must be bf16 [T, H, 576] with 16-byte aligned rows, idx int32")
@@ -654,9 +672,11 @@ def attend_partial(q, pool, idx, sm_scale, kv_scale=1.0, opart=None, lpart=None,
     _need(opart.is_contiguous() and lpart.is_contiguous() and opart.shape[:3] == (split, T, H), "partials layout")
     Rv = int(R if R is not None else pool.shape[0])
     pptr = pool.data_ptr() if torch.is_tensor(pool) else int(pool)
-    _lib.call("spmla_attn_splitk", q.data_ptr(), q.stride(0), q.stride(1), pptr, Rv, idx.data_ptr(), idx.stride(0),
-              K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), split, None, 0, 0, None, 0,
-              opart.data_ptr(), lpart.data_ptr(), _stream(q))
+    rb = int(row_bytes) if row_bytes is not None else (int(pool.shape[-1]) if torch.is_tensor(pool) else ROW656)
+    _need(rb in (ROW656, ROW576), "attend_partial: Row656 or Row576 rows")
+    _lib.call("spmla_attn576" if rb == ROW576 else "spmla_attn_splitk", q.data_ptr(), q.stride(0), q.stride(1), pptr,
+              Rv, idx.data_ptr(), idx.stride(0), K, _ptr(kcount), T, H, float(sm_scale), float(kv_scale), split, None,
+              0, 0, None, 0, opart.data_ptr(), lpart.data_ptr(), _stream(q))
     return opart, lpart
 
 

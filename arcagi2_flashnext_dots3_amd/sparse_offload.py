@@ -78,7 +78,8 @@ class LayerOffload:
     row_fmt="e2m2"): "row656" lines decoded once when filled, or "e2m2": the reference's compact GPU row cache
     (offload_rowfmt.py:1-22 with its compact cache lines, csrc/offload_attn2.cu:210-256), Row400 lines in HBM (39%
     fewer bytes per line) whose selected lines are decoded into Row656 staging each step before the HBM-tier
-    attention (same values, bit-identical results). two_choice (ways):
+    attention (same values, bit-identical results); with cache_mode="ways" the W-way pool holds Row400 lines the same
+    way (misses copied in as they are, the step's pool rows decoded into staging for the attention). two_choice (ways):
     the reference's two-choice set placement (ARC_OFFLOAD_TWO_CHOICE, offload_fill.py:16-23): a missing row whose set
     has no free way takes one in a second, hashed set before it spills; lookups and invalidations cover both sets.
     """
@@ -101,8 +102,8 @@ class LayerOffload:
         check_host_budget(self.R * HOST_ROW[row_fmt])
         self.host = torch.zeros((self.R, HOST_ROW[row_fmt]), dtype=torch.uint8, pin_memory=True)
         self.C = min(int(cache_rows), self.R)
-        if cache_fmt not in HOST_ROW or (cache_fmt == "e2m2" and (row_fmt != "e2m2" or cache_mode != "static")):
-            raise ValueError("cache_fmt 'e2m2' needs row_fmt='e2m2' and cache_mode='static'")
+        if cache_fmt not in HOST_ROW or (cache_fmt == "e2m2" and row_fmt != "e2m2"):
+            raise ValueError("cache_fmt 'e2m2' needs row_fmt='e2m2'")
         self.cache_fmt = cache_fmt
         self.cache = torch.zeros((max(self.C, 1) if cache_mode == "static" else 1, HOST_ROW[cache_fmt]),
                                  dtype=torch.uint8, device=self.device)
@@ -124,7 +125,8 @@ class LayerOffload:
         if cache_mode == "ways":
             if self.C <= 0 or self.C % int(ways):
                 raise ValueError("cache_mode='ways' needs cache_rows a positive multiple of ways")
-            self.wc = kernels.RowCache(self.C, int(ways), int(spill_rows), self.device, two=two_choice)
+            self.wc = kernels.RowCache(self.C, int(ways), int(spill_rows), self.device, two=two_choice,
+                                       row_bytes=HOST_ROW[cache_fmt])
 
     # ------------------------------------------------------------------------------------------------ rows in
     def store(self, kv_c_normed, k_pe, slots, kv_scale=1.0):
@@ -322,10 +324,10 @@ class LayerOffload:
         side.wait_event(ev_split)
         with torch.cuda.stream(side):
             if self.cache_fmt == "e2m2":
-                # compact lines: decode the step's hot lines (compacted per token, -1 padded) into Row656 staging in
-                # the same order, then attend there through the identity map
-                hstaged = self._buf("hstaged", (T * K, ROW), torch.uint8)
-                kernels.row400_gather(self.cache[:self.C], hbm.reshape(-1).to(torch.int64), hstaged)
+                # compact lines: decode the step's hot lines (compacted per token, -1 padded) into Row576 staging in
+                # the same order (the decoded values are Row576 values), then attend there through the identity map
+                hstaged = self._buf("hstaged", (T * K, kernels.ROW576), torch.uint8)
+                kernels.row400_decode_tiers(self.cache[:self.C], hbm, hcnt, hstaged)
                 kernels.attend_partial(q, hstaged, sidx, sm_scale, kv_scale, op[0:1], lp[0:1], kcount=hcnt)
             else:
                 kernels.attend_partial(q, self.cache[:self.C], hbm, sm_scale, kv_scale, op[0:1], lp[0:1],
@@ -355,12 +357,31 @@ class LayerOffload:
 
     def _attend_ways(self, q, idx, sm_scale, kv_scale, out, lse, num_heads, return_lse):
         """W-way cache step: look up / place / resolve, copy the misses in, attend over the pool. Entries left on
-        the host (spill area full) take the host tier, merged in the host-tier attention's epilogue."""
+        the host (spill area full) take the host tier, merged in the host-tier attention's epilogue. Compact Row400
+        lines (cache_fmt="e2m2") are decoded per step into staging in the order of the row list the attention
+        reads (Row576 staging for the hits, Row656 for the fresh rows that take the merging attention)."""
         T, H, _ = q.shape
         K = idx.shape[1]
         wc = self.wc
+        compact_pool = self.cache_fmt == "e2m2"
         res = self._buf("res", (T, K), torch.int32)
         fmt = 2 if self.row_fmt == "e2m2" else 0
+        ident = self._identity(T, K, q.device)
+
+        def pool_rows(rows, name, width, counts=None):
+            """(pool, index map) the attention reads for pool rows `rows` [T, K] (< 0: none): the pool itself, or the
+            rows decoded into staging row t * K + k -- for lists compacted per token (counts: the attention reads
+            only those entries) the identity map, else a map that keeps the entries without a row at -1."""
+            if not compact_pool:
+                return wc.pool, rows
+            st = self._buf(name, (T * K, width), torch.uint8)
+            kernels.row400_decode_tiers(wc.pool, rows, counts, st)
+            if counts is not None:
+                return st, ident
+            m = self._buf(name + "_map", (T, K), torch.int32)
+            torch.where(rows >= 0, ident, torch.full_like(ident, -1), out=m)
+            return st, m
+
         if T * K <= wc.cap and self.overlap_fill:
             # placement, then the PCIe copy of the misses on the second stream while the resolution, the hit / fresh
             # split and the attention over the hits run here; the fresh rows' attention merges the hits' partial
@@ -380,14 +401,17 @@ class LayerOffload:
             kernels.wcache_split(wc, res, hit, hcnt, fresh, fcnt)
             op = self._buf("opart", (1, T, H, kernels.D_LAT), torch.float32)
             lp = self._buf("lpart", (1, T, H), torch.float32)
-            kernels.attend_partial(q, wc.pool, hit, sm_scale, kv_scale, op, lp, kcount=hcnt)
+            src, rows = pool_rows(hit, "hstaged", kernels.ROW576, hcnt)
+            kernels.attend_partial(q, src, rows, sm_scale, kv_scale, op, lp, kcount=hcnt)
             main.wait_event(ev_fill)
-            kernels.attend_merge(q, wc.pool, fresh, sm_scale, kv_scale, op[0], lp[0], out=out, lse=lse, kcount=fcnt)
+            src, rows = pool_rows(fresh, "fstaged", ROW, fcnt)
+            kernels.attend_merge(q, src, rows, sm_scale, kv_scale, op[0], lp[0], out=out, lse=lse, kcount=fcnt)
             return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
         kernels.wcache_step(wc, idx, self.R, res)
         kernels.wcache_fill(wc, self.host, self.R, fmt, T * K)
         if T * K <= wc.cap:                                  # every miss fits the spill area: one HBM tier
-            kernels.attend(q, wc.pool, res, sm_scale, kv_scale, out=out, lse=lse)
+            src, rows = pool_rows(res, "hstaged", kernels.ROW576)
+            kernels.attend(q, src, rows, sm_scale, kv_scale, out=out, lse=lse)
         else:
             hbm = self._buf("hbm", (T, K), torch.int32)
             host = self._buf("host", (T, K), torch.int32)
@@ -396,14 +420,14 @@ class LayerOffload:
             kernels.split_res(idx, res, hbm, hcnt, host, mcnt)
             op = self._buf("opart", (1, T, H, kernels.D_LAT), torch.float32)
             lp = self._buf("lpart", (1, T, H), torch.float32)
-            kernels.attend_partial(q, wc.pool, hbm, sm_scale, kv_scale, op, lp, kcount=hcnt)
+            src, rows = pool_rows(hbm, "hstaged", kernels.ROW576, hcnt)
+            kernels.attend_partial(q, src, rows, sm_scale, kv_scale, op, lp, kcount=hcnt)
             staged = self._buf("staged", (T * K, ROW), torch.uint8)
             if self.row_fmt == "e2m2":
                 kernels.row400_gather_tiers(self.host, host, mcnt, staged)
             else:
                 kernels.gather_tiers(self.host, host, mcnt, staged)
-            kernels.attend_merge(q, staged, self._identity(T, K, q.device), sm_scale, kv_scale, op[0], lp[0],
-                                 out=out, lse=lse, kcount=mcnt)
+            kernels.attend_merge(q, staged, ident, sm_scale, kv_scale, op[0], lp[0], out=out, lse=lse, kcount=mcnt)
         return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
 
     def hit_rate(self, idx):

@@ -13,10 +13,13 @@ torch-CPU restatement (oracle/cpu_port.py) of the same step on this host's cores
 carries `host_tier_variant`: BASELINE config 3 (same shapes, 2M-row pool in pinned host memory, 25% HBM hot set,
 Zipf(1.1) selections) measured in the same run, and `host_tier_compact_variant`: the same with the host pool in the
 reference's compact Row400 rows (decoded on the way in; 400 instead of 656 bytes per row over PCIe), and
-`host_tier_ways_variant`: compact host rows behind the dynamic 16-way row cache instead of the static hot set, on a
-stream of fresh Zipf draws (`--config 3 --cache ways`); `host_tier_ways_two_choice_variant` the same with two-choice
-set placement (`--two-choice`); `host_tier_compact_cache_variant` keeps the static hot set as compact Row400 lines in
-HBM (`--host-rows e2m2 --cache-fmt e2m2`).
+`host_tier_compact_cache_variant` keeps the static hot set as compact Row400 lines in HBM (`--host-rows e2m2
+--cache-fmt e2m2`); `host_tier_production_variant` is the reference's shipped offload mode (mode_submit.json: compact
+host rows, a dynamic 8-way two-choice row cache of compact Row400 lines, the miss copy beside the attention over the
+hits) on a stream of fresh Zipf draws (`--config 3 --cache ways --ways 8 --two-choice --host-rows e2m2 --cache-fmt
+e2m2`); `host_tier_overflow_one_choice_variant` / `..._two_choice_variant` run it with a 131,072-line cache (the
+reference's two-choice geometry, offload_fill.py:16-20), whose sets overflow, without and with two-choice placement,
+reporting misses and spill rows per step.
 
 Other configs print their own JSON line (same keys): 1 = B=1 / 16 heads / K=256 check + timing, 3 = offload split-K,
 4 = indexer logits + top-2048 at L = 32768 and 131072, 5 = chunked prefill (8192 queries) + cache write, 6 = the
@@ -326,18 +329,20 @@ def run_config3(a, dev, steps=None, row_fmt="row656", cache_fmt="row656", host_d
     return res
 
 
-def run_config3_ways(a, dev, steps=None, row_fmt="e2m2", W=16, two=False):
+def run_config3_ways(a, dev, steps=None, row_fmt="e2m2", W=16, two=False, cache_fmt="row656", C=None):
     """Config 3 shapes with the dynamic W-way cache in place of the static hot set: every step draws fresh Zipf(1.1)
     selections (a decode stream); the cache is warmed over the 64 warm-up steps' draws, then each timed step looks
     its rows up, places the misses, copies them in over PCIe (beside the attention over the hits) and attends.
-    two: two-choice set placement (a miss whose set is full takes a way in a second, hashed set)."""
+    two: two-choice set placement (a miss whose set is full takes a way in a second, hashed set); cache_fmt "e2m2":
+    compact Row400 lines (the reference's production mode with row_fmt "e2m2", W = 8 and two); C: cache lines
+    (default a quarter of the pool)."""
     import torch
     from arcagi2_flashnext_dots3_amd.sparse_offload import HOST_ROW, LayerOffload
     steps = steps or a.steps
     warm_n = max(2, a.warmup // 4)
-    C = R3 // 4
+    C = int(C or R3 // 4)
     lo = LayerOffload(R3, dev, cache_rows=C, row_fmt=row_fmt, cache_mode="ways", ways=W, spill_rows=B * K,
-                      two_choice=two)
+                      two_choice=two, cache_fmt=cache_fmt)
     _cache_fill(lo.host, R3, 1, dev, fmt=2 if row_fmt == "e2m2" else 0)
     perm = torch.randperm(R3, generator=torch.Generator().manual_seed(3))
     gq = torch.Generator().manual_seed(0)
@@ -372,9 +377,11 @@ def run_config3_ways(a, dev, steps=None, row_fmt="e2m2", W=16, two=False):
            "hit_rate": round(hit, 4), "misses_per_step": round(misses / nstat, 1),
            "spill_rows_per_step": round(spills / nstat, 1), "pcie_bytes_per_step": int(mb),
            "pcie_gbs_achieved": round(mb / (ms * 1e-3) / 1e9, 2), "h2d_copy_gbs": round(h2d, 2),
-           "host_row_format": row_fmt, "ways": W, "two_choice": bool(two),
+           "host_row_format": row_fmt, "cache_line_format": cache_fmt, "ways": W, "two_choice": bool(two),
+           "cache_lines": C,
            "workload": f"config 3 shapes with a dynamic {W}-way set-associative{' two-choice' * two} HBM cache of "
-                       f"524,288 lines (+ 131,072 spill rows) over a 2,097,152-row "
+                       f"{C:,} {'compact Row400' if cache_fmt == 'e2m2' else 'Row656'} lines (+ 131,072 spill rows) "
+                       f"over a 2,097,152-row "
                        f"{'compact Row400' if row_fmt == 'e2m2' else 'Row656'}"
                        " pinned host pool; each step a fresh Zipf(1.1) draw of B=64 x top-2048 rows; warmed over "
                        "64 steps; per step: lookup / place / resolve, miss copy over PCIe beside the attention over "
@@ -758,6 +765,11 @@ def _child_variant(args, timeout=600):
         return {"error": repr(e)[:300]}
 
 
+# the reference's shipped offload mode as config-3 options (mode_submit.json: ARC_OFFLOAD_WAYS=8, ROW_FMT=e2m2, CCACHE=1,
+# OVERLAP=1, TWO_CHOICE=1)
+PRODUCTION = ["--host-rows", "e2m2", "--cache", "ways", "--ways", "8", "--two-choice", "--cache-fmt", "e2m2"]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -772,8 +784,10 @@ def main():
                     help="config 3: static frequency hot set (BASELINE's definition) or the dynamic W-way cache")
     ap.add_argument("--ways", type=int, default=16, help="config 3 --cache ways: lines per set")
     ap.add_argument("--two-choice", action="store_true", help="config 3 --cache ways: two-choice set placement")
+    ap.add_argument("--cache-rows", type=int, default=0,
+                    help="config 3 --cache ways: cache lines (default a quarter of the pool, 524,288)")
     ap.add_argument("--cache-fmt", default="row656", choices=["row656", "e2m2"],
-                    help="config 3 static cache with --host-rows e2m2: Row656 lines, or compact Row400 lines in HBM")
+                    help="config 3 with --host-rows e2m2: Row656 cache lines, or compact Row400 lines in HBM")
     ap.add_argument("--host-direct", action="store_true",
                     help="config 3 static cache, Row656 host rows: the host-tier attention reads the pinned rows in "
                          "place over PCIe instead of a staging copy into HBM")
@@ -807,13 +821,15 @@ def main():
             for key, extra in (("host_tier_variant", ["--host-rows", "row656"]),
                                ("host_tier_compact_variant", ["--host-rows", "e2m2"]),
                                ("host_tier_compact_cache_variant", ["--host-rows", "e2m2", "--cache-fmt", "e2m2"]),
-                               ("host_tier_ways_variant", ["--host-rows", "e2m2", "--cache", "ways"]),
-                               ("host_tier_ways_two_choice_variant",
-                                ["--host-rows", "e2m2", "--cache", "ways", "--two-choice"])):
+                               ("host_tier_production_variant", PRODUCTION),
+                               ("host_tier_overflow_one_choice_variant",
+                                [x for x in PRODUCTION if x != "--two-choice"] + ["--cache-rows", "131072"]),
+                               ("host_tier_overflow_two_choice_variant", PRODUCTION + ["--cache-rows", "131072"])):
                 print(f"[bench] {key}: child process", file=sys.stderr, flush=True)
                 res[key] = _child_variant(["--config", "3", "--steps", st, "--warmup", str(a.warmup)] + extra)
     elif a.config == 3:
-        r = run_config3_ways(a, dev, row_fmt=a.host_rows, W=a.ways, two=a.two_choice) if a.cache == "ways" else \
+        r = run_config3_ways(a, dev, row_fmt=a.host_rows, W=a.ways, two=a.two_choice, cache_fmt=a.cache_fmt,
+                             C=a.cache_rows) if a.cache == "ways" else \
             run_config3(a, dev, row_fmt=a.host_rows, cache_fmt=a.cache_fmt, host_direct=a.host_direct)
         res = _line("offload split-K decode step us (host tier + HBM hot rows), B=64 top2048", r["ms_per_step"] * 1e3,
                     "us", a, r["ms_per_step"], "bf16 MFMA, fp32 accumulate", {"workload": r["workload"]},

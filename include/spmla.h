@@ -174,6 +174,13 @@ int spmla_row400_copy(const void* src, long long R_src, const long long* src_row
 int spmla_row400_gather_tiers(const void* src, long long R, const int* rows, long long r_st, const int* counts, int T,
                               int K, void* dst, long long dst_stride, int dst_fmt, void* stream);
 
+/* Compact Row400 lines in HBM decoded for the attention (the reference's compact GPU row cache, ARC_OFFLOAD_CCACHE,
+ * whose loaders decode the lines in shared memory, csrc/offload_attn2.cu:210-256): dst row t * K + k = the dst_fmt row
+ * (0 = Row656, 1 = Row576) of src row rows[t * r_st + k] (zero row when outside [0, R)) for k < counts[t] (counts
+ * NULL: every k < K); other dst rows untouched. src in HBM: 16 lanes per row, each decoding one 32-value block. */
+int spmla_row400_decode_tiers(const void* src, long long R, const int* rows, long long r_st, const int* counts, int T,
+                              int K, void* dst, long long dst_stride, int dst_fmt, void* stream);
+
 /* Dynamic W-way HBM row cache, bookkeeping of one decode step (no row copies). Host row h lives in set h % S
  * (S = C / W), in any line st * W + w with tag[line] == h (-1 empty). For the selected rows idx [T][K] (invalid =
  * outside [0, R)): entries whose row is cached pin their line for the step; each distinct missing row takes a ticket
@@ -205,12 +212,15 @@ int spmla_wcache_resolve(const int* idx, long long idx_st, int T, int K, long lo
                          int* cnt, int* pin, int* claim, int* rdst, long long* miss_rows, long long* miss_dst,
                          int* state, int cap, int two, int* res, long long res_st, void* stream);
 
-/* The step's row copies: for each miss m < state[1] with miss_dst[m] >= 0, pool row miss_dst[m] (Row656) = host row
- * miss_rows[m] (host_fmt 0: Row656 bytes; 2: a compact Row400 row decoded to Row656). n_max bounds the miss count
- * (T * K of the step). 64 workgroups, rows streamed two per wave (the PCIe gather). Replaces the copy half of the
- * reference's fill (_sa_fill_kernel sparse_offload.py:722-760; the split fill's gather, offload_fill.py:311-333). */
-int spmla_wcache_fill(const void* host, long long R, int host_fmt, const long long* miss_rows, const long long* miss_dst,
-                      const int* state, int n_max, void* pool, long long R_pool, void* stream);
+/* The step's row copies: for each miss m < state[1] with miss_dst[m] >= 0, pool row miss_dst[m] = host row
+ * miss_rows[m]. host_fmt / pool_fmt: 0 / 0 Row656 bytes into Row656 lines; 2 / 0 a compact Row400 row decoded into a
+ * Row656 line; 2 / 2 the Row400 bytes as they are into compact Row400 lines (the reference's compact GPU row cache,
+ * ARC_OFFLOAD_CCACHE). n_max bounds the miss count (T * K of the step). 64 workgroups, rows streamed two per wave
+ * (the PCIe gather). Replaces the copy half of the reference's fill (_sa_fill_kernel sparse_offload.py:722-760; the
+ * split fill's gather, offload_fill.py:311-333). */
+int spmla_wcache_fill(const void* host, long long R, int host_fmt, int pool_fmt, const long long* miss_rows,
+                      const long long* miss_dst, const int* state, int n_max, void* pool, long long R_pool,
+                      void* stream);
 
 /* Clear the lines that cache rows slots[i] (a rewritten host row must not be served stale); two = 1 also clears
  * the rows' second sets. Replaces _sa_invalidate_kernel (sparse_offload.py:782-789) and, for two-choice placement,

@@ -74,7 +74,8 @@ def test_version():
       None, 0, None), -5),
     (("spmla_wcache_step", None, 0, 1, 8, 100, None, 8, 4, None, None, None, None, None, None, None, None, 0, 2, None,
       0, None), -2),
-    (("spmla_wcache_fill", None, 0, 1, None, None, None, 4, None, 0, None), -2),
+    (("spmla_wcache_fill", None, 0, 1, 0, None, None, None, 4, None, 0, None), -2),
+    (("spmla_wcache_fill", None, 0, 0, 2, None, None, None, 4, None, 0, None), -2),    # Row656 rows, Row400 lines
     (("spmla_bmm_fp8", None, 0, 0, 1, None, 0, 0, 1, None, 0, 0, 0, 0, None, 0, 0, 1, 0, 1, 1, 1, 12, None), -2),
     (("spmla_mla_query", None, 0, 0, None, 0, 0, None, None, 1, 0, None, 0, 0, None), -2),
     (("spmla_wcache_invalidate", None, 1, 10, None, 6, 4, 0, None), -2),

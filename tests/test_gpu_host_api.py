@@ -109,6 +109,17 @@ def test_shard_store_and_sharded_topk(dev):
     assert np.max(np.abs(glg[fin] - exp_lg[fin]) / np.maximum(1, np.abs(exp_lg[fin]))) <= 2e-5
     # selection is exact on the GPU's own logits
     assert np.array_equal(out.cpu().numpy(), ref.topk(glg, ctx.numpy(), K + 3))
+    # the reference's fp8 indexer query (shard_indexer.py:118-120): e4m3 queries give the logits of their exact bf16
+    # values, bit for bit, and the fp64 oracle's over those values
+    q8 = (q.float() * 4.0).to(torch.float8_e4m3fn)
+    lg8 = st.logits(q8.to(dev), w.to(dev), bt.to(dev), req.to(dev), ctx.to(dev), L)
+    lgw = st.logits(q8.to(torch.bfloat16).to(dev), w.to(dev), bt.to(dev), req.to(dev), ctx.to(dev), L)
+    torch.cuda.synchronize()
+    assert torch.equal(lg8, lgw)
+    exp8 = ref.index_logits(q8.float().numpy(), w.numpy(), store, bt.numpy(), bs, req.numpy(), ctx.numpy(), L)
+    g8 = lg8.cpu().numpy()
+    assert np.array_equal(np.isinf(g8), np.isinf(exp8))
+    assert np.max(np.abs(g8[fin] - exp8[fin]) / np.maximum(1, np.abs(exp8[fin]))) <= 2e-5
 
 
 def _offload_layer(dev, R, C, seed, **kw):

@@ -160,10 +160,39 @@ def test_layer_offload_compact_rows(dev, C, cache_fmt):
     # bf16 output: 1e-2 absolute plus its own rounding (2^-9 relative)
     assert np.all(np.abs(out.float().cpu().numpy() - eo) <= 1e-2 + 2.0 ** -9 * np.abs(eo))
     assert np.abs(lse.cpu().numpy() - el).max() < 1e-3
-    if C and cache_fmt == "e2m2":                      # same values as Row656 lines: bit-identical attention
+    if C and cache_fmt == "e2m2":
+        # same values as Row656 lines (the compact lines' hot tier is attended from Row576 staging, the Row656
+        # lines' from the lines themselves: the two kernels differ only in fp32 summation order)
         lo2 = LayerOffload(R, dev, key="l1", cache_rows=C, row_fmt="e2m2")
         lo2.host.copy_(lo.host)
         lo2.set_hot_rows(torch.arange(0, 2 * C, 2, dtype=torch.int64))
         o2, l2 = lo2.attend(q.to(dev), idx.to(dev), sm, kv_scale, return_lse=True)
         torch.cuda.synchronize()
-        assert torch.equal(out, o2) and torch.equal(lse, l2)
+        err = (out.float() - o2.float()).abs() / o2.float().abs().clamp_min(1.0)
+        assert float(err.max()) <= 1e-2 and float((lse - l2).abs().max()) <= 1e-4
+
+
+@pytest.mark.parametrize("width,with_counts", [(576, True), (656, True), (576, False)])
+def test_row400_decode_tiers(dev, width, with_counts):
+    """Compact lines in HBM decoded per token list (spmla_row400_decode_tiers): out row t * K + k = the oracle's decode
+    of src row rows[t, k] for k < counts[t] (every k without counts; invalid rows give zero rows), other out rows
+    untouched; wide-range blocks, special blocks and arbitrary bytes decode as the oracle does."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    n, R, T, K = 700, 1000, 5, 300
+    kv, pe = _inputs(n, 7)
+    src_np = _oracle_rows(kv, pe, np.arange(n), R, 0.5, 0)
+    src_np[n:] = np.random.default_rng(8).integers(0, 256, (R - n, 400))
+    src = torch.from_numpy(src_np).to(dev)
+    g = np.random.default_rng(9)
+    rows = g.integers(-2, R + 2, (T, K)).astype(np.int32)
+    counts = np.array([K, 0, 17, 299, 150], dtype=np.int32)
+    out = torch.full((T * K, width), 0xA5, dtype=torch.uint8, device=dev)
+    print(f"[decode_tiers] width={width} counts={with_counts}", flush=True)
+    kernels.row400_decode_tiers(src, torch.from_numpy(rows).to(dev),
+                                torch.from_numpy(counts).to(dev) if with_counts else None, out)
+    got = out.cpu().numpy()
+    for t in range(T):
+        c = counts[t] if with_counts else K
+        exp = ref.row400_gather(src_np, rows[t, :c], fmt=width)
+        assert np.array_equal(got[t * K:t * K + c], exp), t
+        assert np.all(got[t * K + c:(t + 1) * K] == 0xA5)

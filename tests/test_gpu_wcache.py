@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from oracle import spmla_ref as ref
-from tests.helpers import make_pool_656, make_q
+from tests.helpers import attn_excess, make_pool_656, make_q
 
 pytestmark = pytest.mark.gpu
 
@@ -54,8 +54,9 @@ def _check_step(wc, host_rows, idx, res, tag0, rr0, R):
     assert len(set(sp.values())) == len(sp)
 
 
-@pytest.mark.parametrize("W,host_fmt", [(4, 0), (16, 0), (16, 2)])
-def test_wcache_steps(dev, W, host_fmt):
+@pytest.mark.parametrize("W,host_fmt,pool_fmt", [(4, 0, 0), (16, 0, 0), (16, 2, 0), (8, 2, 2)])
+def test_wcache_steps(dev, W, host_fmt, pool_fmt):
+    """pool_fmt 2: compact Row400 lines, which receive the host's Row400 bytes as they are."""
     from arcagi2_flashnext_dots3_amd import kernels
     R, C, T, K = 20000, 1024, 4, 512
     if host_fmt == 0:
@@ -67,9 +68,9 @@ def test_wcache_steps(dev, W, host_fmt):
         pe = ref.f32_to_bf16_bits(torch.randn(R, 64, generator=g).numpy())
         host_np = np.zeros((R, 400), dtype=np.uint8)
         ref.cache_write_400(kv, pe, np.arange(R), host_np)
-        host_rows = ref.row400_gather(host_np, np.arange(R), fmt=656)
+        host_rows = host_np if pool_fmt == 2 else ref.row400_gather(host_np, np.arange(R), fmt=656)
     host = torch.from_numpy(host_np).pin_memory()
-    wc = kernels.RowCache(C, W, T * K, dev)
+    wc = kernels.RowCache(C, W, T * K, dev, row_bytes=400 if pool_fmt == 2 else 656)
     for step in range(6):
         idx = _selections(T, K, R, step)
         tag0, rr0 = wc.tag.cpu().numpy().astype(np.int64), wc.rr.cpu().numpy()
@@ -232,3 +233,52 @@ def test_layer_offload_two_choice_matches_single_tier(dev):
         torch.cuda.synchronize()
         assert torch.equal(out, o1) and torch.equal(lse, l1)
     assert lo.hit_rate(idx) > 0.0
+
+
+@pytest.mark.parametrize("cap,overlap", [(4096, False), (4096, True), (64, True)])
+def test_layer_offload_compact_ways(dev, cap, overlap):
+    """The reference's production offload mode (mode_submit.json: ARC_OFFLOAD_WAYS=8, ARC_OFFLOAD_ROW_FMT=e2m2,
+    ARC_OFFLOAD_CCACHE=1, ARC_OFFLOAD_OVERLAP=1, ARC_OFFLOAD_TWO_CHOICE=1): compact Row400 host rows and compact
+    Row400 lines in an 8-way two-choice pool, the step's pool rows decoded for the attention. With a spill area
+    covering the step and no overlap, the result equals bit for bit the single-tier attention over the host rows
+    decoded to Row576 (same bytes, same kernel, same order); with the overlap or a small spill area (rows left on the
+    host) it matches within the tier-merge tolerance; and it matches the fp64 oracle over the decoded rows."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    from arcagi2_flashnext_dots3_amd.sparse_offload import LayerOffload
+    R, T, H, K, ks = 6000, 4, 64, 1024, 0.5
+    g = torch.Generator().manual_seed(11)
+    kv = (torch.randn(R, 512, generator=g) * 2).to(torch.bfloat16)
+    pe = torch.randn(R, 64, generator=g).to(torch.bfloat16)
+    lo = LayerOffload(R, dev, cache_rows=512, cache_mode="ways", ways=8, spill_rows=cap, overlap_fill=overlap,
+                      two_choice=True, row_fmt="e2m2", cache_fmt="e2m2")
+    assert lo.wc.pool.shape[1] == 400
+    lo.store(kv.to(dev), pe.to(dev), torch.arange(R, dtype=torch.int64, device=dev), kv_scale=ks)
+    q = make_q(T, H, seed=12).to(dev)
+    sm = 192 ** -0.5
+    host_np = lo.host.numpy()
+    for step in range(4):
+        print(f"[compact ways] cap={cap} overlap={overlap} step={step}", flush=True)
+        idx = torch.from_numpy(_selections(T, K, R, step, hot=300)).to(dev)
+        out, lse = lo.attend(q, idx, sm, ks, return_lse=True)
+        staged = torch.empty(T * K, 576, dtype=torch.uint8, device=dev)
+        kernels.row400_gather(lo.host, idx.reshape(-1).to(torch.int64), staged, pcie=True)
+        sidx = torch.where((idx >= 0) & (idx < R), torch.arange(T * K, device=dev, dtype=torch.int32).view(T, K),
+                           torch.full_like(idx, -1))
+        o1, l1 = kernels.attend(q, staged, sidx, sm, ks)
+        torch.cuda.synchronize()
+        if cap >= T * K and not overlap:
+            assert torch.equal(out, o1) and torch.equal(lse, l1)
+        else:
+            err = (out.float() - o1.float()).abs() / o1.float().abs().clamp_min(1.0)
+            assert float(err.max()) <= 1e-2
+            assert float((lse - l1).abs().max()) <= 1e-4
+        if step == 3:
+            i_np = idx.cpu().numpy()
+            rows576 = ref.row400_gather(host_np, i_np.reshape(-1), fmt=576)
+            local = np.where((i_np >= 0) & (i_np < R), np.arange(T * K).reshape(T, K), -1)
+            eo, el = ref.attention(q.float().cpu().numpy(), rows576, local, sm, ks, fmt=576)
+            assert attn_excess(out.float().cpu().numpy(), eo) <= 0
+            fin = np.isfinite(el)
+            assert np.abs(lse.cpu().numpy()[fin] - el[fin]).max() <= 1e-3
+    st = lo.wc.state.cpu().numpy()
+    assert lo.hit_rate(idx) > 0.0 and st[3] > 0
