@@ -794,6 +794,8 @@ def main():
     ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
                     help="only run 5 plain device-to-device copies of BYTES bytes (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
+    ap.add_argument("--rows", type=int, default=656, choices=[656, 576],
+                    help="config 2: 576 times the step over a Row576 cache alone (the row576_variant of the default line)")
     ap.add_argument("--idx-sets", type=int, default=4,
                     help="steps rotate over this many independent top-k draws; 4 sets select 344 MB of rows, more "
                          "than the 256 MB Infinity Cache, so rows come from HBM rather than from the previous step")
@@ -812,7 +814,22 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calib_bytes": a.copy_calib}), flush=True)
         return
-    if a.config == 2:
+    if a.config == 2 and a.rows == 576:         # config 2 over the plugin's Row576 cache alone (profiling)
+        gq = torch.Generator().manual_seed(0)
+        q = torch.randn(B, H, D, generator=gq).to(torch.bfloat16).to(dev)
+        idxs = []
+        for n in range(a.idx_sets):
+            gi = torch.Generator().manual_seed(2 + n)
+            idxs.append(torch.stack([torch.randperm(CTX, generator=gi)[:K] + b * CTX for b in range(B)])
+                        .to(torch.int32).to(dev))
+        out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+        lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+        r = run_row576(a, dev, q, idxs, out, lse)
+        res = _line(METRIC, r["gbs"], "GB/s", a, r["step_us"] / 1e3, "fp8e4m3 rows x bf16 q: bf16 MFMA (QK), f16 MFMA (PV)",
+                    {"workload": r["workload"]}, {"bound": "hbm", "achieved": r["gbs"], "peak": HBM_PEAK_GBS,
+                                                  "unit": "GB/s", "frac": r["frac"], "traffic": None,
+                                                  "kernel": r["kernel"]}, detail=r)
+    elif a.config == 2:
         res = run_config2(a, dev)
         if not a.no_variant:
             # each config-3 variant in a fresh child process (its own GPU context and pinned pool), so no variant
