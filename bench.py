@@ -8,7 +8,9 @@ sequence held as Row656 KV rows in HBM (latent / rope N(0,1), written by the lib
 N(0,1), top-2048 row indices per sequence drawn uniformly without replacement, softmax scale 1/sqrt(192), bf16 out +
 fp32 LSE. One step = one spmla_attn_splitk launch over the whole batch (inputs resident in HBM). `value` = effective
 GB/s = algorithmic bytes / step time, algorithmic bytes = 131072 rows x 656 B + q + idx + out + lse = 104,366,080 B.
-`roofline` is timed live with HIP events on the stream the kernel is launched on; `cpu_baseline` times the float32
+`roofline` is timed live with HIP events on the stream the kernel is launched on, and its `traffic` (HBM bytes per
+launch) is counted in the same run: four rocprofv3 --pmc child runs (FETCH_SIZE and WRITE_SIZE over a few probe
+launches, and over a plain 256 MiB device copy that calibrates the counters; --no-traffic skips them); `cpu_baseline` times the float32
 torch-CPU restatement (oracle/cpu_port.py) of the same step on this host's cores. Unless --no-variant, the line also
 carries `host_tier_variant`: BASELINE config 3 (same shapes, 2M-row pool in pinned host memory, 25% HBM hot set,
 Zipf(1.1) selections) measured in the same run, and `host_tier_compact_variant`: the same with the host pool in the
@@ -190,17 +192,17 @@ def run_config2(a, dev):
     eager_ms = _timed(step, a.steps, a.warmup)          # right after, at the same settled clocks
     gbs = ALG_BYTES / (ms * 1e-3) / 1e9
     # unsplit decode launches run the head-group kernel, split ones the 128-head kernel with its in-kernel merge
-    kname = "spmla::pk::attn_kernel<false>" if split == 1 else "spmla::attn::fwd_kernel"
+    kname = "spmla::pk::attn_kernel<false, false>" if split == 1 else "spmla::attn::fwd_kernel"
     roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": kname, "alg_bytes_per_launch": ALG_BYTES,
             "mfma_tflops": round(ALG_FLOPS / (ms * 1e-3) / 1e12, 2),
             "mfma_frac_bf16_peak": round(ALG_FLOPS / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
-    tf = os.path.join(ROOT, "profiles", "attn_kernel_config2_traffic.json")
-    if os.path.exists(tf):   # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (calibrated)
-        tj = json.load(open(tf))
-        if tj.get("kernel") == kname:
-            roof["traffic"] = tj.get("bytes_per_launch")
+    if not a.no_traffic:     # HBM bytes per launch, counted in this run (rocprofv3 --pmc over probe children)
+        tr = measure_traffic(r"attn_kernel<false, false>" if split == 1 else "fwd_kernel",
+                             ["--config", "2", "--probe", "--idx-sets", str(a.idx_sets)])
+        roof["traffic"] = tr.get("bytes_per_launch")
+        roof["traffic_detail"] = tr
     cfg = {"workload": "BASELINE config 2: all-HBM sparse-MLA decode, B=64, H=128, ctx=32768/seq, top-2048, Row656 "
                        "rows, bf16 out + fp32 LSE; launches replayed from a HIP graph after 0.2 s of untimed back-to-back "
                        "launches (steady-state clocks)",
@@ -214,6 +216,61 @@ def run_config2(a, dev):
     if not a.no_variant:
         res["row576_variant"] = run_row576(a, dev, q, idxs, out, lse)
     return res
+
+
+def run_probe(a, dev):
+    """A few eager launches of config 2's step and nothing else (the launches a counter run reads)."""
+    import torch
+    from arcagi2_flashnext_dots3_amd import kernels
+    pool, q, idxs = build_inputs(dev, a.idx_sets)
+    out = torch.empty(B, H, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+    for i in range(2 * len(idxs)):
+        kernels.attend(q, pool, idxs[i % len(idxs)], SM_SCALE, out=out, lse=lse)
+    torch.cuda.synchronize()
+    return {"probe_launches": 2 * len(idxs)}
+
+
+def _pmc(counter, regex, args, timeout=180):
+    """Average per-dispatch value of one rocprofv3 counter over the kernels matching regex, in a child run of this
+    script with `args` (from /tmp, as rocprofv3 wants); None when the profiler or the child fails."""
+    import csv
+    import re
+    import subprocess
+    import tempfile
+    d = tempfile.mkdtemp(prefix="spmla_pmc_", dir="/tmp")
+    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "run", "--",
+           sys.executable, os.path.abspath(__file__)] + args
+    env = dict(os.environ, TMPDIR="/tmp")
+    try:
+        subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, timeout=timeout)
+    except Exception:
+        return None
+    vals = []
+    for root, _, files in os.walk(d):
+        for f in files:
+            if f.endswith("counter_collection.csv"):
+                for row in csv.DictReader(open(os.path.join(root, f))):
+                    if row.get("Counter_Name") == counter and re.search(regex, row.get("Kernel_Name", "")):
+                        vals.append(float(row["Counter_Value"]))
+    return sum(vals) / len(vals) if vals else None
+
+
+def measure_traffic(regex, args, calib=1 << 28):
+    """HBM bytes per launch of the kernels matching regex: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) each scaled
+    by the bytes a plain device copy of `calib` bytes moves per KiB that counter reads for it, four counter runs of
+    child processes in this run (one counter per run)."""
+    fk = _pmc("FETCH_SIZE", regex, args)
+    wk = _pmc("WRITE_SIZE", regex, args)
+    cf = _pmc("FETCH_SIZE", "copyBuffer", ["--copy-calib", str(calib)])
+    cw = _pmc("WRITE_SIZE", "copyBuffer", ["--copy-calib", str(calib)])
+    if None in (fk, wk, cf, cw) or cf <= 0 or cw <= 0:
+        return {"bytes_per_launch": None, "error": "a counter run failed",
+                "fetch_kib": fk, "write_kib": wk, "copy_fetch_kib": cf, "copy_write_kib": cw}
+    ff, fw = calib / (cf * 1024), calib / (cw * 1024)
+    return {"bytes_per_launch": int(round(fk * 1024 * ff + wk * 1024 * fw)), "fetch_kib": round(fk, 1),
+            "write_kib": round(wk, 1), "fetch_factor": round(ff, 4), "write_factor": round(fw, 4),
+            "source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE in this run, scaled by a plain copy's readings"}
 
 
 def run_row576(a, dev, q, idxs, out, lse):
@@ -794,6 +851,9 @@ def main():
     ap.add_argument("--copy-calib", type=int, default=0, metavar="BYTES",
                     help="only run 5 plain device-to-device copies of BYTES bytes (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="config 2: skip the in-run rocprofv3 FETCH_SIZE / WRITE_SIZE counting of roofline.traffic")
+    ap.add_argument("--probe", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--rows", type=int, default=656, choices=[656, 576],
                     help="config 2: 576 times the step over a Row576 cache alone (the row576_variant of the default line)")
     ap.add_argument("--idx-sets", type=int, default=4,
@@ -829,6 +889,9 @@ def main():
                     {"workload": r["workload"]}, {"bound": "hbm", "achieved": r["gbs"], "peak": HBM_PEAK_GBS,
                                                   "unit": "GB/s", "frac": r["frac"], "traffic": None,
                                                   "kernel": r["kernel"]}, detail=r)
+    elif a.config == 2 and a.probe:
+        print(json.dumps(run_probe(a, dev)), flush=True)
+        return
     elif a.config == 2:
         res = run_config2(a, dev)
         if not a.no_variant:
