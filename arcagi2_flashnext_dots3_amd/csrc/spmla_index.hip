@@ -763,13 +763,15 @@ __global__ void __launch_bounds__(TK_NT) topk_kernel(TopkParams p) {
 //            takes its slots with one LDS atomic per pass, so the lists are unordered (the finishing pass orders
 //            by key and column, so the result does not depend on it). Otherwise the
 //            next level narrows the prefix to b, and this pass also builds its chunk's histogram of that level
-//            (into the other half of the histogram buffer, which no workgroup of the row is reading).
+//            (into the other half of the histogram buffer, which no workgroup of the row is reading) and, when the
+//            workspace has the overflow area, writes its chunk's keys in b there (at the offset the level-0
+//            histograms give), so that the next level's collect pass reads those keys instead of the row.
 // A finishing pass (one workgroup per row) resolves the candidates' remaining levels, sorts the K winners and
 // writes the positions. Rows with n <= K, and rows whose bin is still too large after two levels (heavy ties), run
 // the one-workgroup selection there. Per-row state lives in the workspace, one header per level (the collect pass
 // of level L reads header L and its first workgroup writes header L + 1).
 enum : int { TKW_SELECT = 0, TKW_WHOLE = 1, TKW_CANDS = 2, TKW_FALLBACK = 3 };
-struct TkwHdr { int state, prefix, mask, need, sb, binc, lvl, pad; };   // 32 bytes
+struct TkwHdr { int state, prefix, mask, need, sb, binc, lvl, ovf; };   // 32 bytes; ovf: next level reads the overflow list
 
 struct TopkWs {
   int G, CL;                                      // chunks per row, columns per chunk (multiple of 1024)
@@ -801,6 +803,7 @@ struct TopkWsParams {
   const int* ctx; int rows, Lc, K;
   int* out; long long out_st;
   uint8_t* ws; TopkWs w;
+  unsigned long long* ovf;                        // optional overflow lists, G * CL entries per row (or null)
   int level;
 };
 
@@ -898,6 +901,10 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   const int lane = tid & 63;
   const bool narrow = !whole && !fits && p.level + 1 < 2;   // uniform per row: the next level runs on bin b
   const int nshift = tk_shift(p.level + 1);
+  // level 0 narrowing with an overflow area: the chunk's keys in b go to the row's overflow list (at cb, like the
+  // candidates), where level 1 reads them
+  const bool to_ovf = narrow && p.ovf != nullptr;
+  unsigned long long* ovf_row = p.ovf ? p.ovf + (long long)row * p.w.G * p.w.CL : nullptr;
   if (narrow) {
     for (int i = tid; i < TK_HCOPY * TK_HSTR; i += TK_NT) nh[i] = 0;
     __syncthreads();
@@ -910,21 +917,41 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
     h.sb = st.sb + (int)above;
     h.binc = (int)binc;
     h.lvl = p.level + 1;
+    h.ovf = 0;
     if (whole) { h.state = TKW_WHOLE; h.sb = st.sb + (int)need; }
     else if (fits) h.state = TKW_CANDS;
-    else h.state = p.level + 1 < 2 ? TKW_SELECT : TKW_FALLBACK;
+    else { h.state = p.level + 1 < 2 ? TKW_SELECT : TKW_FALLBACK; h.ovf = to_ovf ? 1 : 0; }
     *next = h;
   }
   unsigned long long* sel = p.w.sel(p.ws, row);
-  unsigned long long* cand = p.w.cand(p.ws, row);
+  unsigned long long* cand = to_ovf ? ovf_row : p.w.cand(p.ws, row);
   const void* x = lrow<F16>(p.lg, row, p.lg_st);
-  const int c0 = g * p.w.CL, c1 = min(c0 + p.w.CL, n);
+  // the keys this workgroup visits: logits columns c0 .. c1, or (a level narrowed with an overflow list) entries
+  // c0 .. c1 of the overflow list: the previous level's bin keys of chunk g, at the offset its histograms give
+  int c0 = g * p.w.CL, c1 = min(c0 + p.w.CL, n);
+  const bool from_ovf = st.ovf != 0;
+  if (from_ovf) {
+    const uint32_t* h0 = p.w.hist(p.ws, row) + (long long)((p.level - 1) & 1) * p.w.G * 2048;
+    const uint32_t pb = ((uint32_t)prefix >> tk_shift(p.level - 1)) & 0x7ffu;
+    int o = 0;
+    for (int c = 0; c < g; ++c) o += (int)h0[(long long)c * 2048 + pb];
+    c0 = o;
+    c1 = o + (int)h0[(long long)g * 2048 + pb];
+  }
   for (int base = c0; base < c1; base += 8 * TK_NT) {
     uint32_t k[8];
+    int jj[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int j = base + i * TK_NT + tid;
-      k[i] = j < c1 ? lkey<F16>(x, j) : 0u;
+      if (from_ovf) {
+        const unsigned long long e = j < c1 ? ovf_row[j] : 0ull;
+        k[i] = (uint32_t)(e >> 32);
+        jj[i] = (int)~(uint32_t)e;
+      } else {
+        k[i] = j < c1 ? lkey<F16>(x, j) : 0u;
+        jj[i] = j;
+      }
     }
     uint32_t selm = 0, candm = 0;
 #pragma unroll
@@ -932,7 +959,7 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
       const bool in = base + i * TK_NT + tid < c1 && (k[i] & mask) == prefix;
       const uint32_t d = (k[i] >> shift) & 0x7ffu;
       selm |= (uint32_t)(in && (d > b || (whole && d == b))) << i;
-      candm |= (uint32_t)(in && fits && d == b) << i;
+      candm |= (uint32_t)(in && (fits || to_ovf) && d == b) << i;
     }
     // the lane's slots: an exclusive scan of the counts over the wave, after the wave's block of the chunk's slots
     // (one LDS atomic; both counts stay below 2^16: at most K winners and TK_CAP candidates per chunk)
@@ -950,9 +977,8 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
     uint32_t so = sb + (off & 0xffffu), co = cb + (off >> 16);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int j = base + i * TK_NT + tid;
-      if ((selm >> i) & 1u) sel[so++] = tk_pack(k[i], j);
-      if ((candm >> i) & 1u) cand[co++] = tk_pack(k[i], j);
+      if ((selm >> i) & 1u) sel[so++] = tk_pack(k[i], jj[i]);
+      if ((candm >> i) & 1u) cand[co++] = tk_pack(k[i], jj[i]);
       if (narrow && base + i * TK_NT + tid < c1 && (k[i] & mask) == prefix && ((k[i] >> shift) & 0x7ffu) == b)
         atomicAdd(&nh[(tid & (TK_HCOPY - 1)) * TK_HSTR + ((k[i] >> nshift) & 0x7ffu)], 1u);
     }
@@ -1242,9 +1268,17 @@ int spmla_topk(const void* logits, long long lg_st, const int* ctx, int rows, in
   return (int)hipGetLastError();
 }
 
+// Workspace: the rows' headers, lists and histograms, then (optional) the rows' overflow lists of G * CL entries,
+// used when a chunk's bin count fits the collect pass's 16-bit slot counters (CL < 2^16).
+static long long topk_ws_base(int rows, int Lc) { return (long long)rows * idx::topk_ws_layout(Lc).row_bytes; }
+static long long topk_ws_ovf(int rows, int Lc) {
+  const idx::TopkWs w = idx::topk_ws_layout(Lc);
+  return w.CL < 65536 ? (long long)rows * w.G * w.CL * 8 : 0;
+}
+
 long long spmla_topk_ws_bytes(int rows, int Lc, int K) {
   if (rows < 0 || Lc < 0 || K <= 0) return 0;
-  return (long long)rows * idx::topk_ws_layout(Lc).row_bytes;
+  return topk_ws_base(rows, Lc) + topk_ws_ovf(rows, Lc);
 }
 
 int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
@@ -1253,10 +1287,13 @@ int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows,
   if (K > idx::TK_KMAX) return SPMLA_ELIMIT;
   if (rows == 0) return SPMLA_OK;
   if (!logits || !ctx || !out || !ws) return SPMLA_EARG;
-  if (((uintptr_t)ws & 15) || ws_bytes < spmla_topk_ws_bytes(rows, Lc, K)) return SPMLA_EARG;
+  const long long base = topk_ws_base(rows, Lc), ovf = topk_ws_ovf(rows, Lc);
+  if (((uintptr_t)ws & 15) || ws_bytes < base) return SPMLA_EARG;
   idx::TopkWsParams p;
   p.lg = logits; p.lg_st = lg_st; p.ctx = ctx; p.rows = rows; p.Lc = Lc; p.K = K; p.out = out; p.out_st = out_st;
   p.ws = (uint8_t*)ws; p.w = idx::topk_ws_layout(Lc);
+  // with room for the overflow lists, a level that narrows hands its bin's keys to the next level in a list
+  p.ovf = ovf > 0 && ws_bytes >= base + ovf ? (unsigned long long*)((uint8_t*)ws + base) : nullptr;
   if (dtype == 1) idx::topk_ws_passes<true>(p, (hipStream_t)stream);
   else idx::topk_ws_passes<false>(p, (hipStream_t)stream);
   return (int)hipGetLastError();
@@ -1270,9 +1307,10 @@ int spmla_topk_scratch(const void* logits, long long lg_st, const int* ctx, int 
   if (K > idx::TK_KMAX) return SPMLA_ELIMIT;
   if (rows == 0) return SPMLA_OK;
   if (!logits || !ctx || !out) return SPMLA_EARG;
-  const long long need = spmla_topk_ws_bytes(rows, Lc, K);
-  if (need <= 0) return SPMLA_EARG;
-  if (need > idx::TOPK_SCRATCH_BYTES) return SPMLA_ELIMIT;   // beyond the fixed scratch: use spmla_topk_ws
+  const long long full = spmla_topk_ws_bytes(rows, Lc, K), base = topk_ws_base(rows, Lc);
+  if (full <= 0) return SPMLA_EARG;
+  if (base > idx::TOPK_SCRATCH_BYTES) return SPMLA_ELIMIT;   // beyond the fixed scratch: use spmla_topk_ws
+  const long long need = full <= idx::TOPK_SCRATCH_BYTES ? full : base;   // the overflow lists when they fit
   void* ws = nullptr;
   const int rc = scratch_ptr(&ws);
   if (rc != SPMLA_OK) return rc;

@@ -229,9 +229,10 @@ def _attn_counter_bytes(T, H):
     return (4 * T * ((H + 127) // 128) + 255) // 256 * 256
 
 
-def topk(logits, ctx, K, out=None, single_pass=False):
+def topk(logits, ctx, K, out=None, single_pass=False, ws=None):
     """logits [rows, Lc] fp32 or fp16, ctx [rows] int32 -> [rows, K] int32 positions (value desc, position asc; -1
-    pad). Several workgroups per row (spmla_topk_ws) unless single_pass (spmla_topk, one workgroup per row)."""
+    pad). Several workgroups per row (spmla_topk_ws; ws: a uint8 workspace, else a cached one of
+    spmla_topk_ws_bytes) unless single_pass (spmla_topk, one workgroup per row)."""
     rows, Lc = logits.shape
     _need(logits.dtype in _LG_DT and logits.stride(1) == 1, "fp32 / fp16 logits with contiguous rows")
     _need(ctx.dtype == torch.int32 and ctx.is_contiguous(), "ctx int32")
@@ -244,7 +245,8 @@ def topk(logits, ctx, K, out=None, single_pass=False):
                   out.stride(0), _LG_DT[logits.dtype], _stream(logits))
         return out
     nb = int(_lib.lib().spmla_topk_ws_bytes(rows, Lc, K))
-    ws, _ = _workspace("topk", logits.device, nb)
+    if ws is None:
+        ws, _ = _workspace("topk", logits.device, nb)
     _lib.call("spmla_topk_ws", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K, out.data_ptr(),
               out.stride(0), ws.data_ptr(), ws.numel(), _LG_DT[logits.dtype], _stream(logits))
     return out

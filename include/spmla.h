@@ -70,13 +70,16 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
 int spmla_topk(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
                long long out_st, int dtype, void* stream);
 
-/* Bytes of workspace spmla_topk_ws needs for rows x Lc (0 for invalid sizes). */
+/* Bytes of workspace spmla_topk_ws uses for rows x Lc (0 for invalid sizes): the per-row state, lists and histograms,
+ * then the overflow lists (8 bytes per column) through which a narrowing level hands its boundary bin's keys to the
+ * next level instead of that level reading the row again. */
 long long spmla_topk_ws_bytes(int rows, int Lc, int K);
 
 /* spmla_topk with the same result, spread over several workgroups per row: a histogram pass and a collect pass over
  * chunks of 8192 or more columns (at most 8 chunks per row), then one workgroup per row that resolves the boundary bin
- * and sorts. ws: device memory of at least spmla_topk_ws_bytes(rows, Lc, K) bytes, 16-byte aligned, any contents
- * (every pass writes what the next reads); calls that share a workspace must not overlap. Same replacement as
+ * and sorts. ws: device memory of spmla_topk_ws_bytes(rows, Lc, K) bytes (a smaller one without the overflow lists is
+ * accepted: the second level then reads the row again), 16-byte aligned, any contents (every pass writes what the
+ * next reads); calls that share a workspace must not overlap. Same replacement as
  * spmla_topk (fast_topk.local + merge at P = 1, dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:52-78;
  * csrc/topk_select.cu:251-286; shard_indexer.py:194-221). */
 int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
@@ -85,8 +88,8 @@ int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows,
 /* spmla_topk_ws without a caller workspace and without any allocation: the passes use the library's own
  * fixed device scratch (a file-scope array of spmla_topk_scratch_bytes() = 16 MiB per GPU, held from library load
  * until the process ends; its device address is looked up once per device on the first call there). Same result
- * as spmla_topk_ws. Sizes whose workspace (spmla_topk_ws_bytes) exceeds the scratch return SPMLA_ELIMIT (e.g. 64 rows
- * fit at any Lc up to 2^31). All calls on one GPU share the scratch: calls that overlap on one GPU (other streams,
+ * as spmla_topk_ws (the overflow lists included when they fit the scratch). Sizes whose workspace without the
+ * overflow lists exceeds the scratch return SPMLA_ELIMIT (e.g. 64 rows fit at any Lc up to 2^31). All calls on one GPU share the scratch: calls that overlap on one GPU (other streams,
  * other threads) race and must not be issued. The scratch keeps the last call's contents; the passes need no
  * particular initial contents. No counterpart in the reference: for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). */

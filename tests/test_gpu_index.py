@@ -51,15 +51,19 @@ def test_index_logits(dev, rows, L, seed):
 
 
 def _topk_check(dev, lg, ctx, K):
-    """Both top-k paths (several workgroups per row with a workspace; one workgroup per row) against the oracle."""
-    from arcagi2_flashnext_dots3_amd import kernels
+    """The top-k paths against the oracle: several workgroups per row with the full workspace (a narrowing level
+    hands its bin's keys to the next in the overflow lists), the same with a workspace too small for those lists (the
+    next level reads the row again), and one workgroup per row."""
+    from arcagi2_flashnext_dots3_amd import _lib, kernels
     exp = ref.topk(lg, ctx, K)
-    for single in (False, True):
-        out = kernels.topk(torch.from_numpy(lg).to(dev), torch.from_numpy(ctx).to(dev), K, single_pass=single)
+    nb = int(_lib.lib().spmla_topk_ws_bytes(lg.shape[0], lg.shape[1], K))
+    small = torch.empty(nb - 16, dtype=torch.uint8, device=dev)
+    for single, ws in ((False, None), (False, small), (True, None)):
+        out = kernels.topk(torch.from_numpy(lg).to(dev), torch.from_numpy(ctx).to(dev), K, single_pass=single, ws=ws)
         torch.cuda.synchronize()
         got = out.cpu().numpy()
         bad = np.where((got != exp).any(1))[0]
-        assert bad.size == 0, f"single_pass={single}: rows {bad[:8]} differ"
+        assert bad.size == 0, f"single_pass={single} ws={'small' if ws is not None else 'full'}: rows {bad[:8]} differ"
 
 
 def test_topk_random_and_lengths(dev):

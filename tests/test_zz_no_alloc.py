@@ -27,7 +27,8 @@ def test_topk_scratch_matches_workspace(dev):
     for step, (rows, L, K) in enumerate([(64, 131072, 2048), (9, 20000, 1024)]):
         lg, ctx = _logits(rows, L, 40 + step)
         print(f"[no-alloc topk] call {step}: rows={rows} L={L} K={K}", flush=True)
-        assert lib.spmla_topk_ws_bytes(rows, L, K) <= lib.spmla_topk_scratch_bytes()
+        # (the first call's overflow lists do not fit the scratch: it runs without them, re-reading the row at the
+        # second level, while the workspace path below uses them; both are exact)
         dl, dc = lg.to(dev), ctx.to(dev)
         got = kernels.topk_scratch(dl, dc, K)
         exp = kernels.topk(dl, dc, K)                 # spmla_topk_ws with its own workspace
@@ -43,7 +44,7 @@ def test_topk_scratch_matches_workspace(dev):
 def test_topk_scratch_rejects_oversize(dev):
     from arcagi2_flashnext_dots3_amd import _lib, kernels
     lib = _lib.lib()
-    rows, L, K = 128, 131072, 2048                  # 128 x 180 KB of workspace > 16 MiB
+    rows, L, K = 128, 131072, 2048                  # 128 x 180 KB of workspace > 16 MiB, even without overflow lists
     assert lib.spmla_topk_ws_bytes(rows, L, K) > lib.spmla_topk_scratch_bytes()
     lg = torch.zeros(rows, L, device=dev)
     ctx = torch.full((rows,), L, dtype=torch.int32, device=dev)
