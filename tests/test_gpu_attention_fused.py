@@ -164,3 +164,59 @@ def test_graph_capture_ascending_batches(dev):
             o, l = kernels.attend(qs[1 - n], pool, ids[1 - n], sm)       # eager work between the replays
             torch.cuda.synchronize()
             assert torch.equal(o, eager[1 - n][0]) and torch.equal(l, eager[1 - n][1])
+
+
+def test_auto_split_large_k_single_token(dev):
+    """One token over K = 20000 rows with the default split: auto_split returns 1 (every split of 8 would exceed the
+    split kernel's 2048-row limit), so the head-group kernel takes any K; the result matches the fp64 oracle."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    T, H, R, K = 1, 128, 30000, 20000
+    assert kernels.auto_split(T, H, K) == 1
+    pool = make_pool_656(R, seed=71)[0]
+    q = make_q(T, H, seed=72)
+    idx = distinct_idx(T, K, R, seed=73)
+    sm = 192 ** -0.5
+    print("[fused] T=1 K=20000 default split", flush=True)
+    o, l = _run(dev, q, pool, idx, sm)
+    o_ref, l_ref = ref.attention(q.float().numpy(), pool, idx.numpy(), sm)
+    _vs_oracle(o, l, o_ref, l_ref)
+
+
+def test_first_launches_from_two_threads(dev):
+    """The first attention launches of a fresh process, issued from two host threads at once (the per-device dynamic
+    LDS attribute is set under a lock by whichever thread comes first): both results equal a later single-threaded
+    launch bit for bit."""
+    import os
+    import subprocess
+    import sys
+    code = r"""
+import threading, torch, sys
+sys.path.insert(0, %r)
+from arcagi2_flashnext_dots3_amd import kernels
+from tests.helpers import make_pool_656, make_q, distinct_idx
+dev = torch.device("cuda:0")
+pool = torch.from_numpy(make_pool_656(3000, seed=81)[0]).to(dev)
+q = make_q(8, 128, seed=82).to(dev)
+idx = distinct_idx(8, 512, 3000, seed=83).to(dev)
+res, err = [None, None], []
+def go(i):
+    try:
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            o, l = kernels.attend(q, pool, idx, 192 ** -0.5, split=1)
+        s.synchronize()
+        res[i] = (o, l)
+    except Exception as e:
+        err.append(repr(e))
+ts = [threading.Thread(target=go, args=(i,)) for i in range(2)]
+[t.start() for t in ts]; [t.join() for t in ts]
+assert not err, err
+o, l = kernels.attend(q, pool, idx, 192 ** -0.5, split=1)
+torch.cuda.synchronize()
+for r in res:
+    assert torch.equal(r[0], o) and torch.equal(r[1], l)
+print("two-thread first launches ok")
+""" % os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("[fused] first launches from two threads (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "two-thread first launches ok" in r.stdout, (r.stdout[-500:], r.stderr[-1500:])
