@@ -48,7 +48,7 @@ constexpr int L_QROPE = NW * NBUF * TILE;      // 135168
 constexpr int L_ML = L_QROPE + HG * QRS;       // 156160: per wave m[32], l[32]
 constexpr int L_TOTAL = L_ML + NW * 64 * 4;    // 157184
 static_assert(L_TOTAL <= 160 * 1024, "LDS budget");
-static_assert(NW * 8 * 4 * 64 * 16 <= L_QROPE, "merge staging (8 output tiles per wave) fits the tile buffers");
+static_assert(8 * 4 * 64 * 16 <= NBUF * TILE, "merge staging (8 output tiles) fits a wave's tile buffers");
 
 // e4m3 pairs -> bf16 / f16 pairs (exact), through the compiler builtins so that the hazard recognizer sees the
 // VALU writes that feed MFMA operands. The packed result is bit-cast whole (extracting single bf16 lanes from
@@ -520,10 +520,29 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     mcur = mnxt;
   }
 
-  // ---- merge the 4 waves: per head M = max m_w, L = sum l_w 2^(m_w - M), O = sum O_w 2^(m_w - M) / L
+  // ---- merge the 4 waves: per head M = max m_w, L = sum l_w 2^(m_w - M), O = sum O_w 2^(m_w - M) / L.
+  // Two rounds of 8 output tiles (32 dims x 32 heads each): every wave stages its 8 tiles of the round, unscaled, in
+  // its own tile buffers ([tile][qd][lane] f32x4, 32 KiB), which no other wave reads or copies into during the loop,
+  // and wave w then reduces tiles 8r + 2w, 8r + 2w + 1 over the four waves. Round 0 is staged as soon as the wave's
+  // own loop ends (its last copy landed at the top of its last tile), so only the slowest wave's staging follows
+  // the barrier. (Keeping the reducing wave's own share in registers instead makes the compiler copy the whole
+  // accumulator out of AGPRs at the loop exit.)
   l_run += __shfl_xor(l_run, 32, 64);
   SPMLA_LDS float* s_ml = (SPMLA_LDS float*)(lds + L_ML);
-  lds_barrier();                                 // every wave is done with its tiles (no copy in flight)
+  auto xo_at = [&](int v, int lb, int qd) -> SPMLA_LDS f32x4* {
+    return (SPMLA_LDS f32x4*)(lds + L_TILES + v * NBUF * TILE) + (lb * 4 + qd) * 64 + lane;
+  };
+  auto stage = [&](int rnd) {
+#pragma unroll
+    for (int lb = 0; lb < 8; ++lb) {
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x16& o = O[8 * rnd + lb];
+        *xo_at(w, lb, qd) = f32x4{o[4 * qd], o[4 * qd + 1], o[4 * qd + 2], o[4 * qd + 3]};
+      }
+    }
+  };
+  stage(0);
   // the wave's (O, l_run) are relative to 2^(m_run + eps)
   if (half == 0) { s_ml[w * 64 + l32] = m_run > -__builtin_inff() ? m_run + (float)eps : m_run; s_ml[w * 64 + 32 + l32] = l_run; }
   lds_barrier();
@@ -559,32 +578,27 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
 #pragma unroll
   for (int v = 0; v < NW; ++v) fv[v] *= inv;
 
-  SPMLA_LDS f32x4* xo = (SPMLA_LDS f32x4*)(lds + L_TILES);   // [wave][tile 0..7][qd][lane]
   // output head of this lane, recomputed from the lane id (cheaper than keeping it live across the loop)
   const int oc = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31);
   const int ho = col_head(oc), to = col_tok(oc);
   const bool hoval = col_ok(oc);
 #pragma unroll
   for (int rnd = 0; rnd < 2; ++rnd) {
-#pragma unroll
-    for (int b = 0; b < 8; ++b)
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x16& o = O[8 * rnd + b];
-        xo[((w * 8 + b) * 4 + qd) * 64 + lane] = f32x4{o[4 * qd], o[4 * qd + 1], o[4 * qd + 2], o[4 * qd + 3]};
-      }
-    lds_barrier();
-    // wave w reduces output tiles 2w, 2w + 1 of this round and writes them
+    if (rnd == 1) {
+      lds_barrier();                               // round 0's tiles are read
+      stage(1);
+      lds_barrier();
+    }
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) {
-      const int b = 2 * w + bb;
-      const int mt = 8 * rnd + b;
+      const int lb = 2 * w + bb;
+      const int mt = 8 * rnd + lb;
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int v = 0; v < NW; ++v) {
-          const f32x4 x = xo[((v * 8 + b) * 4 + qd) * 64 + lane];
+          const f32x4 x = *xo_at(v, lb, qd);
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(x[e], fv[v], acc[e]);
         }
@@ -605,7 +619,6 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
         }
       }
     }
-    lds_barrier();
   }
   if (w == 0 && half == 0 && hoval) {
     if (p.opart == nullptr) p.lse[(long long)to * p.lse_st + ho] = lse_v;
