@@ -17,10 +17,11 @@
 //   -1 where the value is +-inf and in slots >= n. fp32 or fp16 logits: an fp16 key is the same order key of the
 //   16-bit pattern placed in the top half of the 32-bit key (low half zero), so one radix code serves both.
 //   gfx950: one 1024-thread workgroup per row, the row's keys in VGPRs (32 per thread, all loads in flight):
-//   11/11/10-bit radix levels with an LDS histogram; keys above the boundary bin are appended with one LDS atomic
-//   per wave; once the boundary bin holds at most TK_CAP keys the remaining levels run on those candidates alone;
-//   ties on the final key take the lowest columns. The K winners are bitonic-sorted in LDS (only the stages whose
-//   pairs cross waves take a workgroup barrier).
+//   11/11/10-bit radix levels with an LDS histogram; keys above the boundary bin are appended at slots from a block
+//   scan of per-thread counts (wave scans on DPP); once the boundary bin holds at most TK_CAP keys the remaining
+//   levels run on those candidates alone; ties on the final key take the lowest columns. The K winners are
+//   bitonic-sorted in LDS (only the stages whose pairs cross waves take a workgroup barrier); on the several-
+//   workgroup path, whose lists arrive in column order, fp16 winners are ordered by a stable radix sort instead.
 #include "spmla_common.h"
 #include <limits.h>
 
@@ -272,33 +273,52 @@ __device__ inline const void* lrow(const void* lg, int row, long long st) {
   return (const uint8_t*)lg + (long long)row * st * (F16 ? 2 : 4);
 }
 
-// block-wide exclusive scan of a per-thread count (1024 threads = 16 waves)
+// Inclusive prefix sum over the 64 lanes of a wave on the VALU: DPP row shifts 1, 2, 4, 8 scan each 16-lane row,
+// then row_bcast:15 adds row 0's total to row 1 and row 2's to row 3, and row_bcast:31 adds rows 0-1's total to rows
+// 2 and 3 (gfx9 DPP controls). A lane whose DPP source is outside its row adds 0.
+__device__ inline uint32_t wave_incl_scan(uint32_t x) {
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false);   // row_shr:1
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false);   // row_shr:2
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false);   // row_shr:4
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false);   // row_shr:8
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);   // row_bcast:15, rows 1, 3
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);   // row_bcast:31, rows 2, 3
+  return x;
+}
+// Minimum / maximum over the wave (uniform result): quad permutations and row mirrors within each 16-lane row,
+// then the four rows' results through readlane.
+template <bool MAX>
+__device__ inline uint32_t wave_minmax(uint32_t x) {
+  auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xb1, 0xf, 0xf, false));   // quad_perm [1, 0, 3, 2]
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4e, 0xf, 0xf, false));   // quad_perm [2, 3, 0, 1]
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x140, 0xf, 0xf, false));  // row_mirror
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+  return op(op(a, b), op(c, d));
+}
+
+// block-wide exclusive scan of a per-thread count (1024 threads = 16 waves): wave scans on the VALU, the 16 wave
+// totals through LDS (wsum: 16-byte aligned, 16 words); every thread sums the totals of the waves before its own
 __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* wsum, uint32_t* total) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  uint32_t inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t t = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += t;
-  }
+  const uint32_t inc = wave_incl_scan(v);
   if (lane == 63) wsum[wv] = inc;
   __syncthreads();
-  if (wv == 0) {
-    const uint32_t w = lane < TK_NT / 64 ? wsum[lane] : 0u;
-    uint32_t wi = w;
+  uint32_t before = 0u, tot = 0u;
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      const uint32_t t = __shfl_up(wi, o, 64);
-      if (lane >= o) wi += t;
+  for (int q = 0; q < TK_NT / 256; ++q) {
+    const u32x4 s4 = ((const u32x4*)wsum)[q];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      before += 4 * q + e < wv ? s4[e] : 0u;
+      tot += s4[e];
     }
-    if (lane < TK_NT / 64) wsum[lane] = wi - w;
-    if (lane == TK_NT / 64 - 1) wsum[16] = wi;
   }
-  __syncthreads();
-  const uint32_t r = wsum[wv] + inc - v;
-  *total = wsum[16];
-  __syncthreads();
-  return r;
+  *total = tot;
+  __syncthreads();                                   // wsum is free for the next scan
+  return before + inc - v;
 }
 
 // bitonic sort of n (power of two) uint64 in LDS, descending. Thread t handles pairs t, t + 1024, ...; for a
@@ -464,7 +484,7 @@ struct TopkLds {
   uint32_t hist[TK_HCOPY * TK_HSTR];
   unsigned long long sel[TK_KMAX];
   unsigned long long cand[TK_CAP];
-  uint32_t wsum[17];
+  __attribute__((aligned(16))) uint32_t wsum[17];
   uint32_t sh[8];
 };
 
@@ -536,8 +556,8 @@ __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, ui
   int t = tid;                                       // opaque copy: keeps the slot indices from being hoisted
   asm volatile("" : "+v"(t));
 #pragma unroll
-  for (int i = 0; i < TK_EPT; ++i) {
-    const int c = t + i * TK_NT;
+  for (int i = 0; i < TK_EPT; ++i) {              // consecutive candidates: the winners appended below keep their
+    const int c = TK_EPT * t + i;                  // order in L.cand (column order for the workspace path)
     vm |= (uint32_t)(c < nc) << i;
     e[i] = c < nc ? L.cand[c] : 0ull;
   }
@@ -736,6 +756,102 @@ __device__ __forceinline__ void tk_emit_sorted(const Src& src, int nsel, int kou
   }
 }
 
+// Stable LSD radix sort of L.sel[0, n) (n <= 2048) by key (the high word) descending, then the emit of
+// tk_emit_sorted. Entries with equal keys keep their order in L.sel, so lists appended in column order come out
+// (key desc, column asc) with no sort on the columns. Keys are offset by the smallest key, and only the bytes that
+// the offsets span are sorted (fp16 keys: their low half is zero). One pass: wave-local stable ranks from 16 ballots
+// (entries 2t, 2t + 1 of thread t, waves in order), per-wave digit counts, one scan over (digit, wave), a scatter.
+// LDS: L.cand as the scatter buffer, L.hist for the counts and offsets.
+template <class Src, bool F16>
+__device__ __forceinline__ void tk_emit_radix(const Src& src, int n, int kout, int* o, TopkLds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  unsigned long long* tmp = L.cand;
+  uint32_t* whist = L.hist;                      // [digit][wave] counts of the pass
+  uint32_t* woff = L.hist + 4096;                // [digit][wave] first slot of the wave's entries of the digit
+  uint32_t* red = (uint32_t*)(L.cand + TK_KMAX); // 16 waves x (min, max)
+  static_assert(2 * 4096 <= TK_HCOPY * TK_HSTR && TK_CAP >= TK_KMAX + 16, "radix sort LDS");
+  for (int i = tid; i < 4096; i += TK_NT) whist[i] = 0u;
+  const bool v0 = 2 * tid < n, v1 = 2 * tid + 1 < n;   // entries past n: zero, sorted last
+  unsigned long long x0 = v0 ? L.sel[2 * tid] : 0ull, x1 = v1 ? L.sel[2 * tid + 1] : 0ull;
+  uint32_t kmn = 0xffffffffu, kmx = 0u;
+  if (v0) { kmn = (uint32_t)(x0 >> 32); kmx = kmn; }
+  if (v1) { kmn = min(kmn, (uint32_t)(x1 >> 32)); kmx = max(kmx, (uint32_t)(x1 >> 32)); }
+  kmn = wave_minmax<false>(kmn);
+  kmx = wave_minmax<true>(kmx);
+  if (lane == 0) { red[2 * wv] = kmn; red[2 * wv + 1] = kmx; }
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < TK_NT / 64; ++v) { kmn = min(kmn, red[2 * v]); kmx = max(kmx, red[2 * v + 1]); }
+  const uint32_t range = kmx > kmn ? kmx - kmn : 0u;
+  const int first = F16 ? 2 : 0;                 // lowest byte that can differ
+  const int last = range ? (31 - __builtin_clz(range)) >> 3 : -1;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  for (int byte = first; byte <= last; ++byte) {   // uniform
+    const int sh = 8 * byte;
+    // padding entries (key 0: every real key is at least -inf's 0x007fffff) take digit 255 in every pass
+    const uint32_t k0 = (uint32_t)(x0 >> 32), k1 = (uint32_t)(x1 >> 32);
+    const uint32_t d0 = k0 ? 255u - ((k0 - kmn) >> sh & 255u) : 255u;
+    const uint32_t d1 = k1 ? 255u - ((k1 - kmn) >> sh & 255u) : 255u;
+    // lanes whose entry 0 / entry 1 has this lane's digit d0 (ma / mb) or d1 (mc / md)
+    unsigned long long ma = ~0ull, mb = ~0ull, mc = ~0ull, md = ~0ull;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const unsigned long long b0 = __ballot((d0 >> k) & 1u), b1 = __ballot((d1 >> k) & 1u);
+      const unsigned long long s0 = (unsigned long long)(long long)-(int)((d0 >> k) & 1u);
+      const unsigned long long s1 = (unsigned long long)(long long)-(int)((d1 >> k) & 1u);
+      ma &= ~(b0 ^ s0); mb &= ~(b1 ^ s0); mc &= ~(b0 ^ s1); md &= ~(b1 ^ s1);
+    }
+    // stable rank among the wave's entries of the same digit (order: lane, then entry)
+    const uint32_t r0 = (uint32_t)(__popcll(ma & below) + __popcll(mb & below));
+    const uint32_t r1 = (uint32_t)(__popcll(mc & below) + __popcll(md & below)) + (d0 == d1 ? 1u : 0u);
+    if (r0 == 0u) whist[d0 * 16 + wv] = (uint32_t)(__popcll(ma) + __popcll(mb));
+    if (r1 == 0u) whist[d1 * 16 + wv] = (uint32_t)(__popcll(mc) + __popcll(md));
+    __syncthreads();
+    uint32_t c[16], tot = 0u, incl = 0u;
+    if (tid < 256) {                              // digit tid: offsets over the waves, then over the digits
+      u32x4* hp = (u32x4*)(whist + tid * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 v = hp[q];
+        hp[q] = u32x4{0u, 0u, 0u, 0u};           // cleared for the next pass
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { c[4 * q + e] = tot; tot += v[e]; }
+      }
+      incl = wave_incl_scan(tot);
+      if (lane == 63) L.wsum[wv] = incl;
+    }
+    __syncthreads();
+    if (tid < 256) {
+      uint32_t bse = incl - tot;
+      for (int v = 0; v < wv; ++v) bse += L.wsum[v];
+      u32x4* op = (u32x4*)(woff + tid * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) op[q] = u32x4{bse + c[4 * q], bse + c[4 * q + 1], bse + c[4 * q + 2], bse + c[4 * q + 3]};
+    }
+    __syncthreads();
+    tmp[woff[d0 * 16 + wv] + r0] = x0;
+    tmp[woff[d1 * 16 + wv] + r1] = x1;
+    __syncthreads();
+    x0 = tmp[2 * tid];
+    x1 = tmp[2 * tid + 1];
+  }
+  // entries 2t, 2t + 1 of the sorted order are in this thread's registers
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int slot = 2 * tid + e;
+    if (slot < kout) {
+      int r = -1;
+      const unsigned long long x = e ? x1 : x0;
+      if (slot < n) {
+        const uint32_t key = (uint32_t)(x >> 32);
+        const int j = (int)(~(uint32_t)x);
+        if (!Src::inf(key)) r = src.id(j);
+      }
+      o[slot] = r;
+    }
+  }
+}
+
 struct TopkParams {
   const void* lg; long long lg_st;                // fp32 or fp16 (the kernel's F16), stride in elements
   const int* ctx; int rows, Lc, K;
@@ -760,8 +876,8 @@ __global__ void __launch_bounds__(TK_NT) topk_kernel(TopkParams p) {
 //            remaining need; it writes its chunk's keys above b (and in b when that completes the need) to the row's
 //            winner list, and the keys in b to the candidate list when the bin holds at most TK_CAP keys. A chunk's
 //            entries start at the offset the histograms of the chunks before it give; inside the chunk each wave
-//            takes its slots with one LDS atomic per pass, so the lists are unordered (the finishing pass orders
-//            by key and column, so the result does not depend on it). Otherwise the
+//            takes its slots from a block scan per pass over 8 consecutive columns per thread, so every list is
+//            in column order (the finishing pass's stable radix sort of fp16 keys relies on it). Otherwise the
 //            next level narrows the prefix to b, and this pass also builds its chunk's histogram of that level
 //            (into the other half of the histogram buffer, which no workgroup of the row is reading) and, when the
 //            workspace has the overflow area, writes its chunk's keys in b there (at the offset the level-0
@@ -856,10 +972,9 @@ __global__ void __launch_bounds__(TK_NT) topk_hist_kernel(TopkWsParams p) {
 
 template <bool F16>
 __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
-  __shared__ uint32_t wsum[17];
+  __shared__ __attribute__((aligned(16))) uint32_t wsum[17];
   __shared__ uint32_t sh[8];
   __shared__ uint32_t nh[TK_HCOPY * TK_HSTR];       // the next level's histogram of this chunk (when narrowing)
-  __shared__ uint32_t wcnt;                         // slots taken in the chunk: winners (low 16 bits), candidates
   const int row = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
   const int n = tkw_n(p, row);
   if (n <= p.K) return;
@@ -895,10 +1010,8 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   (void)block_excl_scan(mine, wsum, &sum);
   if ((uint32_t)b0 == b) sh[4] = q0;
   if ((uint32_t)b1 == b) sh[4] = q1;
-  if (tid == 0) wcnt = 0u;
   __syncthreads();
   const uint32_t sb = (uint32_t)st.sb + sum, cb = sh[4];   // this chunk's first winner / candidate slot
-  const int lane = tid & 63;
   const bool narrow = !whole && !fits && p.level + 1 < 2;   // uniform per row: the next level runs on bin b
   const int nshift = tk_shift(p.level + 1);
   // level 0 narrowing with an overflow area: the chunk's keys in b go to the row's overflow list (at cb, like the
@@ -938,48 +1051,61 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
     c0 = o;
     c1 = o + (int)h0[(long long)g * 2048 + pb];
   }
+  // thread t visits the 8 consecutive entries 8t .. 8t + 7 of each 8192-entry pass, and the slots of a pass come
+  // from one block scan of the per-thread counts: every list the pass appends to stays in column order (the
+  // finishing pass's stable sort relies on it to order equal keys by column)
+  const bool vec = !from_ovf && ((uintptr_t)x & 15u) == 0u;   // 16-byte aligned row: vector loads
+  uint32_t sbase = sb, cbase = cb;                  // running slot bases of this chunk's lists
   for (int base = c0; base < c1; base += 8 * TK_NT) {
     uint32_t k[8];
     int jj[8];
+    const int j0 = base + 8 * tid;
+    if (from_ovf) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int j = base + i * TK_NT + tid;
-      if (from_ovf) {
-        const unsigned long long e = j < c1 ? ovf_row[j] : 0ull;
+      for (int i = 0; i < 8; ++i) {
+        const unsigned long long e = j0 + i < c1 ? ovf_row[j0 + i] : 0ull;
         k[i] = (uint32_t)(e >> 32);
         jj[i] = (int)~(uint32_t)e;
+      }
+    } else if (vec && j0 + 8 <= c1) {
+      if constexpr (F16) {
+        const u32x4 v = *(const u32x4*)((const uint16_t*)x + j0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { k[2 * i] = okey16(v[i] & 0xffffu); k[2 * i + 1] = okey16(v[i] >> 16); }
       } else {
-        k[i] = j < c1 ? lkey<F16>(x, j) : 0u;
-        jj[i] = j;
+        const f32x4 a = *(const f32x4*)((const float*)x + j0), b = *(const f32x4*)((const float*)x + j0 + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { k[i] = okey(a[i]); k[4 + i] = okey(b[i]); }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) jj[i] = j0 + i;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        k[i] = j0 + i < c1 ? lkey<F16>(x, j0 + i) : 0u;
+        jj[i] = j0 + i;
       }
     }
-    uint32_t selm = 0, candm = 0;
+    uint32_t selm = 0, candm = 0, binm = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const bool in = base + i * TK_NT + tid < c1 && (k[i] & mask) == prefix;
+      const bool in = j0 + i < c1 && (k[i] & mask) == prefix;
       const uint32_t d = (k[i] >> shift) & 0x7ffu;
       selm |= (uint32_t)(in && (d > b || (whole && d == b))) << i;
       candm |= (uint32_t)(in && (fits || to_ovf) && d == b) << i;
+      binm |= (uint32_t)(in && d == b) << i;
     }
-    // the lane's slots: an exclusive scan of the counts over the wave, after the wave's block of the chunk's slots
-    // (one LDS atomic; both counts stay below 2^16: at most K winners and TK_CAP candidates per chunk)
-    const uint32_t cntv = (uint32_t)__popc(selm) | ((uint32_t)__popc(candm) << 16);
-    uint32_t inc = cntv;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t t = __shfl_up(inc, o, 64);
-      if (lane >= o) inc += t;
-    }
-    uint32_t wb = 0u;
-    if (lane == 63) wb = atomicAdd(&wcnt, inc);
-    wb = __shfl(wb, 63, 64);
-    const uint32_t off = wb + inc - cntv;
-    uint32_t so = sb + (off & 0xffffu), co = cb + (off >> 16);
+    // both counts stay below 2^16: a pass holds 8192 entries
+    uint32_t tot;
+    const uint32_t off = block_excl_scan((uint32_t)__popc(selm) | ((uint32_t)__popc(candm) << 16), wsum, &tot);
+    uint32_t so = sbase + (off & 0xffffu), co = cbase + (off >> 16);
+    sbase += tot & 0xffffu;
+    cbase += tot >> 16;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       if ((selm >> i) & 1u) sel[so++] = tk_pack(k[i], jj[i]);
       if ((candm >> i) & 1u) cand[co++] = tk_pack(k[i], jj[i]);
-      if (narrow && base + i * TK_NT + tid < c1 && (k[i] & mask) == prefix && ((k[i] >> shift) & 0x7ffu) == b)
+      if (narrow && ((binm >> i) & 1u))
         atomicAdd(&nh[(tid & (TK_HCOPY - 1)) * TK_HSTR + ((k[i] >> nshift) & 0x7ffu)], 1u);
     }
   }
@@ -1022,6 +1148,12 @@ __global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
     if (st.state == TKW_CANDS)
       tk_resolve_cands(L, st.binc, st.lvl, (uint32_t)st.prefix, (uint32_t)st.mask, (uint32_t)st.need,
                        (uint32_t)st.sb, n);
+    if constexpr (F16) {
+      // fp16 keys: at most two radix passes (the keys' low half is zero), faster than the bitonic network here;
+      // fp32 keys need three or four, slower than it (measured on the bench's indexer logits)
+      tk_emit_radix<RowSrc<F16>, F16>(src, p.K, p.K, o, L);   // the lists arrive in column order
+      return;
+    }
     nsel = p.K;
   }
   tk_emit_sorted(src, nsel, p.K, o, L);
