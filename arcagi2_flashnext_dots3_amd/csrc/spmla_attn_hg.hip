@@ -79,6 +79,13 @@ __device__ inline uint32_t pk_bf16(float a, float b) {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
+// The value of lane l ^ 32 (v_permlane32_swap: one VALU op; __shfl_xor would be an LDS round trip per tile).
+__device__ inline float half_swap(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (__lane_id() & 32) ? r[0] : r[1]);
+}
+
 // QK MFMAs with the accumulator in VGPRs. The compiler builtin puts every MFMA result in AGPRs when the function
 // uses AGPRs, which here would evict part of the PV accumulator around each QK phase; inline asm pins the QK
 // accumulator (read by the scale FMAs) to VGPRs. Hazards the compiler cannot see inside asm are covered here:
@@ -415,7 +422,7 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
     float mx = S[0];
 #pragma unroll
     for (int i = 1; i < 16; ++i) mx = fmaxf(mx, S[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;             // c > 0; -inf stays -inf
+    mx = fmaxf(mx, half_swap(mx)) * c;                      // c > 0; -inf stays -inf
     const bool need = mx > m_run + TAU;                      // also true for the first finite tile
     if (__ballot(need)) {
       const float mn = need ? mx : m_run;
@@ -527,7 +534,7 @@ __global__ void __launch_bounds__(256, 1) attn_kernel(Params p) {
   // own loop ends (its last copy landed at the top of its last tile), so only the slowest wave's staging follows
   // the barrier. (Keeping the reducing wave's own share in registers instead makes the compiler copy the whole
   // accumulator out of AGPRs at the loop exit.)
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run += half_swap(l_run);
   SPMLA_LDS float* s_ml = (SPMLA_LDS float*)(lds + L_ML);
   auto xo_at = [&](int v, int lb, int qd) -> SPMLA_LDS f32x4* {
     return (SPMLA_LDS f32x4*)(lds + L_TILES + v * NBUF * TILE) + (lb * 4 + qd) * 64 + lane;

@@ -24,16 +24,14 @@
 //   workgroup path, whose lists arrive in column order, fp16 winners are ordered by a stable radix sort instead.
 #include "spmla_common.h"
 #include <limits.h>
+#include <algorithm>
 
 namespace spmla {
 namespace idx {
 
 // ------------------------------------------------------------------------------------------------ logits
-#ifndef SPMLA_LG_TPW
-#define SPMLA_LG_TPW 8
-#endif
-constexpr int LG_TPW = SPMLA_LG_TPW;      // 32-key tiles per wave (any value >= 1; 8 measured best, build-time knob)
-constexpr int LG_KPB = 4 * LG_TPW * 32;   // keys per 4-wave workgroup
+constexpr int LG_NWV = 12;                // waves per logits workgroup: the 12 a CU holds (3 per SIMD)
+constexpr int LG_TPW = 16;                // 32-key tiles per wave and workgroup when the rows overfill the device
 
 struct LogitParams {
   const uint16_t* q; long long q_st, q_sh;   // q[row][64][128] bf16
@@ -48,6 +46,7 @@ struct LogitParams {
   int clamp;                                 // 1: logits clamped at 60000 (shard kernels); 0: unclamped (paged)
   const int* lo;                             // optional per-row first valid position (flat layout: cu_seqlen_ks)
   const float* kscale; long long k_st;       // flat layout: key j codes at store + j * k_st, scale kscale[j]
+  int tpg;                                   // 32-key tiles per workgroup (the launcher's lg_grid)
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -58,19 +57,21 @@ __device__ inline uint32_t fp8hi_bf16x2(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
 }
 
-// Logits workgroup: 4 independent waves, wave w computing all 64 heads for keys j_blk + 256w + [0, 256) in eight
-// 32-key tiles. Per tile the key codes (32 rows x 128 B, 16-byte chunks XOR-swizzled by row so the MFMA operand
-// reads are bank-conflict free), the key scales and the block-table entries are copied global -> LDS by LDS DMA
-// into the wave's private rings: the codes of tiles t + 1 and t + 2 and the block-table entries of tiles t + 3 and
-// t + 4 are in flight while tile t is computed. Completion is counted by hand (no other global load in the loop),
-// and no wave waits for another.
+// Logits workgroup: the 12 waves of one CU (one workgroup per CU, so no later-dispatched workgroup waits behind an
+// older one's issue priority) share a range of 32-key tiles of one row. Each wave computes all 64 heads of one tile
+// per step and takes its tiles one at a time from an LDS counter (claimed a step before its block-table copy goes
+// out), so the waves finish together whatever each one's memory service; the logits of a key do not depend on
+// which wave computes them. Per tile the key codes (32 rows x 128 B, 16-byte chunks XOR-swizzled by row so the MFMA
+// operand reads are bank-conflict free), the key scales and the block-table entries are copied global -> LDS by
+// LDS DMA into the wave's private rings: the codes of steps t + 1 and t + 2 and the block-table entries of steps
+// t + 3 and t + 4 are in flight while step t is computed. Completion is counted by hand (no other global load in
+// the loop), and no wave waits for another.
 constexpr int LG_NBUF = 3;                  // code / scale ring depth
 constexpr int LG_NBT = 4;                   // block-table ring depth
 constexpr int LG_CODES = 32 * 128;
 constexpr int LG_OFF_SC = LG_NBUF * LG_CODES;
 constexpr int LG_OFF_BT = LG_OFF_SC + LG_NBUF * 128;
 constexpr int LG_WAVE = LG_OFF_BT + LG_NBT * 128;   // LDS bytes per wave
-constexpr int LG_WAVES = 4;
 
 // Key layouts: LY_ROW 132-byte rows [128 codes | scale] (the rank-sharded store); LY_SHUF vLLM's paged SHUFFLE
 // layout (P = 1, rpb = keys per block): key t of a block has its 16-byte chunk c at (t / 16) * 2048 + (t % 16) * 16
@@ -79,55 +80,59 @@ constexpr int LG_WAVES = 4;
 // block table (dsa_sm89.py:97-118).
 enum { LY_ROW = 0, LY_SHUF = 1, LY_FLAT = 2 };
 template <bool POW2, int LY, bool F16OUT = false>
-__global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
+__global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
   constexpr bool SHUF = LY == LY_SHUF, FLAT = LY == LY_FLAT;
-  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LG_WAVES * LG_WAVE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LG_NWV * LG_WAVE];
+  __shared__ int claim;                                     // next unclaimed tile of the workgroup's range
   const int row = blockIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   SPMLA_LDS uint8_t* lds = (SPMLA_LDS uint8_t*)lds_raw + wv * LG_WAVE;
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5, l32 = lane & 31;
   const int ctx = p.ctx[row];
-  const int j_wv = blockIdx.y * LG_KPB + wv * LG_TPW * 32;   // first key of this wave
   float* orow = (float*)p.out + (long long)row * p.out_st;            // fp32 output row
   _Float16* hrow = (_Float16*)p.out + (long long)row * p.out_st;      // fp16 output row
   auto put = [&](int j, float v) {
     if constexpr (F16OUT) hrow[j] = (_Float16)v;                       // round to nearest even (+-inf kept)
     else orow[j] = v;
   };
-  if (j_wv >= p.Lc) return;
-  const int nt = min(LG_TPW, (p.Lc - j_wv + 31) >> 5);        // tiles of this wave (uniform)
-  if ((long long)j_wv * p.P + p.rank >= ctx || p.lim == 0) {   // no key of this wave has a row
-    if (!p.noinf)
-      for (int j = j_wv + lane; j < j_wv + 32 * nt && j < p.Lc; j += 64) put(j, -__builtin_inff());
-    return;
-  }
+  // tiles [tb, te) of the row; keys j with j P + rank < ctx lie in tiles below tv (claimable)
+  const int tb = blockIdx.y * p.tpg;
+  const int te = min(tb + p.tpg, (p.Lc + 31) >> 5);
+  const long long nvalid = ctx > p.rank ? ((long long)ctx - p.rank + p.P - 1) / p.P : 0;   // keys below ctx
+  const int tv = p.lim == 0 ? tb : (int)min((long long)te, max((long long)tb, (nvalid + 31) >> 5));
+  if (!p.noinf)                                                         // keys of the range past ctx
+    for (int j = 32 * tv + (int)threadIdx.x; j < 32 * te && j < p.Lc; j += LG_NWV * 64) put(j, -__builtin_inff());
+  if (tv <= tb) return;                                     // uniform over the workgroup: no barrier below
+  if (threadIdx.x == 0) claim = tb + 5 * LG_NWV;
+  __syncthreads();
   const int* btr = FLAT ? nullptr : p.bt + (long long)p.req[row] * p.bt_st;
   const int lo = p.lo ? p.lo[row] : 0;
   // n / d, n % d: shifts when every divisor is a power of two (POW2), else 32-bit division
   auto dv = [&](uint32_t n, uint32_t d, int sh) -> uint32_t { return POW2 ? n >> sh : n / d; };
   auto md = [&](uint32_t n, uint32_t d, int sh) -> uint32_t { return POW2 ? n & (d - 1u) : n % d; };
-  // positions without a block-table entry read the wave's first entry (in range)
-  const int* bt_dummy = FLAT ? nullptr : btr + dv((uint32_t)(j_wv * p.P + p.rank), (uint32_t)p.bs, p.bs_sh);
-  auto key_pos = [&](int t, int r, uint32_t& pos) -> bool {
-    const int j = j_wv + 32 * t + r;
+  // positions without a block-table entry read the range's first entry (key 32 tb < nvalid: in range)
+  const int* bt_dummy = FLAT ? nullptr : btr + dv((uint32_t)(32 * tb * p.P + p.rank), (uint32_t)p.bs, p.bs_sh);
+  // step t of the wave computes tile id; a tile id at or past tv is no tile (the wave's ids only grow)
+  auto key_pos = [&](int id, int r, uint32_t& pos) -> bool {
+    const int j = 32 * id + r;
     const long long ps = (long long)j * p.P + p.rank;
     pos = (uint32_t)ps;
-    return t < nt && j < p.Lc && ps < ctx && ps >= lo;
+    return id < tv && j < p.Lc && ps < ctx && ps >= lo;
   };
-  // LDS DMA of the block-table entries of tile t (lanes 0..31: key l32)
-  auto issue_bt = [&](int t) {
+  // LDS DMA of the block-table entries of step t (tile id; lanes 0..31: key l32)
+  auto issue_bt = [&](int t, int id) {
     if (!FLAT && lane < 32) {
       uint32_t pos;
-      const bool in = key_pos(t, l32, pos);
+      const bool in = key_pos(id, l32, pos);
       dma4(in ? btr + dv(pos, (uint32_t)p.bs, p.bs_sh) : bt_dummy, lds + LG_OFF_BT + (t & (LG_NBT - 1)) * 128);
     }
   };
-  // LDS DMA of the codes and scales of tile t (its block-table entries already in LDS). Lane l32 maps key l32 to
-  // its row; the copying lanes take the row addresses from those lanes. Returns the lane's key-valid flag.
-  auto issue_codes = [&](int t) -> bool {
+  // LDS DMA of the codes and scales of step t (tile id; its block-table entries already in LDS). Lane l32 maps key
+  // l32 to its row; the copying lanes take the row addresses from those lanes. Returns the lane's key-valid flag.
+  auto issue_codes = [&](int t, int id) -> bool {
     uint32_t pos;
-    bool ok = key_pos(t, l32, pos);
+    bool ok = key_pos(id, l32, pos);
     const uint8_t* rp;
     const void* sp;
     if (FLAT) {                                        // key pos itself (pos < Lc = number of keys)
@@ -157,9 +162,14 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
     return ok;
   };
 
-  // prologue: block-table entries of tiles 0..3 (waited for), then the codes of tiles 0 and 1; the query loads
+  // tile ids of steps t .. t + 4 (uniform); steps 0 .. 4 take tiles tb + k LG_NWV + wv, later ones are claimed
+  int i0 = tb + wv, i1 = i0 + LG_NWV, i2 = i1 + LG_NWV, i3 = i2 + LG_NWV, i4 = i3 + LG_NWV;
+  // prologue: block-table entries of steps 0..3 (waited for), then the codes of steps 0 and 1; the query loads
   // overlap the copies
-  for (int t = 0; t < LG_NBT; ++t) issue_bt(t);
+  issue_bt(0, i0);
+  issue_bt(1, i1);
+  issue_bt(2, i2);
+  issue_bt(3, i3);
   // query fragments (bf16 A operand): M block m = heads 32m..32m+31 (lane head 32m + l32); k-pair kp covers dims
   // 32kp + 16half + 0..15, MFMA 2kp taking the first 8 and 2kp+1 the next 8 (same permutation as the key operand)
   const uint16_t* qr = p.q + (long long)row * p.q_st;
@@ -180,12 +190,12 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
   }
   wait_vm<0>();
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // DMA'd entries read below after the wait
-  bool ok0 = issue_codes(0);
-  bool ok1 = issue_codes(1);
+  bool ok0 = issue_codes(0, i0);
+  bool ok1 = issue_codes(1, i1);
   int nprev = 5;                                            // copies issued by the previous step
 
 #pragma unroll 1
-  for (int t = 0; t < nt; ++t) {
+  for (int t = 0; i0 < tv; ++t) {
     // codes / scales of tile t and block-table entries of tile t + 2 are complete once at most the previous
     // step's copies are outstanding
     if (nprev == 6) wait_vm<6>();
@@ -194,8 +204,11 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     bool ok2 = false;
     nprev = 0;
-    if (t + 2 < nt) { ok2 = issue_codes(t + 2); nprev = 5; }
-    if (!FLAT && t + 4 < nt) { issue_bt(t + 4); nprev += 1; }
+    if (i2 < tv) { ok2 = issue_codes(t + 2, i2); nprev = 5; }
+    if (!FLAT && i4 < tv) { issue_bt(t + 4, i4); nprev += 1; }
+    // the tile of step t + 5, read at the next step (an LDS atomic: no vector-memory count)
+    int nxt = 0;
+    if (lane == 0) nxt = atomicAdd(&claim, 1);
     // tile t
     const SPMLA_LDS uint8_t* cb = lds + (t % LG_NBUF) * LG_CODES + l32 * 128;
     bf16x8 kb[8];
@@ -229,7 +242,7 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
     }
     float part = pa + pb;
     part += __shfl_xor(part, 32, 64);
-    const int j = j_wv + 32 * t + l32;
+    const int j = 32 * i0 + l32;
     if (half == 0 && j < p.Lc) {
       const float lg = p.clamp ? fminf(part * sc, 60000.f) : part * sc;
       if (ok0) put(j, lg);
@@ -237,7 +250,10 @@ __global__ void __launch_bounds__(256) logits_kernel(LogitParams p) {
     }
     ok0 = ok1;
     ok1 = ok2;
+    i0 = i1; i1 = i2; i2 = i3; i3 = i4;
+    i4 = __builtin_amdgcn_readfirstlane(nxt);
   }
+  wait_vm<0>();                              // copies of steps past the last tile (dummy rows) land before exit
 }
 
 // ------------------------------------------------------------------------------------------------ top-k
@@ -1296,6 +1312,29 @@ static void topk_ws_passes(TopkWsParams p, hipStream_t stream) {
 
 using namespace spmla;
 
+// Logits grid: one 12-wave workgroup per CU. With at most as many rows as CUs, each row's tiles are split over
+// CUs / rows workgroups, one round of the whole grid (a wave pays its two-round-trip prologue, ~6 us under load,
+// once); with more rows, workgroups of LG_TPW tiles per wave, rounds fine enough for a short tail.
+inline int lg_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+inline dim3 lg_grid(int rows, int cols, int& tpg) {
+  const long long tiles = ((long long)cols + 31) / 32;      // per row
+  const long long cus = lg_cus();
+  const long long g = rows <= cus ? cus / rows : std::max(1LL, tiles / ((long long)idx::LG_NWV * idx::LG_TPW));
+  tpg = (int)std::max(1LL, (tiles + g - 1) / g);
+  return dim3(rows, (unsigned)((tiles + tpg - 1) / tpg));
+}
+
+
 extern "C" {
 
 int spmla_index_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
@@ -1321,14 +1360,14 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
   p.lim = R_local * P;
   p.clamp = 1;
   p.lo = nullptr; p.kscale = nullptr; p.k_st = 0;
-  dim3 grid(rows, (Lc + idx::LG_KPB - 1) / idx::LG_KPB);
+  const dim3 grid = lg_grid(rows, Lc, p.tpg);
   const bool pow2 = p.bs_sh >= 0 && p.rpb_sh >= 0 && p.p_sh >= 0;
   if (out_dtype == 1) {
-    if (pow2) hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_ROW, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
-    else hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_ROW, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    if (pow2) hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_ROW, true>), grid, dim3(idx::LG_NWV * 64), 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_ROW, true>), grid, dim3(idx::LG_NWV * 64), 0, (hipStream_t)stream, p);
   } else {
-    if (pow2) hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_ROW>), grid, dim3(256), 0, (hipStream_t)stream, p);
-    else hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_ROW>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    if (pow2) hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_ROW>), grid, dim3(idx::LG_NWV * 64), 0, (hipStream_t)stream, p);
+    else hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_ROW>), grid, dim3(idx::LG_NWV * 64), 0, (hipStream_t)stream, p);
   }
   return (int)hipGetLastError();
 }
@@ -1355,11 +1394,11 @@ int spmla_paged_mqa_logits(const void* q, long long q_st, long long q_sh, const 
   p.lim = p.R_local;
   p.clamp = 0;
   p.lo = nullptr; p.kscale = nullptr; p.k_st = 0;
-  dim3 grid(rows, (Lc + idx::LG_KPB - 1) / idx::LG_KPB);
+  const dim3 grid = lg_grid(rows, Lc, p.tpg);
   if (p.bs_sh >= 0)
-    hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_SHUF>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_SHUF>), grid, dim3(idx::LG_NWV * 64), 0, (hipStream_t)stream, p);
   else
-    hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_SHUF>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_SHUF>), grid, dim3(idx::LG_NWV * 64), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 
@@ -1382,8 +1421,8 @@ int spmla_mqa_logits(const void* q, long long q_st, long long q_sh, const float*
   p.lim = N;
   p.clamp = 0;
   p.lo = ks; p.kscale = kscale; p.k_st = k_st;
-  dim3 grid(M, (N + idx::LG_KPB - 1) / idx::LG_KPB);
-  hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_FLAT>), grid, dim3(256), 0, (hipStream_t)stream, p);
+  const dim3 grid = lg_grid(M, N, p.tpg);
+  hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_FLAT>), grid, dim3(idx::LG_NWV * 64), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 
