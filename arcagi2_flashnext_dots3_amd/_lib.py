@@ -23,6 +23,8 @@ SIGNATURES = {
     "spmla_topk": [P, LL, P, I, I, I, P, LL, I, P],
     "spmla_topk_ws_bytes": [I, I, I],
     "spmla_topk_ws": [P, LL, P, I, I, I, P, LL, P, LL, I, P],
+    "spmla_topk_ws_prehist": [P, LL, P, I, I, I, P, LL, P, LL, I, P],
+    "spmla_index_logits_hist": [P, LL, LL, P, LL, P, LL, I, LL, P, LL, I, P, P, I, I, I, I, I, P, LL, I, P, LL, I, P],
     "spmla_topk_scratch_bytes": [],
     "spmla_topk_scratch": [P, LL, P, I, I, I, P, LL, I, P],
     "spmla_topk_local": [P, LL, P, I, I, I, I, I, P, I, P],

@@ -29,6 +29,18 @@
 namespace spmla {
 namespace idx {
 
+// torch's order-preserving key of an fp32 value (the top-k's radix key; -0 < +0, NaN largest)
+__device__ inline uint32_t okey(float v) {
+  const uint32_t x = f2u(v);
+  if (v != v) return 0xffffffffu;
+  return (x & 0x80000000u) ? ~x : (x | 0x80000000u);
+}
+// the same key for an fp16 pattern, in the top 16 bits (low 16 bits zero; NaN largest)
+__device__ inline uint32_t okey16(uint32_t h) {
+  if ((h & 0x7fffu) > 0x7c00u) return 0xffff0000u;
+  return ((h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u)) << 16;
+}
+
 // ------------------------------------------------------------------------------------------------ logits
 constexpr int LG_NWV = 12;                // waves per logits workgroup: the 12 a CU holds (3 per SIMD)
 constexpr int LG_TPW = 16;                // 32-key tiles per wave and workgroup when the rows overfill the device
@@ -47,6 +59,9 @@ struct LogitParams {
   const int* lo;                             // optional per-row first valid position (flat layout: cu_seqlen_ks)
   const float* kscale; long long k_st;       // flat layout: key j codes at store + j * k_st, scale kscale[j]
   int tpg;                                   // 32-key tiles per workgroup (the launcher's lg_grid)
+  // optional level-0 top-k histograms (P == 1): workgroup (row, g) counts the top-k keys of its columns j <
+  // min(ctx, Lc) into hist + row * hist_rs bytes + g * 2048 bins (its columns are top-k chunk g)
+  uint32_t* hist; long long hist_rs;
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -84,6 +99,7 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
   constexpr bool SHUF = LY == LY_SHUF, FLAT = LY == LY_FLAT;
   __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LG_NWV * LG_WAVE];
   __shared__ int claim;                                     // next unclaimed tile of the workgroup's range
+  __shared__ uint32_t hh[1024];                             // level-0 histogram (p.hist): 2048 16-bit counts
   const int row = blockIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   SPMLA_LDS uint8_t* lds = (SPMLA_LDS uint8_t*)lds_raw + wv * LG_WAVE;
@@ -103,9 +119,18 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
   const int tv = p.lim == 0 ? tb : (int)min((long long)te, max((long long)tb, (nvalid + 31) >> 5));
   if (!p.noinf)                                                         // keys of the range past ctx
     for (int j = 32 * tv + (int)threadIdx.x; j < 32 * te && j < p.Lc; j += LG_NWV * 64) put(j, -__builtin_inff());
-  if (tv <= tb) return;                                     // uniform over the workgroup: no barrier below
+  // the top-k's histogram covers columns below min(ctx, Lc) (P == 1: all in tiles below tv, none in the fill)
+  uint32_t* hrow_out = p.hist ? (uint32_t*)((uint8_t*)p.hist + (long long)row * p.hist_rs) + blockIdx.y * 2048 : nullptr;
+  if (tv <= tb) {                                           // uniform over the workgroup: no barrier below
+    if (hrow_out)
+      for (int b = (int)threadIdx.x; b < 2048; b += LG_NWV * 64) hrow_out[b] = 0u;
+    return;
+  }
   if (threadIdx.x == 0) claim = tb + 5 * LG_NWV;
+  if (hrow_out)
+    for (int b = (int)threadIdx.x; b < 1024; b += LG_NWV * 64) hh[b] = 0u;
   __syncthreads();
+  const int nh = hrow_out ? min(ctx, p.Lc) : 0;             // columns the histogram counts
   const int* btr = FLAT ? nullptr : p.bt + (long long)p.req[row] * p.bt_st;
   const int lo = p.lo ? p.lo[row] : 0;
   // n / d, n % d: shifts when every divisor is a power of two (POW2), else 32-bit division
@@ -245,8 +270,17 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
     const int j = 32 * i0 + l32;
     if (half == 0 && j < p.Lc) {
       const float lg = p.clamp ? fminf(part * sc, 60000.f) : part * sc;
+      const bool counted = j < nh;                          // a top-k column: always written
       if (ok0) put(j, lg);
-      else if (!p.noinf) put(j, -__builtin_inff());
+      else if (!p.noinf || counted) put(j, -__builtin_inff());
+      if (counted) {                                        // the key of the value as stored
+        const float v = ok0 ? lg : -__builtin_inff();
+        uint32_t key;
+        if constexpr (F16OUT) key = okey16(__builtin_bit_cast(uint16_t, (_Float16)v));
+        else key = okey(v);
+        const uint32_t bin = key >> 21;
+        atomicAdd(&hh[bin >> 1], 1u << (16 * (bin & 1u)));
+      }
     }
     ok0 = ok1;
     ok1 = ok2;
@@ -254,6 +288,10 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
     i4 = __builtin_amdgcn_readfirstlane(nxt);
   }
   wait_vm<0>();                              // copies of steps past the last tile (dummy rows) land before exit
+  if (hrow_out) {                            // every wave has counted its tiles
+    __syncthreads();
+    for (int b = (int)threadIdx.x; b < 2048; b += LG_NWV * 64) hrow_out[b] = (hh[b >> 1] >> (16 * (b & 1))) & 0xffffu;
+  }
 }
 
 // ------------------------------------------------------------------------------------------------ top-k
@@ -261,16 +299,6 @@ constexpr int TK_NT = 1024;
 constexpr int TK_KMAX = 2048;
 constexpr int TK_CAP = 4096;
 
-__device__ inline uint32_t okey(float v) {
-  const uint32_t x = f2u(v);
-  if (v != v) return 0xffffffffu;
-  return (x & 0x80000000u) ? ~x : (x | 0x80000000u);
-}
-// the same key for an fp16 pattern, in the top 16 bits (low 16 bits zero; NaN largest)
-__device__ inline uint32_t okey16(uint32_t h) {
-  if ((h & 0x7fffu) > 0x7c00u) return 0xffff0000u;
-  return ((h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u)) << 16;
-}
 // key of logit j of a row (fp32 or fp16 elements)
 template <bool F16>
 __device__ inline uint32_t lkey(const void* x, long long j) {
@@ -1296,9 +1324,9 @@ namespace spmla {
 namespace idx {
 // the passes of spmla_topk_ws on fp32 (F16 false) or fp16 logits
 template <bool F16>
-static void topk_ws_passes(TopkWsParams p, hipStream_t stream) {
+static void topk_ws_passes(TopkWsParams p, hipStream_t stream, bool hist = true) {
   p.level = 0;
-  hipLaunchKernelGGL(topk_hist_kernel<F16>, dim3(p.rows, p.w.G), dim3(TK_NT), 0, stream, p);
+  if (hist) hipLaunchKernelGGL(topk_hist_kernel<F16>, dim3(p.rows, p.w.G), dim3(TK_NT), 0, stream, p);
   for (int level = 0; level < 2; ++level) {        // the level-1 histograms come from the level-0 collect
     p.level = level;
     hipLaunchKernelGGL(topk_collect_kernel<F16>, dim3(p.rows, p.w.G), dim3(TK_NT), 0, stream, p);
@@ -1337,11 +1365,11 @@ inline dim3 lg_grid(int rows, int cols, int& tpg) {
 
 extern "C" {
 
-int spmla_index_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
-                       const void* store, long long R_local, int rows_per_block, long long block_stride,
-                       const int* block_table, long long bt_st, int block_size, const int* req, const int* ctx,
-                       int rows, int H, int D, int Lc, int P, int rank, int noinf, void* out, long long out_st,
-                       int out_dtype, void* stream) {
+static int logits_row(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
+                      const void* store, long long R_local, int rows_per_block, long long block_stride,
+                      const int* block_table, long long bt_st, int block_size, const int* req, const int* ctx,
+                      int rows, int H, int D, int Lc, int P, int rank, int noinf, void* out, long long out_st,
+                      int out_dtype, void* stream, uint32_t* hist, long long hist_rs, int tpg, int gy) {
   if (rows < 0 || Lc < 0 || P <= 0 || rank < 0 || rank >= P || block_size <= 0 || rows_per_block <= 0) return SPMLA_EARG;
   if (out_dtype != 0 && out_dtype != 1) return SPMLA_EARG;
   if (rows == 0 || Lc == 0) return SPMLA_OK;
@@ -1350,7 +1378,7 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
   if (!q || !w || !store || !block_table || !req || !ctx || !out) return SPMLA_EARG;
   if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)store & 3) || (block_stride & 3))
     return SPMLA_EALIGN;
-  idx::LogitParams p;
+  idx::LogitParams p{};
   p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh; p.w = w; p.w_st = w_st;
   p.store = (const uint8_t*)store; p.R_local = R_local; p.rpb = rows_per_block; p.blk_stride = block_stride;
   p.bt = block_table; p.bt_st = bt_st; p.bs = block_size; p.req = req; p.ctx = ctx;
@@ -1360,7 +1388,12 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
   p.lim = R_local * P;
   p.clamp = 1;
   p.lo = nullptr; p.kscale = nullptr; p.k_st = 0;
-  const dim3 grid = lg_grid(rows, Lc, p.tpg);
+  dim3 grid = lg_grid(rows, Lc, p.tpg);
+  if (tpg > 0) {                                            // workgroup g = top-k chunk g < gy (the histogram's)
+    p.tpg = tpg;
+    grid = dim3(rows, (unsigned)gy);
+  }
+  p.hist = hist; p.hist_rs = hist_rs;
   const bool pow2 = p.bs_sh >= 0 && p.rpb_sh >= 0 && p.p_sh >= 0;
   if (out_dtype == 1) {
     if (pow2) hipLaunchKernelGGL((idx::logits_kernel<true, idx::LY_ROW, true>), grid, dim3(idx::LG_NWV * 64), 0, (hipStream_t)stream, p);
@@ -1370,6 +1403,31 @@ int spmla_index_logits(const void* q, long long q_st, long long q_sh, const floa
     else hipLaunchKernelGGL((idx::logits_kernel<false, idx::LY_ROW>), grid, dim3(idx::LG_NWV * 64), 0, (hipStream_t)stream, p);
   }
   return (int)hipGetLastError();
+}
+
+int spmla_index_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
+                       const void* store, long long R_local, int rows_per_block, long long block_stride,
+                       const int* block_table, long long bt_st, int block_size, const int* req, const int* ctx,
+                       int rows, int H, int D, int Lc, int P, int rank, int noinf, void* out, long long out_st,
+                       int out_dtype, void* stream) {
+  return logits_row(q, q_st, q_sh, w, w_st, store, R_local, rows_per_block, block_stride, block_table, bt_st,
+                    block_size, req, ctx, rows, H, D, Lc, P, rank, noinf, out, out_st, out_dtype, stream, nullptr, 0, 0, 0);
+}
+
+int spmla_index_logits_hist(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
+                            const void* store, long long R_local, int rows_per_block, long long block_stride,
+                            const int* block_table, long long bt_st, int block_size, const int* req, const int* ctx,
+                            int rows, int H, int D, int Lc, int noinf, void* out, long long out_st, int out_dtype,
+                            void* topk_ws, long long ws_bytes, int K, void* stream) {
+  if (rows < 0 || Lc < 0 || K <= 0 || (out_dtype != 0 && out_dtype != 1)) return SPMLA_EARG;
+  if (K > idx::TK_KMAX) return SPMLA_ELIMIT;
+  if (rows == 0 || Lc == 0) return SPMLA_OK;
+  const idx::TopkWs tw = idx::topk_ws_layout(Lc);
+  if (!topk_ws || ((uintptr_t)topk_ws & 15) || ws_bytes < (long long)rows * tw.row_bytes) return SPMLA_EARG;
+  if (tw.CL >= 65536) return SPMLA_ELIMIT;                  // 16-bit counts per chunk: use the separate pass
+  return logits_row(q, q_st, q_sh, w, w_st, store, R_local, rows_per_block, block_stride, block_table, bt_st,
+                    block_size, req, ctx, rows, H, D, Lc, 1, 0, noinf, out, out_st, out_dtype, stream,
+                    tw.hist((uint8_t*)topk_ws, 0), tw.row_bytes, tw.CL / 32, tw.G);
 }
 
 int spmla_paged_mqa_logits(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
@@ -1384,7 +1442,7 @@ int spmla_paged_mqa_logits(const void* q, long long q_st, long long q_sh, const 
   if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)cache & 3) || (block_stride & 3) ||
       block_stride < (long long)block_size * 132)
     return SPMLA_EALIGN;
-  idx::LogitParams p;
+  idx::LogitParams p{};
   p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh; p.w = w; p.w_st = w_st;
   p.store = (const uint8_t*)cache; p.R_local = num_blocks * block_size; p.rpb = block_size;
   p.blk_stride = block_stride; p.bt = block_table; p.bt_st = bt_st; p.bs = block_size; p.req = req; p.ctx = ctx;
@@ -1412,7 +1470,7 @@ int spmla_mqa_logits(const void* q, long long q_st, long long q_sh, const float*
   if (((uintptr_t)q & 15) || (q_st & 7) || (q_sh & 7) || ((uintptr_t)k & 3) || (k_st & 3) || k_st < 128 ||
       ((uintptr_t)kscale & 3))
     return SPMLA_EALIGN;
-  idx::LogitParams p;
+  idx::LogitParams p{};
   p.q = (const uint16_t*)q; p.q_st = q_st; p.q_sh = q_sh; p.w = w; p.w_st = w_st;
   p.store = (const uint8_t*)k; p.R_local = N; p.rpb = 1; p.blk_stride = 0;
   p.bt = nullptr; p.bt_st = 0; p.bs = 1; p.req = nullptr; p.ctx = ke;
@@ -1452,8 +1510,8 @@ long long spmla_topk_ws_bytes(int rows, int Lc, int K) {
   return topk_ws_base(rows, Lc) + topk_ws_ovf(rows, Lc);
 }
 
-int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
-                  long long out_st, void* ws, long long ws_bytes, int dtype, void* stream) {
+static int topk_ws_run(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                       long long out_st, void* ws, long long ws_bytes, int dtype, void* stream, bool hist) {
   if (rows < 0 || Lc < 0 || K <= 0 || (dtype != 0 && dtype != 1)) return SPMLA_EARG;
   if (K > idx::TK_KMAX) return SPMLA_ELIMIT;
   if (rows == 0) return SPMLA_OK;
@@ -1465,9 +1523,19 @@ int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows,
   p.ws = (uint8_t*)ws; p.w = idx::topk_ws_layout(Lc);
   // with room for the overflow lists, a level that narrows hands its bin's keys to the next level in a list
   p.ovf = ovf > 0 && ws_bytes >= base + ovf ? (unsigned long long*)((uint8_t*)ws + base) : nullptr;
-  if (dtype == 1) idx::topk_ws_passes<true>(p, (hipStream_t)stream);
-  else idx::topk_ws_passes<false>(p, (hipStream_t)stream);
+  if (dtype == 1) idx::topk_ws_passes<true>(p, (hipStream_t)stream, hist);
+  else idx::topk_ws_passes<false>(p, (hipStream_t)stream, hist);
   return (int)hipGetLastError();
+}
+
+int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                  long long out_st, void* ws, long long ws_bytes, int dtype, void* stream) {
+  return topk_ws_run(logits, lg_st, ctx, rows, Lc, K, out, out_st, ws, ws_bytes, dtype, stream, true);
+}
+
+int spmla_topk_ws_prehist(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                          long long out_st, void* ws, long long ws_bytes, int dtype, void* stream) {
+  return topk_ws_run(logits, lg_st, ctx, rows, Lc, K, out, out_st, ws, ws_bytes, dtype, stream, false);
 }
 
 long long spmla_topk_scratch_bytes(void) { return idx::TOPK_SCRATCH_BYTES; }

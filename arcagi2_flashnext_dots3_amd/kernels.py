@@ -252,6 +252,73 @@ def topk(logits, ctx, K, out=None, single_pass=False, ws=None):
     return out
 
 
+
+def topk_prehist(logits, ctx, K, ws, out=None):
+    """topk over logits whose first-level histograms spmla_index_logits_hist already wrote into ws (same rows, Lc, K,
+    ctx and dtype; spmla_topk_ws_prehist): the histogram pass is skipped, the result is topk's."""
+    rows, Lc = logits.shape
+    _need(logits.dtype in _LG_DT and logits.stride(1) == 1, "fp32 / fp16 logits with contiguous rows")
+    _need(ctx.dtype == torch.int32 and ctx.is_contiguous(), "ctx int32")
+    if out is None:
+        out = torch.empty(rows, K, dtype=torch.int32, device=logits.device)
+    _need(out.dtype == torch.int32 and out.stride(1) == 1 and out.shape[0] >= rows and out.shape[1] >= K,
+          "out int32 [rows, >= K] with contiguous rows")
+    _lib.call("spmla_topk_ws_prehist", logits.data_ptr(), logits.stride(0), ctx.data_ptr(), rows, Lc, K,
+              out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _LG_DT[logits.dtype], _stream(logits))
+    return out
+
+
+def logits_hist(q, w, base, R, rpb, bstride, block_table, block_size, req, ctx, Lc, K, lg, ws, noinf=False):
+    """spmla_index_logits_hist (P = 1): the logits into lg [rows, >= Lc] (fp32 / fp16) and the first-level top-k
+    histograms into ws. Returns False without a launch when the fused path does not apply (a top-k chunk of 65536 or
+    more columns); the caller then runs the logits and topk separately."""
+    rows = q.shape[0]
+    rc = _lib.lib().spmla_index_logits_hist(
+        q.data_ptr(), q.stride(0), q.stride(1), w.data_ptr(), w.stride(0), base.data_ptr(), R, rpb, bstride,
+        block_table.data_ptr(), block_table.stride(0), block_size, req.data_ptr(), ctx.data_ptr(), rows, q.shape[1],
+        q.shape[2], Lc, int(bool(noinf)), lg.data_ptr(), lg.stride(0), _LG_DT[lg.dtype], ws.data_ptr(), ws.numel(),
+        K, _stream(q))
+    if rc == -5:
+        return False
+    if rc != 0:
+        raise RuntimeError(f"spmla_index_logits_hist failed: {rc} ({_lib.ERRORS.get(rc, 'hip error')})")
+    return True
+
+
+def logits_topk(q, w, store, block_table, block_size, req, ctx, Lc, K, lg=None, out=None, noinf=False,
+                dtype=torch.float32, ws=None):
+    """index_logits (P = 1) then topk of its [rows, Lc] logits, with the top-k's first histogram pass done in the
+    logits epilogue (logits_hist + topk_prehist) when it applies, else the two separate calls; same logits and
+    positions either way. Returns (logits, positions)."""
+    rows, H, D = q.shape
+    _need(q.dtype == torch.bfloat16 and q.stride(2) == 1, "q bf16 with contiguous head dim")
+    _need(w.dtype == torch.float32 and w.stride(1) == 1, "w fp32")
+    _need(req.dtype == torch.int32 and ctx.dtype == torch.int32 and block_table.dtype == torch.int32, "int32 tables")
+    _need(ctx.is_contiguous(), "ctx int32 contiguous")
+    if store.dim() == 3:
+        rpb, bstride, R = store.shape[1], store.stride(0), store.shape[0] * store.shape[1]
+    else:
+        R = store.shape[0]
+        rpb, bstride = max(1, R), max(1, R) * KEYROW
+    if lg is None:
+        lg = torch.empty(rows, max(Lc, 1), dtype=dtype, device=q.device)
+    _need(lg.dtype in _LG_DT and lg.stride(1) == 1 and lg.shape[0] >= rows and lg.shape[1] >= Lc,
+          "logits fp32 / fp16 [rows, >= Lc] with contiguous rows")
+    if out is None:
+        out = torch.empty(rows, K, dtype=torch.int32, device=q.device)
+    if rows == 0 or Lc == 0:
+        out[:rows, :K] = -1
+        return lg, out
+    lgv = lg[:rows, :Lc]
+    if ws is None:
+        ws, _ = _workspace("topk", q.device, int(_lib.lib().spmla_topk_ws_bytes(rows, Lc, K)))
+    if logits_hist(q, w, store, R, rpb, bstride, block_table, block_size, req, ctx, Lc, K, lg, ws, noinf):
+        topk_prehist(lgv, ctx, K, ws, out=out)
+    else:
+        index_logits(q, w, store, block_table, block_size, req, ctx, Lc, out=lg, noinf=noinf)
+        topk(lgv, ctx, K, out=out, ws=ws)
+    return lg, out
+
 def topk_scratch(logits, ctx, K, out=None):
     """topk without a workspace or any allocation in the library (spmla_topk_scratch): the passes use the library's
     fixed per-GPU scratch. Calls that overlap on one GPU race. Sizes beyond the scratch raise (SPMLA_ELIMIT)."""

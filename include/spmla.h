@@ -85,6 +85,27 @@ long long spmla_topk_ws_bytes(int rows, int Lc, int K);
 int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
                   long long out_st, void* ws, long long ws_bytes, int dtype, void* stream);
 
+/* spmla_index_logits (P = 1, rank 0) that also writes the first radix level of spmla_topk_ws into the top-k's
+ * workspace ws (spmla_topk_ws_bytes(rows, Lc, K) bytes, 16-byte aligned): the logits workgroups cover the top-k's
+ * column chunks and count the keys of the values they store in columns j < min(ctx[row], Lc), so the pass that would
+ * re-read the logits for that histogram is not needed (spmla_topk_ws_prehist). Columns j < min(ctx, Lc) whose key
+ * has no block-table entry are written -inf even with noinf != 0 (they are top-k columns). SPMLA_ELIMIT when a
+ * chunk reaches 65536 columns (16-bit counts; Lc above 8 x 64512): use spmla_index_logits and spmla_topk_ws. The
+ * reference computes the logits and then selects in separate calls (shard_indexer.py:63-91 then fast_topk.py:52-78 /
+ * csrc/topk_select.cu:75-201 at P = 1, shard_indexer.py:194-221); the pair of entry points below is the same
+ * computation with the selection's first pass done in the logits epilogue. */
+int spmla_index_logits_hist(const void* q, long long q_st, long long q_sh, const float* w, long long w_st,
+                            const void* store, long long R_local, int rows_per_block, long long block_stride,
+                            const int* block_table, long long bt_st, int block_size, const int* req, const int* ctx,
+                            int rows, int H, int D, int Lc, int noinf, void* out, long long out_st, int out_dtype,
+                            void* topk_ws, long long ws_bytes, int K, void* stream);
+
+/* spmla_topk_ws whose workspace already holds the first-level histograms of these logits (written by
+ * spmla_index_logits_hist with the same rows, Lc, K, ctx and dtype, and no other use of the workspace in between):
+ * the histogram pass is skipped; same result as spmla_topk_ws. */
+int spmla_topk_ws_prehist(const void* logits, long long lg_st, const int* ctx, int rows, int Lc, int K, int* out,
+                          long long out_st, void* ws, long long ws_bytes, int dtype, void* stream);
+
 /* spmla_topk_ws without a caller workspace and without any allocation: the passes use the library's own
  * fixed device scratch (a file-scope array of spmla_topk_scratch_bytes() = 16 MiB per GPU, held from library load
  * until the process ends; its device address is looked up once per device on the first call there). Same result

@@ -53,6 +53,15 @@ def test_version():
     (("spmla_topk", 256, 16, 256, 1, 10, 16, 256, 16, 2, None), -2),          # dtype 0 (fp32) or 1 (fp16) only
     (("spmla_topk_ws", None, 0, None, 1, 10, 5000, None, 0, None, 0, 0, None), -5),
     (("spmla_topk_ws", None, 0, None, 1, 10, 16, None, 0, None, 0, 1, None), -2),
+    (("spmla_topk_ws_prehist", None, 0, None, 1, 10, 5000, None, 0, None, 0, 0, None), -5),
+    (("spmla_topk_ws_prehist", None, 0, None, 1, 10, 0, None, 0, None, 0, 0, None), -2),
+    (("spmla_index_logits_hist", None, 0, 0, None, 0, None, 0, 1, 0, None, 0, 64, None, None, 1, 64, 128, 1000, 0,
+      None, 0, 0, None, 0, 0, None), -2),                                      # K = 0
+    (("spmla_index_logits_hist", 256, 0, 0, 256, 0, 256, 0, 1, 0, 256, 0, 64, 256, 256, 1, 64, 128, 1000, 0,
+      256, 0, 0, 8, 1 << 40, 2048, None), -2),                                 # workspace not 16-byte aligned
+    # a top-k chunk of 65536 or more columns (Lc 600000): the fused histogram's 16-bit counts do not apply
+    (("spmla_index_logits_hist", 256, 0, 0, 256, 0, 256, 0, 1, 0, 256, 0, 64, 256, 256, 1, 64, 128, 600000, 0,
+      256, 0, 0, 256, 1 << 40, 2048, None), -5),
     (("spmla_topk_scratch", None, 0, None, 1, 10, 5000, None, 0, 0, None), -5),
     (("spmla_topk_scratch", None, 0, None, -1, 10, 16, None, 0, 1, None), -2),
     # 128 rows x 131072 columns need more workspace than the fixed 16 MiB scratch (placeholder pointers 256)

@@ -159,6 +159,44 @@ def test_logits_then_topk_end_to_end(dev):
     assert exact >= 1
 
 
+
+@pytest.mark.parametrize("dtype,noinf", [(torch.float32, False), (torch.float16, False), (torch.float32, True)])
+def test_logits_hist_topk_matches_separate(dev, dtype, noinf):
+    """The first-level top-k histogram built in the logits epilogue (spmla_index_logits_hist, then
+    spmla_topk_ws_prehist) against the separate calls on the same inputs: identical logits bit for bit and identical
+    positions, which are also the oracle's top-k of those logits. Rows with ctx below Lc (a short last chunk, ctx 0,
+    ctx <= K), indexer-like concentrated values on some rows, and (noinf False) a block-table entry missing inside
+    ctx, whose keys both paths write as -inf."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    rows, L, bs, K = 10, 40000, 64, 2048
+    nbp = (L + bs - 1) // bs
+    nb = rows * nbp + 2
+    store = _keys(nb, bs, 60)
+    g = torch.Generator().manual_seed(61)
+    bt = torch.randperm(nb, generator=g)[: rows * nbp].reshape(rows, nbp).to(torch.int32)
+    if not noinf:
+        bt[3, 5] = -1
+    q = torch.randn(rows, 64, 128, generator=g).to(torch.bfloat16)
+    q[6:] = (q[6:].float() * 0.05 + 1.0).to(torch.bfloat16)           # concentrated logits (second radix level)
+    w = torch.rand(rows, 64, generator=g)
+    req = torch.arange(rows, dtype=torch.int32)
+    ctx = torch.full((rows,), L, dtype=torch.int32)
+    ctx[1], ctx[2], ctx[4], ctx[5] = 0, 2048, 9000, 33000
+    st = torch.from_numpy(store).to(dev).view(nb, bs, 132)
+    args = (q.to(dev), w.to(dev), st, bt.to(dev), bs, req.to(dev), ctx.to(dev))
+    print(f"[logits+topk fused] dtype={dtype} noinf={noinf}", flush=True)
+    lg1 = torch.zeros(rows, L, dtype=dtype, device=dev)
+    lg2 = torch.zeros(rows, L, dtype=dtype, device=dev)
+    kernels.index_logits(*args, L, out=lg1, noinf=noinf)
+    tk1 = kernels.topk(lg1, ctx.to(dev), K)
+    _, tk2 = kernels.logits_topk(*args, L, K, lg=lg2, noinf=noinf)
+    torch.cuda.synchronize()
+    iv = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(lg1.view(iv), lg2.view(iv)), "logits differ between the fused and the separate path"
+    assert torch.equal(tk1, tk2), "positions differ between the fused and the separate path"
+    exp = ref.topk(lg1.float().cpu().numpy(), ctx.numpy(), K)
+    assert np.array_equal(tk2.cpu().numpy(), exp)
+
 # ---- fp16 logits (the reference's ARC_SHARD_F16OUT buffer) and top-k over fp16 keys
 def test_index_logits_f16_is_the_rounded_f32(dev):
     """fp16 logits bit for bit equal to the fp32 launch's logits rounded to nearest even (numpy's float32 -> float16),
