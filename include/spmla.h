@@ -76,7 +76,7 @@ int spmla_topk(const void* logits, long long lg_st, const int* ctx, int rows, in
 long long spmla_topk_ws_bytes(int rows, int Lc, int K);
 
 /* spmla_topk with the same result, spread over several workgroups per row: a histogram pass and a collect pass over
- * chunks of 8192 or more columns (at most 8 chunks per row), then one workgroup per row that resolves the boundary bin
+ * chunks of 8192 or more columns (at most 4 chunks per row), then one workgroup per row that resolves the boundary bin
  * and sorts. ws: device memory of spmla_topk_ws_bytes(rows, Lc, K) bytes (a smaller one without the overflow lists is
  * accepted: the second level then reads the row again), 16-byte aligned, any contents (every pass writes what the
  * next reads); calls that share a workspace must not overlap. Same replacement as
@@ -90,7 +90,7 @@ int spmla_topk_ws(const void* logits, long long lg_st, const int* ctx, int rows,
  * column chunks and count the keys of the values they store in columns j < min(ctx[row], Lc), so the pass that would
  * re-read the logits for that histogram is not needed (spmla_topk_ws_prehist). Columns j < min(ctx, Lc) whose key
  * has no block-table entry are written -inf even with noinf != 0 (they are top-k columns). SPMLA_ELIMIT when a
- * chunk reaches 65536 columns (16-bit counts; Lc above 8 x 64512): use spmla_index_logits and spmla_topk_ws. The
+ * chunk reaches 65536 columns (16-bit counts; Lc above 4 x 64512): use spmla_index_logits and spmla_topk_ws. The
  * reference computes the logits and then selects in separate calls (shard_indexer.py:63-91 then fast_topk.py:52-78 /
  * csrc/topk_select.cu:75-201 at P = 1, shard_indexer.py:194-221); the pair of entry points below is the same
  * computation with the selection's first pass done in the logits epilogue. */

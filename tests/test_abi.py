@@ -64,8 +64,8 @@ def test_version():
       256, 0, 0, 256, 1 << 40, 2048, None), -5),
     (("spmla_topk_scratch", None, 0, None, 1, 10, 5000, None, 0, 0, None), -5),
     (("spmla_topk_scratch", None, 0, None, -1, 10, 16, None, 0, 1, None), -2),
-    # 128 rows x 131072 columns need more workspace than the fixed 16 MiB scratch (placeholder pointers 256)
-    (("spmla_topk_scratch", 256, 131072, 256, 128, 131072, 2048, 256, 2048, 0, None), -5),
+    # 256 rows x 131072 columns need more workspace than the fixed 16 MiB scratch (placeholder pointers 256)
+    (("spmla_topk_scratch", 256, 131072, 256, 256, 131072, 2048, 256, 2048, 0, None), -5),
     (("spmla_topk_local", None, 0, None, 1, 0, 1, 100, 4096, None, 0, None), -5),
     (("spmla_topk_local", None, 0, None, 1, 2, 2, 100, 16, None, 0, None), -2),
     (("spmla_topk_local", 256, 100, 256, 1, 0, 1, 100, 16, 256, 3, None), -2),

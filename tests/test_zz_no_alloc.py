@@ -44,7 +44,7 @@ def test_topk_scratch_matches_workspace(dev):
 def test_topk_scratch_rejects_oversize(dev):
     from arcagi2_flashnext_dots3_amd import _lib, kernels
     lib = _lib.lib()
-    rows, L, K = 128, 131072, 2048                  # 128 x 180 KB of workspace > 16 MiB, even without overflow lists
+    rows, L, K = 256, 131072, 2048                  # 256 x 112 KiB of workspace > 16 MiB, even without overflow lists
     assert lib.spmla_topk_ws_bytes(rows, L, K) > lib.spmla_topk_scratch_bytes()
     lg = torch.zeros(rows, L, device=dev)
     ctx = torch.full((rows,), L, dtype=torch.int32, device=dev)
