@@ -1040,6 +1040,9 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
     t0 += h0; t1 += h1;
     if (c < g) { q0 += h0; q1 += h1; }
   }
+  // defaults: with histograms that do not add up to the row (a workspace that was never filled for these logits) no
+  // thread finds the boundary; the lists below are bounds-checked either way, so such a call writes only its own lists
+  if (tid == 0) { sh[1] = 0u; sh[2] = 0u; sh[3] = 0u; sh[4] = 0u; }
   uint32_t tot;
   const uint32_t before = block_excl_scan(t0 + t1, wsum, &tot);
   if (before < need && before + t0 >= need) { sh[1] = (uint32_t)b0; sh[2] = before; sh[3] = t0; }
@@ -1083,18 +1086,21 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   }
   unsigned long long* sel = p.w.sel(p.ws, row);
   unsigned long long* cand = to_ovf ? ovf_row : p.w.cand(p.ws, row);
+  const uint32_t clim = to_ovf ? (uint32_t)(p.w.G * p.w.CL) : (uint32_t)TK_CAP;   // entries of the candidate list
   const void* x = lrow<F16>(p.lg, row, p.lg_st);
   // the keys this workgroup visits: logits columns c0 .. c1, or (a level narrowed with an overflow list) entries
   // c0 .. c1 of the overflow list: the previous level's bin keys of chunk g, at the offset its histograms give
   int c0 = g * p.w.CL, c1 = min(c0 + p.w.CL, n);
-  const bool from_ovf = st.ovf != 0;
+  const bool from_ovf = st.ovf != 0 && p.ovf != nullptr;
   if (from_ovf) {
     const uint32_t* h0 = p.w.hist(p.ws, row) + (long long)((p.level - 1) & 1) * p.w.G * 2048;
     const uint32_t pb = ((uint32_t)prefix >> tk_shift(p.level - 1)) & 0x7ffu;
-    int o = 0;
-    for (int c = 0; c < g; ++c) o += (int)h0[(long long)c * 2048 + pb];
-    c0 = o;
-    c1 = o + (int)h0[(long long)g * 2048 + pb];
+    const uint32_t lim = (uint32_t)(p.w.G * p.w.CL);   // entries of the row's overflow list
+    uint32_t o = 0;
+    for (int c = 0; c < g; ++c) o += h0[(long long)c * 2048 + pb];
+    const uint32_t e = o + h0[(long long)g * 2048 + pb];
+    c0 = (int)min(o, lim);
+    c1 = (int)min(max(e, o), lim);
   }
   // thread t visits the 8 consecutive entries 8t .. 8t + 7 of each 8192-entry pass, and the slots of a pass come
   // from one block scan of the per-thread counts: every list the pass appends to stays in column order (the
@@ -1148,8 +1154,8 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
     cbase += tot >> 16;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if ((selm >> i) & 1u) sel[so++] = tk_pack(k[i], jj[i]);
-      if ((candm >> i) & 1u) cand[co++] = tk_pack(k[i], jj[i]);
+      if ((selm >> i) & 1u) { if (so < (uint32_t)TK_KMAX) sel[so] = tk_pack(k[i], jj[i]); ++so; }
+      if ((candm >> i) & 1u) { if (co < clim) cand[co] = tk_pack(k[i], jj[i]); ++co; }
       if (narrow && ((binm >> i) & 1u))
         atomicAdd(&nh[(tid & (TK_HCOPY - 1)) * TK_HSTR + ((k[i] >> nshift) & 0x7ffu)], 1u);
     }
@@ -1183,16 +1189,18 @@ __global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
   if (full) {
     nsel = tk_select(src, p.K, L);                  // few columns, or ties too heavy for the lists
   } else {
+    // the header's counts, kept inside the lists (they are, whenever the histograms were this row's)
+    const int nsb = min(max(st.sb, 0), p.K), nbc = min(max(st.binc, 0), TK_CAP);
+    const uint32_t nneed = (uint32_t)min(max(st.need, 0), p.K - nsb);
     const unsigned long long* sel = p.w.sel(p.ws, row);
-    for (int i = tid; i < st.sb; i += TK_NT) L.sel[i] = sel[i];
+    for (int i = tid; i < nsb; i += TK_NT) L.sel[i] = sel[i];
     if (st.state == TKW_CANDS) {
       const unsigned long long* cand = p.w.cand(p.ws, row);
-      for (int i = tid; i < st.binc; i += TK_NT) L.cand[i] = cand[i];
+      for (int i = tid; i < nbc; i += TK_NT) L.cand[i] = cand[i];
     }
     __syncthreads();
     if (st.state == TKW_CANDS)
-      tk_resolve_cands(L, st.binc, st.lvl, (uint32_t)st.prefix, (uint32_t)st.mask, (uint32_t)st.need,
-                       (uint32_t)st.sb, n);
+      tk_resolve_cands(L, nbc, st.lvl, (uint32_t)st.prefix, (uint32_t)st.mask, nneed, (uint32_t)nsb, n);
     if constexpr (F16) {
       // fp16 keys: at most two radix passes (the keys' low half is zero), faster than the bitonic network here;
       // fp32 keys need three or four, slower than it (measured on the bench's indexer logits)

@@ -495,9 +495,12 @@ def run_config4(a, dev):
         ws = torch.empty(int(kernels._lib.lib().spmla_topk_ws_bytes(B, L, K)), dtype=torch.uint8, device=dev)
 
         def fused(dst=lg):
-            _ok = kernels.logits_hist(q, w, kc, st.R_local, st.RPB, st.STRIDE_BLK, bt, bs, req, ctx, L, K, dst, ws,
-                                      noinf=True)
-            kernels.topk_prehist(dst, ctx, K, ws, out=out)
+            if kernels.logits_hist(q, w, kc, st.R_local, st.RPB, st.STRIDE_BLK, bt, bs, req, ctx, L, K, dst, ws,
+                                   noinf=True):
+                kernels.topk_prehist(dst, ctx, K, ws, out=out)
+            else:                        # a top-k chunk of 65536 or more columns: the separate calls
+                logits(dst)
+                kernels.topk(dst, ctx, K, out=out, ws=ws)
 
         fused()
         torch.cuda.synchronize()
