@@ -90,7 +90,8 @@ def test_config3_full_size(dev):
 def test_config4_full_size(dev, L, B):
     """indexer logits over L keys per sequence (a scattered block table over the key cache) for
     every row of the launch, the fp64 oracle on 3 rows; top-2048 bit-exact against the oracle's selection on the
-    GPU's own fp32 logits for every row."""
+    GPU's own fp32 logits for every row; the fused step (histogram in the logits epilogue) gives the same logits bit
+    for bit and the same positions."""
     from arcagi2_flashnext_dots3_amd import kernels
     from arcagi2_flashnext_dots3_amd.shard_indexer import ShardStore
     bs, K = 64, 2048
@@ -112,7 +113,11 @@ def test_config4_full_size(dev, L, B):
     print(f"[fullsize] config 4: L={L}, {B} rows", flush=True)
     lg = kernels.index_logits(q, w, kc, bt, bs, req, ctx, L)
     top = kernels.topk(lg, ctx, K)
+    # the step as ShardStore.logits_topk runs it: the top-k's first histogram in the logits epilogue
+    lg2, top2 = kernels.logits_topk(q, w, kc, bt, bs, req, ctx, L, K)
     torch.cuda.synchronize()
+    assert torch.equal(lg2[:, :L].view(torch.int32), lg.view(torch.int32)), "fused logits differ"
+    assert torch.equal(top2, top), "fused positions differ"
     got = lg.cpu().numpy()
     for r in (0, 1, B - 1):                                # oracle on the blocks of three rows
         blocks = bt[r].long()
