@@ -25,7 +25,7 @@ import os
 import torch
 
 from . import kernels
-from .diagnostics import AttnTimer
+from .diagnostics import AccessTrace, AttnTimer
 
 ROW = kernels.ROW656
 HOST_ROW = {"row656": kernels.ROW656, "e2m2": kernels.ROW400}
@@ -82,11 +82,14 @@ class LayerOffload:
     way (misses copied in as they are, the step's pool rows decoded into staging for the attention). two_choice (ways):
     the reference's two-choice set placement (ARC_OFFLOAD_TWO_CHOICE, offload_fill.py:16-23): a missing row whose set
     has no free way takes one in a second, hashed set before it spills; lookups and invalidations cover both sets.
+    trace: a diagnostics.AccessTrace that records the stored slots and the decode rows of a window of calls.
     """
+
+    _count = 0           # layers built in this process (the first one takes the default access trace)
 
     def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
                  spill_rows=131072, overlap_fill=True, two_choice=False, cache_fmt="row656", packed=False,
-                 time_every=None, host_direct=False):
+                 time_every=None, host_direct=False, trace=None):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         if cache_mode not in ("static", "ways"):
@@ -121,7 +124,13 @@ class LayerOffload:
         if time_every is None:
             time_every = int(os.environ.get("ARC_OFFLOAD_ATTN2_TIME", "0") or 0)
         self.timer = AttnTimer(time_every)
+        # stored slots and decode rows over a window of calls to an .npz (diagnostics.AccessTrace; None: taken from
+        # ARC_OFFLOAD_DUMP / ARC_OFFLOAD_DUMP_LAYERS, where the first layer built in the process is the default one)
+        self.trace = trace if trace is not None else AccessTrace.from_env(key, self.device,
+                                                                         first=LayerOffload._count == 0)
+        LayerOffload._count += 1
         self.wc = None
+        self.W = int(ways) if cache_mode == "ways" else 1
         if cache_mode == "ways":
             if self.C <= 0 or self.C % int(ways):
                 raise ValueError("cache_mode='ways' needs cache_rows a positive multiple of ways")
@@ -142,6 +151,8 @@ class LayerOffload:
             raise ValueError("LayerOffload.store: Row656 rows carry their own scales; kv_scale must be 1")
         kpe = k_pe.reshape(k_pe.shape[0], -1)
         slots = slots[:n].to(torch.int64)
+        if self.trace is not None:
+            self.trace.stored(slots)
         fmt = 2 if compact else 0
         kernels.cache_write(kv_c_normed[:n], kpe[:n], slots, self.host, fmt=fmt, kv_scale=kv_scale)
         if self.wc is not None:
@@ -257,6 +268,8 @@ class LayerOffload:
         ql > 1 the request-packed path runs (same result up to the fp32 summation order); mkey / slots (the
         reference's prefetch hints) are accepted and do not change the result. With time_every set, the call is
         timed with GPU events (arm: packed / ways / tiers / host)."""
+        if self.trace is not None:
+            self.trace.access(idx, q.shape[0], self.C, self.W, self.R, slots)
         e0 = self.timer.begin(q.device)
         res = self._attend(q, idx, sm_scale, kv_scale, num_heads, ql, out, lse, return_lse)
         if e0 is not None:

@@ -339,6 +339,32 @@ def test_offload_attend_timer(dev):
     assert lines and lines[0].startswith("[attn time] tiers: n=5")
 
 
+def test_offload_access_trace(dev, tmp_path):
+    """trace= (ARC_OFFLOAD_DUMP): the layer's stores and attend rows go to the npz as the reference's _record lays
+    them out; the attention output is the untraced layer's."""
+    from arcagi2_flashnext_dots3_amd.diagnostics import AccessTrace
+    R, C, T, H, K = 3000, 800, 4, 64, 256
+    tr = AccessTrace(tmp_path / "acc", calls=2, unique=True, log=lambda m: None)
+    lo, _ = _offload_layer(dev, R, C, 22, trace=tr)          # the store before the first attend is not recorded
+    ref_lo, _ = _offload_layer(dev, R, C, 22)
+    q = make_q(T, H, seed=23).to(dev)
+    idx = distinct_idx(T, K, R, seed=24)
+    idx[0, 10:] = -1
+    print("[offload trace]", flush=True)
+    o = lo.attend(q, idx.to(dev), SM, 1.0, H, slots=torch.arange(5, 9, device=dev))
+    assert torch.equal(o, ref_lo.attend(q, idx.to(dev), SM, 1.0, H))
+    kv = torch.randn(2, 512).to(torch.bfloat16).to(dev)
+    pe = torch.randn(2, 64).to(torch.bfloat16).to(dev)
+    lo.store(kv, pe, torch.tensor([40, 41], device=dev))
+    lo.attend(q, idx.to(dev), SM, 1.0, H)
+    torch.cuda.synchronize()
+    z = np.load(tmp_path / "acc.npz")
+    want = np.unique(idx.numpy()[idx.numpy() >= 0]).astype(np.int32)
+    assert z["kinds"].tolist() == [0, 1, 0, 1] and int(z["C"]) == C and int(z["W"]) == 1 and int(z["R"]) == R
+    assert z["e0"].tolist() == [5, 6, 7, 8] and np.array_equal(z["e1"], want)
+    assert z["e2"].tolist() == [40, 41] and np.array_equal(z["e3"], want)
+
+
 def test_portable_impl_offload_decode_and_prefill(dev):
     """Offload mode: decode tokens via LayerOffload.attend, one prefill chunk via staged (compacted) rows; both
     against the oracle over the same rows."""

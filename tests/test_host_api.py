@@ -172,6 +172,55 @@ def test_topk_check_recall():
     assert lines and "mean recall=0.87500" in lines[0]
 
 
+def test_access_trace_window_and_file_layout(tmp_path):
+    """ARC_OFFLOAD_DUMP's record: nothing before after_s or below min_T tokens; then store slots (kind 0) and attend
+    rows (kind 1) until `calls` attend calls, saved as kinds / C / W / R / T / e<i> in an npz; unique mode keeps the
+    sorted distinct valid rows and the step's slots passed to attend."""
+    from arcagi2_flashnext_dots3_amd.diagnostics import AccessTrace
+    now = [100.0]
+    lines = []
+    tr = AccessTrace(tmp_path / "whole", calls=2, after_s=5.0, min_t=2, clock=lambda: now[0], log=lines.append)
+    idx = torch.tensor([[3, -1, 3], [7, 1, 2]], dtype=torch.int64)
+    tr.access(idx, 2, 8, 1, 16)                                     # before after_s: nothing
+    now[0] = 106.0
+    tr.access(idx[:1], 1, 8, 1, 16)                                 # T below min_T: nothing
+    tr.stored(torch.tensor([9]))                                    # not recording yet: nothing
+    tr.access(idx, 2, 8, 1, 16)
+    tr.stored(torch.tensor([4, 5]))
+    tr.access(idx + 1, 2, 8, 1, 16)
+    assert tr.done and len(lines) == 2 and "T=2 C=8 W=1 R=16" in lines[0]
+    z = np.load(tmp_path / "whole.npz")
+    assert z["kinds"].tolist() == [1, 0, 1] and int(z["C"]) == 8 and int(z["W"]) == 1 and int(z["R"]) == 16
+    assert int(z["T"]) == 2 and z["e0"].dtype == np.int32
+    assert np.array_equal(z["e0"], idx.numpy()) and z["e1"].tolist() == [4, 5] and np.array_equal(z["e2"], idx.numpy() + 1)
+    tr.access(idx, 2, 8, 1, 16)                                     # after the window: ignored
+    assert len(lines) == 2
+
+    tu = AccessTrace(tmp_path / "uniq", calls=1, unique=True, log=lines.append)
+    tu.access(idx, 2, 8, 4, 16, slots=torch.tensor([11, 12]))
+    z = np.load(tmp_path / "uniq.npz")
+    assert z["kinds"].tolist() == [0, 1] and z["e0"].tolist() == [11, 12] and z["e1"].tolist() == [1, 2, 3, 7]
+    assert int(z["W"]) == 4
+    with pytest.raises(ValueError):
+        AccessTrace(tmp_path / "x", calls=0)
+
+
+def test_access_trace_switches():
+    """ARC_OFFLOAD_DUMP=path,after_s,calls,min_T with ARC_OFFLOAD_DUMP_LAYERS picking backbone layers by their key
+    (path_L<n>, unique rows) or, without it, the first layer built; only device index 0 records."""
+    from arcagi2_flashnext_dots3_amd.diagnostics import AccessTrace
+    env = {"ARC_OFFLOAD_DUMP": "/tmp/d,2.5,7,3"}
+    assert AccessTrace.from_env(env={}) is None
+    t = AccessTrace.from_env(key="model.layers.4.attn.indexer", device="cuda:0", env=env)
+    assert t.path == "/tmp/d" and t.left == 7 and t.min_t == 3 and not t.unique
+    assert AccessTrace.from_env(device="cuda:0", first=False, env=env) is None
+    assert AccessTrace.from_env(device="cuda:1", env=env) is None
+    env["ARC_OFFLOAD_DUMP_LAYERS"] = "1,17"
+    assert AccessTrace.from_env(key="model.layers.4.attn", env=env) is None
+    t = AccessTrace.from_env(key="model.layers.17.attn", first=False, env=env)
+    assert t.path == "/tmp/d_L17" and t.unique
+
+
 def test_auto_split_respects_the_split_kernel_row_limit():
     """auto_split never picks a split whose rows per split pass the split kernel's limit (2048 rows, whole tiles of
     32): the unsplit head-group kernel takes any K."""
