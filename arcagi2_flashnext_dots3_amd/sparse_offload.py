@@ -83,13 +83,14 @@ class LayerOffload:
     the reference's two-choice set placement (ARC_OFFLOAD_TWO_CHOICE, offload_fill.py:16-23): a missing row whose set
     has no free way takes one in a second, hashed set before it spills; lookups and invalidations cover both sets.
     trace: a diagnostics.AccessTrace that records the stored slots and the decode rows of a window of calls.
+    stats_every=N: every N attend calls, `log` gets the cache's hit rate over that call's rows.
     """
 
     _count = 0           # layers built in this process (the first one takes the default access trace)
 
     def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
                  spill_rows=131072, overlap_fill=True, two_choice=False, cache_fmt="row656", packed=False,
-                 time_every=None, host_direct=False, trace=None):
+                 time_every=None, host_direct=False, trace=None, stats_every=None, log=print):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         if cache_mode not in ("static", "ways"):
@@ -129,6 +130,13 @@ class LayerOffload:
         self.trace = trace if trace is not None else AccessTrace.from_env(key, self.device,
                                                                          first=LayerOffload._count == 0)
         LayerOffload._count += 1
+        # the cache's hit rate over the step's rows as attend finds it, logged every N calls (ARC_OFFLOAD_STATS=N,
+        # sparse_offload.py:1540-1550; a host synchronization per logged call)
+        if stats_every is None:
+            stats_every = int(os.environ.get("ARC_OFFLOAD_STATS", "0") or 0)
+        self.stats_every = int(stats_every)
+        self.log = log
+        self._ncall = 0
         self.wc = None
         self.W = int(ways) if cache_mode == "ways" else 1
         if cache_mode == "ways":
@@ -270,6 +278,10 @@ class LayerOffload:
         timed with GPU events (arm: packed / ways / tiers / host)."""
         if self.trace is not None:
             self.trace.access(idx, q.shape[0], self.C, self.W, self.R, slots)
+        if self.stats_every:
+            self._ncall += 1
+            if self._ncall % self.stats_every == 0:
+                self._stat(idx)
         e0 = self.timer.begin(q.device)
         res = self._attend(q, idx, sm_scale, kv_scale, num_heads, ql, out, lse, return_lse)
         if e0 is not None:
@@ -442,6 +454,13 @@ class LayerOffload:
                 kernels.gather_tiers(self.host, host, mcnt, staged)
             kernels.attend_merge(q, staged, ident, sm_scale, kv_scale, op[0], lp[0], out=out, lse=lse, kcount=mcnt)
         return (out[:, :num_heads], lse[:, :num_heads]) if return_lse else out[:, :num_heads]
+
+    def _stat(self, idx):
+        f = idx.reshape(-1).to(torch.int64)
+        f = f[(f >= 0) & (f < self.R)]
+        if f.numel():
+            self.log(f"[offstats] C={self.C} rows={f.numel()} uniq={int(torch.unique(f).numel())} "
+                     f"hit={self.hit_rate(f.reshape(1, -1)):.3f}")
 
     def hit_rate(self, idx):
         """Fraction of the valid selected rows of idx [T, K] that the HBM cache holds."""

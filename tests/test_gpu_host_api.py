@@ -365,6 +365,25 @@ def test_offload_access_trace(dev, tmp_path):
     assert z["e2"].tolist() == [40, 41] and np.array_equal(z["e3"], want)
 
 
+def test_offload_hit_rate_stats(dev):
+    """stats_every (ARC_OFFLOAD_STATS): every N attend calls one line with the valid rows, the distinct rows and the
+    cache's hit rate over them as the call finds it."""
+    R, C, T, H, K = 3000, 800, 2, 64, 256
+    lines = []
+    lo, _ = _offload_layer(dev, R, C, 25, stats_every=2, log=lines.append)
+    lo.set_hot_rows(torch.arange(0, 2 * C, 2, dtype=torch.int64, device=dev))     # even rows below 1600
+    q = make_q(T, H, seed=26).to(dev)
+    idx = torch.full((T, K), -1, dtype=torch.int32)
+    idx[0, :100] = torch.arange(0, 200, 2)                  # 100 hits
+    idx[1, :100] = torch.arange(1, 200, 2)                  # 100 misses
+    idx[1, 100:150] = torch.arange(0, 100, 2)               # 50 hits, repeated from row 0
+    print("[offload stats]", flush=True)
+    for _ in range(3):
+        lo.attend(q, idx.to(dev), SM, 1.0, H)
+    torch.cuda.synchronize()
+    assert lines == ["[offstats] C=800 rows=250 uniq=200 hit=0.600"]
+
+
 def test_portable_impl_offload_decode_and_prefill(dev):
     """Offload mode: decode tokens via LayerOffload.attend, one prefill chunk via staged (compacted) rows; both
     against the oracle over the same rows."""
