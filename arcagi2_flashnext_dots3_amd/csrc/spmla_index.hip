@@ -5,10 +5,10 @@
 //   logit[row][j] = min(sum_h w[row][h] * relu(q[row][h] . kcode[j]) * ks[j], 60000) for positions j < ctx[row]
 //   (column j holds position j * P + rank of this rank's key store), -inf for j >= ctx (unless noinf); stored as fp32,
 //   or rounded to fp16 (the reference's ARC_SHARD_F16OUT buffer, shard_indexer.py:28-29, :124).
-//   gfx950: each wave streams 8 tiles of 32 keys through a private LDS ring filled by LDS DMA (codes, scales and
-//   block-table entries; two tiles in flight); S = Q K^T on bf16 MFMA (32x32x16; e4m3 key codes convert exactly to
-//   bf16, two per instruction), 64 heads = 2 M blocks, keys as the B operand; the head reduction is in-lane plus
-//   one cross-half exchange. (The fp8 MFMA would take the codes directly, but its internal accumulation keeps only
+//   gfx950: each wave loads the codes of its 32-key tiles straight into the registers of the MFMA B operand (three
+//   tiles of loads in flight; the logits of a workgroup staged in LDS and written once its waves are done);
+//   S = Q K^T on bf16 MFMA (32x32x16; e4m3 key codes convert exactly to bf16, two per instruction), 64 heads = 2 M
+//   blocks, keys as the B operand; the head reduction is in-lane plus one cross-half exchange. (The fp8 MFMA would take the codes directly, but its internal accumulation keeps only
 //   ~2^-12 of the largest product on gfx950, too coarse for the selection.)
 //
 // Top-k (dotsnote/engine/arcstats_pkg/arcstats/fast_topk.py:1-15, csrc/topk_select.cu:1-30 semantics):
@@ -42,7 +42,7 @@ __device__ inline uint32_t okey16(uint32_t h) {
 }
 
 // ------------------------------------------------------------------------------------------------ logits
-constexpr int LG_NWV = 12;                // waves per logits workgroup: the 12 a CU holds (3 per SIMD)
+constexpr int LG_NWV = 8;                 // waves per logits workgroup (2 per SIMD: 256 registers each)
 constexpr int LG_TPW = 16;                // 32-key tiles per wave and workgroup when the rows overfill the device
 
 struct LogitParams {
@@ -72,21 +72,20 @@ __device__ inline uint32_t fp8hi_bf16x2(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
 }
 
-// Logits workgroup: the 12 waves of one CU (one workgroup per CU, so no later-dispatched workgroup waits behind an
-// older one's issue priority) share a range of 32-key tiles of one row. Each wave computes all 64 heads of one tile
-// per step and takes its tiles one at a time from an LDS counter (claimed a step before its block-table copy goes
-// out), so the waves finish together whatever each one's memory service; the logits of a key do not depend on
-// which wave computes them. Per tile the key codes (32 rows x 128 B, 16-byte chunks XOR-swizzled by row so the MFMA
-// operand reads are bank-conflict free), the key scales and the block-table entries are copied global -> LDS by
-// LDS DMA into the wave's private rings: the codes of steps t + 1 and t + 2 and the block-table entries of steps
-// t + 3 and t + 4 are in flight while step t is computed. Completion is counted by hand (no other global load in
-// the loop), and no wave waits for another.
-constexpr int LG_NBUF = 3;                  // code / scale ring depth
-constexpr int LG_NBT = 4;                   // block-table ring depth
-constexpr int LG_CODES = 32 * 128;
-constexpr int LG_OFF_SC = LG_NBUF * LG_CODES;
-constexpr int LG_OFF_BT = LG_OFF_SC + LG_NBUF * 128;
-constexpr int LG_WAVE = LG_OFF_BT + LG_NBT * 128;   // LDS bytes per wave
+// Logits workgroup: the waves of one CU (one workgroup per CU, so no later-dispatched workgroup waits behind an
+// older one's issue priority) share a range of 32-key tiles of one row; wave w computes tiles tb + w, tb + w + NW,
+// ... (NW = LG_NWV), all 64 heads of a tile per step. The key codes go straight from global memory into the
+// registers of the MFMA B operand: lane (k, h) of a tile loads 16-byte chunks 2 kp + h (kp = 0..3) of key k, which
+// are the key's dims 32 kp + 16 h .. + 15 in the order the operand takes them, and the key's scale. A wave keeps
+// LG_D tiles of loads in flight: step t computes tile t, then loads the codes of tile t + LG_D (whose block-table
+// entries were loaded at step t - LG_D) and the block-table entries of tile t + 2 LG_D, so the one wait of a step
+// (for the loads of step t - LG_D) leaves LG_D - 1 steps of loads outstanding. A workgroup whose range holds at
+// most LG_STAGE columns keeps its logits in LDS (with a per-tile mask of the columns to write) and writes them in
+// one pass once every wave is done: the logit stores interleaved with the key reads cost 20% of the read rate at
+// 131072 columns per row (measured on MI355X with a probe of the same access pattern: 181 us for the reads alone,
+// 226 us with a 128-byte store per tile, 201 us with the stores staged to the end).
+constexpr int LG_D = 3;                    // steps of loads in flight per wave
+constexpr int LG_STAGE = 32768;            // columns a workgroup stages in LDS before writing them (128 KiB fp32)
 
 // Key layouts: LY_ROW 132-byte rows [128 codes | scale] (the rank-sharded store); LY_SHUF vLLM's paged SHUFFLE
 // layout (P = 1, rpb = keys per block): key t of a block has its 16-byte chunk c at (t / 16) * 2048 + (t % 16) * 16
@@ -94,16 +93,18 @@ constexpr int LG_WAVE = LG_OFF_BT + LG_NBT * 128;   // LDS bytes per wave
 // prefill gather: key j (column j) at store + j * k_st, scale kscale[j], valid for lo[row] <= j < ctx[row], no
 // block table (dsa_sm89.py:97-118).
 enum { LY_ROW = 0, LY_SHUF = 1, LY_FLAT = 2 };
+typedef uint32_t u32x4u __attribute__((ext_vector_type(4), aligned(4)));   // 16 bytes at a 4-byte boundary
 template <bool POW2, int LY, bool F16OUT = false>
 __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
   constexpr bool SHUF = LY == LY_SHUF, FLAT = LY == LY_FLAT;
-  __shared__ __attribute__((aligned(16))) uint8_t lds_raw[LG_NWV * LG_WAVE];
-  __shared__ int claim;                                     // next unclaimed tile of the workgroup's range
+  constexpr int D = LG_D;
   __shared__ uint32_t hh[1024];                             // level-0 histogram (p.hist): 2048 16-bit counts
+  __shared__ float sbuf[LG_STAGE];                          // staged logits of the range's columns
+  __shared__ uint32_t smask[LG_STAGE / 32];                 // per tile: the columns to write
   const int row = blockIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  SPMLA_LDS uint8_t* lds = (SPMLA_LDS uint8_t*)lds_raw + wv * LG_WAVE;
   const int lane = threadIdx.x & 63;
+  const bool stage = 32LL * p.tpg <= LG_STAGE;              // uniform
   const int half = lane >> 5, l32 = lane & 31;
   const int ctx = p.ctx[row];
   float* orow = (float*)p.out + (long long)row * p.out_st;            // fp32 output row
@@ -112,7 +113,7 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
     if constexpr (F16OUT) hrow[j] = (_Float16)v;                       // round to nearest even (+-inf kept)
     else orow[j] = v;
   };
-  // tiles [tb, te) of the row; keys j with j P + rank < ctx lie in tiles below tv (claimable)
+  // tiles [tb, te) of the row; keys j with j P + rank < ctx lie in tiles below tv (computed)
   const int tb = blockIdx.y * p.tpg;
   const int te = min(tb + p.tpg, (p.Lc + 31) >> 5);
   const long long nvalid = ctx > p.rank ? ((long long)ctx - p.rank + p.P - 1) / p.P : 0;   // keys below ctx
@@ -126,10 +127,10 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
       for (int b = (int)threadIdx.x; b < 2048; b += LG_NWV * 64) hrow_out[b] = 0u;
     return;
   }
-  if (threadIdx.x == 0) claim = tb + 5 * LG_NWV;
-  if (hrow_out)
+  if (hrow_out) {
     for (int b = (int)threadIdx.x; b < 1024; b += LG_NWV * 64) hh[b] = 0u;
-  __syncthreads();
+    __syncthreads();
+  }
   const int nh = hrow_out ? min(ctx, p.Lc) : 0;             // columns the histogram counts
   const int* btr = FLAT ? nullptr : p.bt + (long long)p.req[row] * p.bt_st;
   const int lo = p.lo ? p.lo[row] : 0;
@@ -138,63 +139,52 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
   auto md = [&](uint32_t n, uint32_t d, int sh) -> uint32_t { return POW2 ? n & (d - 1u) : n % d; };
   // positions without a block-table entry read the range's first entry (key 32 tb < nvalid: in range)
   const int* bt_dummy = FLAT ? nullptr : btr + dv((uint32_t)(32 * tb * p.P + p.rank), (uint32_t)p.bs, p.bs_sh);
-  // step t of the wave computes tile id; a tile id at or past tv is no tile (the wave's ids only grow)
+  // key r of tile id: its position, and whether it is a key of the row (id < tv: tiles past tv are no tiles)
   auto key_pos = [&](int id, int r, uint32_t& pos) -> bool {
     const int j = 32 * id + r;
     const long long ps = (long long)j * p.P + p.rank;
     pos = (uint32_t)ps;
     return id < tv && j < p.Lc && ps < ctx && ps >= lo;
   };
-  // LDS DMA of the block-table entries of step t (tile id; lanes 0..31: key l32)
-  auto issue_bt = [&](int t, int id) {
-    if (!FLAT && lane < 32) {
-      uint32_t pos;
-      const bool in = key_pos(id, l32, pos);
-      dma4(in ? btr + dv(pos, (uint32_t)p.bs, p.bs_sh) : bt_dummy, lds + LG_OFF_BT + (t & (LG_NBT - 1)) * 128);
-    }
+  // the block-table entry of this lane's key of tile id (a load from the range's first entry when there is none;
+  // the value is first read when the tile's codes are loaded, LG_D steps later)
+  auto load_bt = [&](int id) -> int {
+    if constexpr (FLAT) return 0;
+    uint32_t pos;
+    const bool in = key_pos(id, l32, pos);
+    return *(in ? btr + dv(pos, (uint32_t)p.bs, p.bs_sh) : bt_dummy);
   };
-  // LDS DMA of the codes and scales of step t (tile id; its block-table entries already in LDS). Lane l32 maps key
-  // l32 to its row; the copying lanes take the row addresses from those lanes. Returns the lane's key-valid flag.
-  auto issue_codes = [&](int t, int id) -> bool {
+  // the codes (chunks 2 kp + half) and scale of this lane's key of tile id; keys that are none read row 0
+  auto load_codes = [&](int id, int blk, u32x4 (&c)[4], float& sc) -> bool {
     uint32_t pos;
     bool ok = key_pos(id, l32, pos);
     const uint8_t* rp;
-    const void* sp;
+    const float* sp;
+    uint32_t cs;                                       // bytes from chunk c to chunk c + 1
     if (FLAT) {                                        // key pos itself (pos < Lc = number of keys)
       rp = p.store + (long long)(ok ? pos : 0u) * p.k_st;
       sp = p.kscale + (ok ? pos : 0u);
+      cs = 16;
     } else {
-      const int blk = ((const SPMLA_LDS int*)(lds + LG_OFF_BT + (t & (LG_NBT - 1)) * 128))[l32];
       ok = ok && blk >= 0;
       const long long tt = (long long)blk * p.bs + md(pos, (uint32_t)p.bs, p.bs_sh);
       ok = ok && tt < p.lim;
       const uint32_t lrow = ok ? dv((uint32_t)tt, (uint32_t)p.P, p.p_sh) : 0u;   // p.lim > 0: row 0 exists
       const uint8_t* kblk = p.store + (long long)dv(lrow, (uint32_t)p.rpb, p.rpb_sh) * p.blk_stride;
       const uint32_t kt = md(lrow, (uint32_t)p.rpb, p.rpb_sh);
-      rp = SHUF ? kblk + (kt >> 4) * 2048u + (kt & 15u) * 16u : kblk + kt * 132u;   // chunk 0
-      sp = SHUF ? kblk + (uint32_t)p.rpb * 128u + 4u * kt : rp + 128;               // scale
+      rp = SHUF ? kblk + (kt >> 4) * 2048u + (kt & 15u) * 16u : kblk + kt * 132u;            // chunk 0
+      sp = (const float*)(SHUF ? kblk + (uint32_t)p.rpb * 128u + 4u * kt : rp + 128);      // scale
+      cs = SHUF ? 256u : 16u;
     }
-    const long long ra = (long long)(uintptr_t)rp;
-    SPMLA_LDS uint8_t* cb = lds + (t % LG_NBUF) * LG_CODES;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 8 * i + (lane >> 3);
-      const int c = (lane & 7) ^ (r & 7);               // chunk that lands in 16-byte slot lane & 7 of row r
-      const long long a = __shfl(ra, r, 64);
-      dma16((const uint8_t*)(uintptr_t)a + (SHUF ? 256 : 16) * c, cb + 8 * i * 128);
+    for (int kp = 0; kp < 4; ++kp) {
+      const u32x4u v = *(const u32x4u*)(rp + cs * (uint32_t)(2 * kp + half));
+      c[kp] = u32x4{v[0], v[1], v[2], v[3]};
     }
-    if (lane < 32) dma4(sp, lds + LG_OFF_SC + (t % LG_NBUF) * 128);
+    sc = *sp;
     return ok;
   };
 
-  // tile ids of steps t .. t + 4 (uniform); steps 0 .. 4 take tiles tb + k LG_NWV + wv, later ones are claimed
-  int i0 = tb + wv, i1 = i0 + LG_NWV, i2 = i1 + LG_NWV, i3 = i2 + LG_NWV, i4 = i3 + LG_NWV;
-  // prologue: block-table entries of steps 0..3 (waited for), then the codes of steps 0 and 1; the query loads
-  // overlap the copies
-  issue_bt(0, i0);
-  issue_bt(1, i1);
-  issue_bt(2, i2);
-  issue_bt(3, i3);
   // query fragments (bf16 A operand): M block m = heads 32m..32m+31 (lane head 32m + l32); k-pair kp covers dims
   // 32kp + 16half + 0..15, MFMA 2kp taking the first 8 and 2kp+1 the next 8 (same permutation as the key operand)
   const uint16_t* qr = p.q + (long long)row * p.q_st;
@@ -213,33 +203,16 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) wl[m][i] = __shfl(myw, 8 * (i >> 2) + 4 * half + (i & 3), 64);
   }
-  wait_vm<0>();
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");   // DMA'd entries read below after the wait
-  bool ok0 = issue_codes(0, i0);
-  bool ok1 = issue_codes(1, i1);
-  int nprev = 5;                                            // copies issued by the previous step
 
-#pragma unroll 1
-  for (int t = 0; i0 < tv; ++t) {
-    // codes / scales of tile t and block-table entries of tile t + 2 are complete once at most the previous
-    // step's copies are outstanding
-    if (nprev == 6) wait_vm<6>();
-    else if (nprev == 5) wait_vm<5>();
-    else wait_vm<0>();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    bool ok2 = false;
-    nprev = 0;
-    if (i2 < tv) { ok2 = issue_codes(t + 2, i2); nprev = 5; }
-    if (!FLAT && i4 < tv) { issue_bt(t + 4, i4); nprev += 1; }
-    // the tile of step t + 5, read at the next step (an LDS atomic: no vector-memory count)
-    int nxt = 0;
-    if (lane == 0) nxt = atomicAdd(&claim, 1);
-    // tile t
-    const SPMLA_LDS uint8_t* cb = lds + (t % LG_NBUF) * LG_CODES + l32 * 128;
+  // tile id of the wave's step t; the wave has n steps
+  auto tile = [&](int t) { return tb + wv + t * LG_NWV; };
+  const int n = tv - tb > wv ? (tv - tb - wv + LG_NWV - 1) / LG_NWV : 0;
+  // step t computes tile t
+  auto compute = [&](int id, const u32x4 (&c)[4], float sc, bool ok) {
     bf16x8 kb[8];
 #pragma unroll
     for (int kp = 0; kp < 4; ++kp) {
-      const u32x4 w4 = *(const SPMLA_LDS u32x4*)(cb + 16 * ((2 * kp + half) ^ (l32 & 7)));
+      const u32x4 w4 = c[kp];
       i32x4 a0, a1;
       a0[0] = (int)fp8lo_bf16x2(w4[0]); a0[1] = (int)fp8hi_bf16x2(w4[0]);
       a0[2] = (int)fp8lo_bf16x2(w4[1]); a0[3] = (int)fp8hi_bf16x2(w4[1]);
@@ -248,7 +221,6 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
       kb[2 * kp] = __builtin_bit_cast(bf16x8, a0);
       kb[2 * kp + 1] = __builtin_bit_cast(bf16x8, a1);
     }
-    const float sc = *(const SPMLA_LDS float*)(lds + LG_OFF_SC + (t % LG_NBUF) * 128 + 4 * l32);
     f32x16 acc0 = f32x16{}, acc1 = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -267,31 +239,73 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
     }
     float part = pa + pb;
     part += __shfl_xor(part, 32, 64);
-    const int j = 32 * i0 + l32;
-    if (half == 0 && j < p.Lc) {
-      const float lg = p.clamp ? fminf(part * sc, 60000.f) : part * sc;
-      const bool counted = j < nh;                          // a top-k column: always written
-      if (ok0) put(j, lg);
-      else if (!p.noinf || counted) put(j, -__builtin_inff());
-      if (counted) {                                        // the key of the value as stored
-        const float v = ok0 ? lg : -__builtin_inff();
-        uint32_t key;
-        if constexpr (F16OUT) key = okey16(__builtin_bit_cast(uint16_t, (_Float16)v));
-        else key = okey(v);
-        const uint32_t bin = key >> 21;
-        atomicAdd(&hh[bin >> 1], 1u << (16 * (bin & 1u)));
+    const int j = 32 * id + l32;
+    const float lg = p.clamp ? fminf(part * sc, 60000.f) : part * sc;
+    const float v = ok ? lg : -__builtin_inff();
+    const bool counted = half == 0 && j < nh;               // a top-k column: always written
+    const bool wr = half == 0 && j < p.Lc && (ok || !p.noinf || counted);
+    if (stage) {
+      if (half == 0) sbuf[32 * (id - tb) + l32] = v;
+      const uint64_t m = __ballot(wr);
+      if (lane == 0) smask[id - tb] = (uint32_t)m;
+    } else if (wr) {
+      put(j, v);
+    }
+    if (counted) {                                          // the key of the value as stored
+      uint32_t key;
+      if constexpr (F16OUT) key = okey16(__builtin_bit_cast(uint16_t, (_Float16)v));
+      else key = okey(v);
+      const uint32_t bin = key >> 21;
+      atomicAdd(&hh[bin >> 1], 1u << (16 * (bin & 1u)));
+    }
+  };
+
+  // loads in flight: codes of steps t .. t + D - 1 (slot t % D), block-table entries of steps t + D .. t + 2D - 1
+  // (slot t % 2D). Every step issues the same loads (steps past n read the row-0 key and the range's first
+  // block-table entry, cache hits, and are not computed), so the compiler's wait before a step's first use of its
+  // codes counts the loads of the D - 1 steps after it on every path.
+  u32x4 cd[D][4];
+  float scv[D];
+  bool okv[D];
+  int btv[2 * D];
+#pragma unroll
+  for (int k = 0; k < 2 * D; ++k) btv[k] = load_bt(tile(k));
+#pragma unroll
+  for (int k = 0; k < D; ++k) okv[k] = load_codes(tile(k), btv[k], cd[k], scv[k]);
+#pragma unroll 1
+  for (int t0 = 0; t0 < n; t0 += 2 * D) {
+#pragma unroll
+    for (int s = 0; s < 2 * D; ++s) {
+      const int t = t0 + s;
+      if (t < n) compute(tile(t), cd[s % D], scv[s % D], okv[s % D]);     // uniform
+      okv[s % D] = load_codes(tile(t + D), btv[(s + D) % (2 * D)], cd[s % D], scv[s % D]);
+      btv[s] = load_bt(tile(t + 2 * D));
+    }
+  }
+  if (stage || hrow_out) __syncthreads();   // every wave has computed (and counted) its tiles
+  if (stage) {                               // 4 columns per thread: one 16-byte (fp16: 8-byte) store when all go out
+    const int ncol = 32 * (tv - tb);
+    const bool vec = ((uintptr_t)p.out & (F16OUT ? 7u : 15u)) == 0 && (p.out_st & 3) == 0;   // j % 4 == 0 below
+    for (int i = 4 * (int)threadIdx.x; i < ncol; i += 4 * LG_NWV * 64) {
+      const int j = 32 * tb + i;
+      const uint32_t m4 = (smask[i >> 5] >> (i & 31)) & 15u;
+      const f32x4 v4 = *(const f32x4*)&sbuf[i];
+      if (vec && m4 == 15u && j + 3 < p.Lc) {
+        if constexpr (F16OUT) {
+          typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+          *(f16x4*)(hrow + j) = f16x4{(_Float16)v4[0], (_Float16)v4[1], (_Float16)v4[2], (_Float16)v4[3]};
+        } else {
+          *(f32x4*)(orow + j) = v4;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (((m4 >> k) & 1u) && j + k < p.Lc) put(j + k, v4[k]);
       }
     }
-    ok0 = ok1;
-    ok1 = ok2;
-    i0 = i1; i1 = i2; i2 = i3; i3 = i4;
-    i4 = __builtin_amdgcn_readfirstlane(nxt);
   }
-  wait_vm<0>();                              // copies of steps past the last tile (dummy rows) land before exit
-  if (hrow_out) {                            // every wave has counted its tiles
-    __syncthreads();
+  if (hrow_out)
     for (int b = (int)threadIdx.x; b < 2048; b += LG_NWV * 64) hrow_out[b] = (hh[b >> 1] >> (16 * (b & 1))) & 0xffffu;
-  }
 }
 
 // ------------------------------------------------------------------------------------------------ top-k
