@@ -18,7 +18,7 @@
 //   16-bit pattern placed in the top half of the 32-bit key (low half zero), so one radix code serves both.
 //   gfx950: one 1024-thread workgroup per row, the row's keys in VGPRs (32 per thread, all loads in flight):
 //   11/11/10-bit radix levels with an LDS histogram; keys above the boundary bin are appended at slots from a block
-//   scan of per-thread counts (wave scans on DPP); once the boundary bin holds at most TK_CAP keys the remaining
+//   scan of per-thread counts (wave scans on DPP); once the boundary bin holds at most the candidate cap the remaining
 //   levels run on those candidates alone; ties on the final key take the lowest columns. The K winners are
 //   bitonic-sorted in LDS (only the stages whose pairs cross waves take a workgroup barrier); on the several-
 //   workgroup path, whose lists arrive in column order, fp16 winners are ordered by a stable radix sort instead.
@@ -311,7 +311,8 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
 // ------------------------------------------------------------------------------------------------ top-k
 constexpr int TK_NT = 1024;
 constexpr int TK_KMAX = 2048;
-constexpr int TK_CAP = 4096;
+constexpr int TK_CAP = 8192;              // candidate list capacity (workspace and LDS)
+constexpr int TK_CAP1 = 4096;             // the one-workgroup path's candidate threshold
 
 // key of logit j of a row (fp32 or fp16 elements)
 template <bool F16>
@@ -592,7 +593,7 @@ __device__ inline void tk_slots(uint32_t ns, uint32_t nc, TopkLds& L, uint32_t& 
 
 constexpr int TK_KPT = 32;                 // keys per thread per chunk (held in VGPRs)
 constexpr int TK_CH = TK_KPT * TK_NT;      // 32768 columns per chunk
-constexpr int TK_EPT = TK_CAP / TK_NT;     // boundary-bin candidates per thread
+constexpr int TK_EPT = TK_CAP / TK_NT;     // boundary-bin candidates per thread at the full capacity
 
 template <class Src>
 __device__ inline void tk_load(const Src& src, int base, uint32_t (&k)[TK_KPT]) {
@@ -606,16 +607,17 @@ __device__ inline void tk_load(const Src& src, int base, uint32_t (&k)[TK_KPT]) 
 // Finishes a selection from the boundary-bin candidates L.cand[0, nc) (all under (prefix, mask) of level lvl - 1):
 // radix levels lvl..2 on the candidates held in registers; equal final keys go to the lowest columns. sb = entries
 // already in L.sel.
+template <int EPT = TK_EPT>                       // candidates per thread: nc <= EPT * TK_NT
 __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, uint32_t prefix, uint32_t mask,
                                                  uint32_t need, uint32_t sb, int ncols) {
   const int tid = threadIdx.x;
-  unsigned long long e[TK_EPT];
+  unsigned long long e[EPT];
   uint32_t vm = 0;                                   // bit i: e[i] is a candidate
   int t = tid;                                       // opaque copy: keeps the slot indices from being hoisted
   asm volatile("" : "+v"(t));
 #pragma unroll
-  for (int i = 0; i < TK_EPT; ++i) {              // consecutive candidates: the winners appended below keep their
-    const int c = TK_EPT * t + i;                  // order in L.cand (column order for the workspace path)
+  for (int i = 0; i < EPT; ++i) {              // consecutive candidates: the winners appended below keep their
+    const int c = EPT * t + i;                  // order in L.cand (column order for the workspace path)
     vm |= (uint32_t)(c < nc) << i;
     e[i] = c < nc ? L.cand[c] : 0ull;
   }
@@ -624,7 +626,7 @@ __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, ui
     const uint32_t dm = tk_dmask(level);
     tk_clear_hist(L);
 #pragma unroll
-    for (int i = 0; i < TK_EPT; ++i) {
+    for (int i = 0; i < EPT; ++i) {
       const uint32_t k = (uint32_t)(e[i] >> 32);
       if (((vm >> i) & 1u) && (k & mask) == prefix) tk_hist_add(L, (k >> shift) & dm);
     }
@@ -634,7 +636,7 @@ __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, ui
     const bool whole = above + binc == need;
     uint32_t selm = 0;
 #pragma unroll
-    for (int i = 0; i < TK_EPT; ++i) {
+    for (int i = 0; i < EPT; ++i) {
       const uint32_t k = (uint32_t)(e[i] >> 32);
       const uint32_t d = (k >> shift) & dm;
       const bool in = ((vm >> i) & 1u) && (k & mask) == prefix;
@@ -643,7 +645,7 @@ __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, ui
     uint32_t cb = 0, so, co;
     tk_slots(__popc(selm), 0u, L, sb, cb, so, co);
 #pragma unroll
-    for (int i = 0; i < TK_EPT; ++i)
+    for (int i = 0; i < EPT; ++i)
       if ((selm >> i) & 1u) L.sel[so++] = e[i];
     if (whole) { __syncthreads(); return; }
     prefix |= b << shift;
@@ -653,7 +655,7 @@ __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, ui
       // binc candidates carry the final key; the need lowest columns win
       uint32_t eqm = 0;
 #pragma unroll
-      for (int i = 0; i < TK_EPT; ++i)
+      for (int i = 0; i < EPT; ++i)
         eqm |= (uint32_t)(((vm >> i) & 1u) && (uint32_t)(e[i] >> 32) == prefix) << i;
       constexpr int BM_WPT = 8;                    // bitmap words per thread: TK_NT * 8 words in the histogram space
       static_assert(TK_NT * BM_WPT <= TK_HCOPY * TK_HSTR, "bitmap fits the histogram space");
@@ -666,7 +668,7 @@ __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, ui
         for (int w = tid; w < words; w += TK_NT) L.hist[w] = 0u;
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < TK_EPT; ++i)
+        for (int i = 0; i < EPT; ++i)
           if ((eqm >> i) & 1u) {
             const uint32_t j = ~(uint32_t)e[i];
             atomicOr(&L.hist[j >> 5], 1u << (j & 31u));
@@ -697,7 +699,7 @@ __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, ui
       uint32_t cb2 = 0, sb2 = 0;
       tk_slots(0u, __popc(eqm), L, sb2, cb2, so, co);
 #pragma unroll
-      for (int i = 0; i < TK_EPT; ++i)
+      for (int i = 0; i < EPT; ++i)
         if ((eqm >> i) & 1u) L.cand[co++] = (unsigned long long)(uint32_t)e[i] << 32;   // ~j high: desc = j asc
       __syncthreads();
       tk_sort_desc(L.cand, (int)binc);
@@ -711,7 +713,7 @@ __device__ __forceinline__ void tk_resolve_cands(TopkLds& L, int nc, int lvl, ui
 // Selects the K largest candidates (key desc, j asc) of src into L.sel (unordered); returns their number min(n, K).
 // The row's keys sit in VGPRs (32 per thread; longer rows are re-read per 32768-column chunk with all loads of a
 // chunk in flight). Each radix level builds an LDS histogram; the keys above the boundary bin are written to slots
-// from one block scan of per-thread counts; a boundary bin of at most TK_CAP keys is finished on the candidates alone.
+// from one block scan of per-thread counts; a boundary bin of at most TK_CAP1 keys is finished on the candidates alone.
 template <class Src>
 __device__ __forceinline__ int tk_select(const Src& src, int K, TopkLds& L) {
   const int tid = threadIdx.x, n = src.n;
@@ -744,7 +746,7 @@ __device__ __forceinline__ int tk_select(const Src& src, int K, TopkLds& L) {
     uint32_t b, above, binc;
     tk_bin(L, need, b, above, binc);
     const bool whole = above + binc == need;
-    const bool fits = !whole && level < 2 && binc <= (uint32_t)TK_CAP;
+    const bool fits = !whole && level < 2 && binc <= (uint32_t)TK_CAP1;
     uint32_t cb = 0;
     for (int c = 0; c < nch; ++c) {
       if (nch > 1) tk_load(src, c * TK_CH, key);
@@ -769,7 +771,7 @@ __device__ __forceinline__ int tk_select(const Src& src, int K, TopkLds& L) {
     __syncthreads();
     if (whole) return K;
     if (fits) {
-      tk_resolve_cands(L, (int)binc, level + 1, prefix | (b << shift), mask | (dm << shift), need - above, sb, n);
+      tk_resolve_cands<TK_CAP1 / TK_NT>(L, (int)binc, level + 1, prefix | (b << shift), mask | (dm << shift), need - above, sb, n);
       return K;
     }
     prefix |= b << shift;
@@ -932,7 +934,7 @@ __global__ void __launch_bounds__(TK_NT) topk_kernel(TopkParams p) {
 //   hist:    the histogram of the level-0 11-bit digit over each chunk's keys;
 //   collect: every workgroup sums the G histograms of the level and finds the boundary bin b of the row's
 //            remaining need; it writes its chunk's keys above b (and in b when that completes the need) to the row's
-//            winner list, and the keys in b to the candidate list when the bin holds at most TK_CAP keys. A chunk's
+//            winner list, and the keys in b to the candidate list when the bin holds at most p.cap keys. A chunk's
 //            entries start at the offset the histograms of the chunks before it give; inside the chunk each wave
 //            takes its slots from a block scan per pass over 8 consecutive columns per thread, so every list is
 //            in column order (the finishing pass's stable radix sort of fp16 keys relies on it). Otherwise the
@@ -979,6 +981,7 @@ struct TopkWsParams {
   int* out; long long out_st;
   uint8_t* ws; TopkWs w;
   unsigned long long* ovf;                        // optional overflow lists, G * CL entries per row (or null)
+  int cap;                                        // boundary bins of at most cap keys go to the finishing pass
   int level;
 };
 
@@ -1064,7 +1067,7 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   __syncthreads();
   const uint32_t b = sh[1], above = sh[2], binc = sh[3];
   const bool whole = above + binc == need;
-  const bool fits = !whole && binc <= (uint32_t)TK_CAP;
+  const bool fits = !whole && binc <= (uint32_t)p.cap;
   // this chunk's offsets: winners of the chunks before g (bins above b, and b itself when whole); candidates in b
   const uint32_t mine = ((uint32_t)b0 > b || (whole && (uint32_t)b0 == b) ? q0 : 0u) +
                         ((uint32_t)b1 > b || (whole && (uint32_t)b1 == b) ? q1 : 0u);
@@ -1186,7 +1189,7 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   }
 }
 
-template <bool F16>
+template <bool F16, int CAPK>                      // CAPK: the launch's candidate cap (p.cap)
 __global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
   __shared__ TopkLds L;
   const int row = blockIdx.x, tid = threadIdx.x;
@@ -1204,7 +1207,7 @@ __global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
     nsel = tk_select(src, p.K, L);                  // few columns, or ties too heavy for the lists
   } else {
     // the header's counts, kept inside the lists (they are, whenever the histograms were this row's)
-    const int nsb = min(max(st.sb, 0), p.K), nbc = min(max(st.binc, 0), TK_CAP);
+    const int nsb = min(max(st.sb, 0), p.K), nbc = min(max(st.binc, 0), CAPK);
     const uint32_t nneed = (uint32_t)min(max(st.need, 0), p.K - nsb);
     const unsigned long long* sel = p.w.sel(p.ws, row);
     for (int i = tid; i < nsb; i += TK_NT) L.sel[i] = sel[i];
@@ -1214,7 +1217,7 @@ __global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
     }
     __syncthreads();
     if (st.state == TKW_CANDS)
-      tk_resolve_cands(L, nbc, st.lvl, (uint32_t)st.prefix, (uint32_t)st.mask, nneed, (uint32_t)nsb, n);
+      tk_resolve_cands<CAPK / TK_NT>(L, nbc, st.lvl, (uint32_t)st.prefix, (uint32_t)st.mask, nneed, (uint32_t)nsb, n);
     if constexpr (F16) {
       // fp16 keys: at most two radix passes (the keys' low half is zero), faster than the bitonic network here;
       // fp32 keys need three or four, slower than it (measured on the bench's indexer logits)
@@ -1355,7 +1358,8 @@ static void topk_ws_passes(TopkWsParams p, hipStream_t stream, bool hist = true)
     hipLaunchKernelGGL(topk_collect_kernel<F16>, dim3(p.rows, p.w.G), dim3(TK_NT), 0, stream, p);
   }
   p.level = 2;                                      // header 2: the state after both levels
-  hipLaunchKernelGGL(topk_finish_kernel<F16>, dim3(p.rows), dim3(TK_NT), 0, stream, p);
+  if (p.cap > TK_CAP1) hipLaunchKernelGGL((topk_finish_kernel<F16, TK_CAP>), dim3(p.rows), dim3(TK_NT), 0, stream, p);
+  else hipLaunchKernelGGL((topk_finish_kernel<F16, TK_CAP1>), dim3(p.rows), dim3(TK_NT), 0, stream, p);
 }
 
 }  // namespace idx
@@ -1546,6 +1550,10 @@ static int topk_ws_run(const void* logits, long long lg_st, const int* ctx, int 
   p.ws = (uint8_t*)ws; p.w = idx::topk_ws_layout(Lc);
   // with room for the overflow lists, a level that narrows hands its bin's keys to the next level in a list
   p.ovf = ovf > 0 && ws_bytes >= base + ovf ? (unsigned long long*)((uint8_t*)ws + base) : nullptr;
+  // fp32 rows of at most 32768 columns: the finishing pass takes boundary bins of up to 8192 keys, so the level-1
+  // collect has no row to refine on indexer logits (their level-0 bins hold up to ~21% of such a row); longer rows
+  // keep 4096 (their bins pass 8192 anyway, and longer candidate lists only slow the finishing pass)
+  p.cap = dtype == 0 && Lc <= 32768 ? idx::TK_CAP : idx::TK_CAP1;
   if (dtype == 1) idx::topk_ws_passes<true>(p, (hipStream_t)stream, hist);
   else idx::topk_ws_passes<false>(p, (hipStream_t)stream, hist);
   return (int)hipGetLastError();

@@ -112,6 +112,27 @@ def test_topk_concentrated_values(dev):
     _topk_check(dev, lg, ctx, 2048)
 
 
+def test_topk_bins_around_the_candidate_cap(dev):
+    """fp32 rows of 32768 columns whose first-digit boundary bin holds 6000 / 8192 / 8193 / 9000 keys (1000 keys
+    above it, K = 2048): bins of at most 8192 keys are resolved by the finishing pass from the candidate list (the
+    workspace path's cap at this row length), larger ones by a second collect level; every seventh bin value is the
+    same, so the final level resolves ties by column."""
+    g = np.random.default_rng(11)
+    L = 32768
+    sizes = [6000, 8192, 8193, 9000]
+    lg = np.empty((len(sizes), L), np.float32)
+    for r, nb in enumerate(sizes):
+        v = g.uniform(0.0, 200.0, L).astype(np.float32)              # below the bin
+        v[:1000] = g.uniform(400.0, 500.0, 1000)                     # above it (same exponent, higher digit)
+        vals = g.uniform(256.0, 320.0, nb).astype(np.float32)        # one first-digit bin: [256, 320)
+        vals[::7] = 300.0
+        v[1000:1000 + nb] = vals
+        lg[r] = g.permutation(v)
+    ctx = np.full(len(sizes), L, dtype=np.int32)
+    print("[topk] bins around the candidate cap", flush=True)
+    _topk_check(dev, lg, ctx, 2048)
+
+
 def test_topk_ctx_lengths_fixture(dev):
     # context lengths from the reference's own fixture (runtime_dataset/ctx_lengths.json), clipped to L
     with open(os.path.join(HERE, "golden", "ctx_lengths.json")) as f:
