@@ -1038,9 +1038,9 @@ __global__ void __launch_bounds__(TK_NT) topk_collect_kernel(TopkWsParams p) {
   __shared__ uint32_t sh[8];
   __shared__ uint32_t nh[TK_HCOPY * TK_HSTR];       // the next level's histogram of this chunk (when narrowing)
   const int row = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  const TkwHdr st = tkw_state(p, row);              // read beside the row length: one round trip for both
   const int n = tkw_n(p, row);
   if (n <= p.K) return;
-  const TkwHdr st = tkw_state(p, row);
   TkwHdr* next = p.w.hdr(p.ws, row) + p.level + 1;
   if (st.state != TKW_SELECT) {                     // settled at an earlier level: carry the state forward
     if (g == 0 && tid == 0) *next = st;
@@ -1197,12 +1197,8 @@ __global__ void __launch_bounds__(TK_NT) topk_finish_kernel(TopkWsParams p) {
   const RowSrc<F16> src{lrow<F16>(p.lg, row, p.lg_st), n};
   int* o = p.out + (long long)row * p.out_st;
   int nsel = 0;
-  bool full = n <= p.K;
-  TkwHdr st{};
-  if (!full) {
-    st = p.w.hdr(p.ws, row)[p.level];
-    full = st.state != TKW_WHOLE && st.state != TKW_CANDS;
-  }
+  const TkwHdr st = p.w.hdr(p.ws, row)[p.level];   // read beside the row length (unused when n <= K)
+  const bool full = n <= p.K || (st.state != TKW_WHOLE && st.state != TKW_CANDS);
   if (full) {
     nsel = tk_select(src, p.K, L);                  // few columns, or ties too heavy for the lists
   } else {
