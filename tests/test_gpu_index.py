@@ -66,6 +66,47 @@ def _topk_check(dev, lg, ctx, K):
         assert bad.size == 0, f"single_pass={single} ws={'small' if ws is not None else 'full'}: rows {bad[:8]} differ"
 
 
+@pytest.mark.parametrize("dtype,noinf", [(torch.float32, False), (torch.float16, True)])
+def test_index_logits_long_workgroup_ranges(dev, dtype, noinf):
+    """256 rows of 33,000 columns: with one workgroup per row (as many rows as CUs) a workgroup's range passes the
+    32,768 columns it can stage in LDS, so its logits are stored tile by tile; the same rows computed in a 4-row launch
+    (ranges staged and written at the end) give the same values bit for bit, row 0 matches the fp64 oracle, and
+    columns past ctx are -inf (noinf=False) or left as they were (noinf=True)."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    rows, L, bs = 256, 33000, 64
+    nbp = (L + bs - 1) // bs
+    store = _keys(nbp + 1, bs, 40)
+    g = torch.Generator().manual_seed(41)
+    bt = torch.randperm(nbp + 1, generator=g)[:nbp].view(1, nbp).to(torch.int32)
+    q = torch.randn(rows, 64, 128, generator=g).to(torch.bfloat16)
+    w = torch.rand(rows, 64, generator=g)
+    req = torch.zeros(rows, dtype=torch.int32)                          # every row reads the one key sequence
+    ctx = torch.randint(L - 3000, L + 1, (rows,), generator=g).to(torch.int32)
+    ctx[0] = L
+    st = torch.from_numpy(store).to(dev).view(nbp + 1, bs, 132)
+    big = torch.full((rows, L), 7.0, dtype=dtype, device=dev)
+    small = torch.full((4, L), 7.0, dtype=dtype, device=dev)
+    print(f"[logits] long ranges dtype={dtype} noinf={noinf}", flush=True)
+    kernels.index_logits(q.to(dev), w.to(dev), st, bt.to(dev), bs, req.to(dev), ctx.to(dev), L, out=big,
+                         noinf=noinf, dtype=dtype)
+    kernels.index_logits(q[:4].to(dev), w[:4].to(dev), st, bt.to(dev), bs, req[:4].to(dev), ctx[:4].to(dev), L,
+                         out=small, noinf=noinf, dtype=dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(big[:4].view(torch.int16 if dtype == torch.float16 else torch.int32),
+                       small.view(torch.int16 if dtype == torch.float16 else torch.int32))
+    got = big.float().cpu().numpy()
+    c = ctx.numpy()
+    for r in (1, 100, 255):
+        tail = got[r, c[r]:]
+        assert np.all(tail == 7.0) if noinf else np.all(np.isneginf(tail))
+    exp = ref.index_logits(q[:1].float().numpy(), w[:1].numpy(), store, bt.numpy(), bs, req[:1].numpy(),
+                           ctx[:1].numpy(), L)
+    tol = 2e-5 if dtype == torch.float32 else 2.0 ** -10
+    err = np.abs(got[0] - exp[0]) / np.maximum(1.0, np.abs(exp[0]))
+    print(f"[logits] long ranges: row 0 max rel err {err.max():.3e}", flush=True)
+    assert err.max() <= tol
+
+
 def test_topk_random_and_lengths(dev):
     g = np.random.default_rng(0)
     rows, L = 16, 32768
