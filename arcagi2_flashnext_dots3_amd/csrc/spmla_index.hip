@@ -73,8 +73,8 @@ __device__ inline uint32_t fp8hi_bf16x2(uint32_t w) {
 }
 
 // Logits workgroup: the waves of one CU (one workgroup per CU, so no later-dispatched workgroup waits behind an
-// older one's issue priority) share a range of 32-key tiles of one row; wave w computes tiles tb + w, tb + w + NW,
-// ... (NW = LG_NWV), all 64 heads of a tile per step. The key codes go straight from global memory into the
+// older one's issue priority) share a range of 32-key tiles of one row; each wave computes all 64 heads of one tile
+// per step, its first tiles tb + w + k NW (NW = LG_NWV) and later ones claimed from an LDS counter. The key codes go straight from global memory into the
 // registers of the MFMA B operand: lane (k, h) of a tile loads 16-byte chunks 2 kp + h (kp = 0..3) of key k, which
 // are the key's dims 32 kp + 16 h .. + 15 in the order the operand takes them, and the key's scale. A wave keeps
 // LG_D tiles of loads in flight: step t computes tile t, then loads the codes of tile t + LG_D (whose block-table
@@ -101,6 +101,7 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
   __shared__ uint32_t hh[1024];                             // level-0 histogram (p.hist): 2048 16-bit counts
   __shared__ float sbuf[LG_STAGE];                          // staged logits of the range's columns
   __shared__ uint32_t smask[LG_STAGE / 32];                 // per tile: the columns to write
+  __shared__ int claim;                                     // next unclaimed tile of the range
   const int row = blockIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
@@ -127,10 +128,10 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
       for (int b = (int)threadIdx.x; b < 2048; b += LG_NWV * 64) hrow_out[b] = 0u;
     return;
   }
-  if (hrow_out) {
+  if (threadIdx.x == 0) claim = tb + 2 * LG_D * LG_NWV;     // steps 0 .. 2 LG_D - 1 take tiles tb + k NW + w
+  if (hrow_out)
     for (int b = (int)threadIdx.x; b < 1024; b += LG_NWV * 64) hh[b] = 0u;
-    __syncthreads();
-  }
+  __syncthreads();
   const int nh = hrow_out ? min(ctx, p.Lc) : 0;             // columns the histogram counts
   const int* btr = FLAT ? nullptr : p.bt + (long long)p.req[row] * p.bt_st;
   const int lo = p.lo ? p.lo[row] : 0;
@@ -204,9 +205,6 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
     for (int i = 0; i < 16; ++i) wl[m][i] = __shfl(myw, 8 * (i >> 2) + 4 * half + (i & 3), 64);
   }
 
-  // tile id of the wave's step t; the wave has n steps
-  auto tile = [&](int t) { return tb + wv + t * LG_NWV; };
-  const int n = tv - tb > wv ? (tv - tb - wv + LG_NWV - 1) / LG_NWV : 0;
   // step t computes tile t
   auto compute = [&](int id, const u32x4 (&c)[4], float sc, bool ok) {
     bf16x8 kb[8];
@@ -260,26 +258,41 @@ __global__ void __launch_bounds__(LG_NWV * 64) logits_kernel(LogitParams p) {
     }
   };
 
+  // tiles of steps t .. t + 2D - 1 (slot t % 2D, wave-uniform): the first 2D steps take tiles tb + k NW + w, each
+  // later one is claimed from the LDS counter 2D steps ahead (when its block-table entries are loaded), so the waves
+  // finish together whatever each one's issue priority and memory service (with equal static shares the youngest
+  // waves of a workgroup ended up to 31 us after the oldest at 131072 columns). A wave's tiles only grow, so it is
+  // done once a whole round of 2D steps holds no tile below tv.
   // loads in flight: codes of steps t .. t + D - 1 (slot t % D), block-table entries of steps t + D .. t + 2D - 1
-  // (slot t % 2D). Every step issues the same loads (steps past n read the row-0 key and the range's first
-  // block-table entry, cache hits, and are not computed), so the compiler's wait before a step's first use of its
-  // codes counts the loads of the D - 1 steps after it on every path.
+  // (slot t % 2D). Every step issues the same loads and claim (tiles at or past tv read the row-0 key and the
+  // range's first block-table entry, cache hits, and are not computed), so the compiler's wait before a step's first
+  // use of its codes counts the loads of the D - 1 steps after it on every path.
+  int ids[2 * D];
+#pragma unroll
+  for (int k = 0; k < 2 * D; ++k) ids[k] = tb + wv + k * LG_NWV;
   u32x4 cd[D][4];
   float scv[D];
   bool okv[D];
   int btv[2 * D];
 #pragma unroll
-  for (int k = 0; k < 2 * D; ++k) btv[k] = load_bt(tile(k));
+  for (int k = 0; k < 2 * D; ++k) btv[k] = load_bt(ids[k]);
 #pragma unroll
-  for (int k = 0; k < D; ++k) okv[k] = load_codes(tile(k), btv[k], cd[k], scv[k]);
+  for (int k = 0; k < D; ++k) okv[k] = load_codes(ids[k], btv[k], cd[k], scv[k]);
+  bool live = true;
 #pragma unroll 1
-  for (int t0 = 0; t0 < n; t0 += 2 * D) {
+  while (live) {
+    live = false;
 #pragma unroll
     for (int s = 0; s < 2 * D; ++s) {
-      const int t = t0 + s;
-      if (t < n) compute(tile(t), cd[s % D], scv[s % D], okv[s % D]);     // uniform
-      okv[s % D] = load_codes(tile(t + D), btv[(s + D) % (2 * D)], cd[s % D], scv[s % D]);
-      btv[s] = load_bt(tile(t + 2 * D));
+      int nxt = 0;
+      if (lane == 0) nxt = atomicAdd(&claim, 1);            // the tile of step t + 2D (an LDS atomic)
+      if (ids[s] < tv) {                                    // uniform
+        live = true;
+        compute(ids[s], cd[s % D], scv[s % D], okv[s % D]);
+      }
+      okv[s % D] = load_codes(ids[(s + D) % (2 * D)], btv[(s + D) % (2 * D)], cd[s % D], scv[s % D]);
+      ids[s] = __builtin_amdgcn_readfirstlane(nxt);
+      btv[s] = load_bt(ids[s]);
     }
   }
   if (stage || hrow_out) __syncthreads();   // every wave has computed (and counted) its tiles
