@@ -66,6 +66,33 @@ def _topk_check(dev, lg, ctx, K):
         assert bad.size == 0, f"single_pass={single} ws={'small' if ws is not None else 'full'}: rows {bad[:8]} differ"
 
 
+def test_index_logits_short_contexts(dev):
+    """Ranges shorter than a workgroup's waves (8 rows of 6000 columns: 32 workgroups per row of 6 tiles each for 8
+    waves) and rows whose valid keys end inside or before a range (ctx 0, 1, 31, 33, 100, 1500, 1537, 6000): every
+    tile below ctx is computed once and columns past ctx are -inf, against the fp64 oracle."""
+    from arcagi2_flashnext_dots3_amd import kernels
+    rows, L, bs = 8, 6000, 64
+    nbp = (L + bs - 1) // bs
+    nb = rows * nbp + 2
+    store = _keys(nb, bs, 50)
+    g = torch.Generator().manual_seed(51)
+    bt = torch.randperm(nb, generator=g)[: rows * nbp].reshape(rows, nbp).to(torch.int32)
+    q = torch.randn(rows, 64, 128, generator=g).to(torch.bfloat16)
+    w = torch.rand(rows, 64, generator=g)
+    req = torch.arange(rows, dtype=torch.int32)
+    ctx = torch.tensor([0, 1, 31, 33, 100, 1500, 1537, L], dtype=torch.int32)
+    print("[logits] short contexts", flush=True)
+    out = kernels.index_logits(q.to(dev), w.to(dev), torch.from_numpy(store).to(dev).view(nb, bs, 132),
+                               bt.to(dev), bs, req.to(dev), ctx.to(dev), L)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    exp = ref.index_logits(q.float().numpy(), w.numpy(), store, bt.numpy(), bs, req.numpy(), ctx.numpy(), L)
+    assert np.array_equal(np.isinf(got), np.isinf(exp))
+    fin = np.isfinite(exp)
+    err = np.abs(got[fin] - exp[fin]) / np.maximum(1.0, np.abs(exp[fin]))
+    assert err.max() <= 2e-5
+
+
 @pytest.mark.parametrize("dtype,noinf", [(torch.float32, False), (torch.float16, True)])
 def test_index_logits_long_workgroup_ranges(dev, dtype, noinf):
     """256 rows of 33,000 columns: with one workgroup per row (as many rows as CUs) a workgroup's range passes the
