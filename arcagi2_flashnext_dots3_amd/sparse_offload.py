@@ -21,6 +21,7 @@ and attended there by spmla_attn_merge, which merges the HBM tier's partial exac
 reference's tier combine). Without a cache (C = 0) every row takes the host tier.
 """
 import os
+import re
 
 import torch
 
@@ -83,14 +84,15 @@ class LayerOffload:
     the reference's two-choice set placement (ARC_OFFLOAD_TWO_CHOICE, offload_fill.py:16-23): a missing row whose set
     has no free way takes one in a second, hashed set before it spills; lookups and invalidations cover both sets.
     trace: a diagnostics.AccessTrace that records the stored slots and the decode rows of a window of calls.
-    stats_every=N: every N attend calls, `log` gets the cache's hit rate over that call's rows.
+    stats_every=N: every N attend calls, `log` gets the cache's hit rate over that call's rows. lstats_every=N (W-way
+    cache): every N calls, that call's hits, distinct misses and spill rows.
     """
 
     _count = 0           # layers built in this process (the first one takes the default access trace)
 
     def __init__(self, num_host_rows, device, key=None, cache_rows=0, row_fmt="row656", cache_mode="static", ways=16,
                  spill_rows=131072, overlap_fill=True, two_choice=False, cache_fmt="row656", packed=False,
-                 time_every=None, host_direct=False, trace=None, stats_every=None, log=print):
+                 time_every=None, host_direct=False, trace=None, stats_every=None, log=print, lstats_every=None):
         if row_fmt not in HOST_ROW:
             raise ValueError(f"row_fmt must be one of {sorted(HOST_ROW)}")
         if cache_mode not in ("static", "ways"):
@@ -137,6 +139,14 @@ class LayerOffload:
         self.stats_every = int(stats_every)
         self.log = log
         self._ncall = 0
+        # the W-way cache's counts of each call (hits, distinct misses, spill rows), logged every N calls
+        # (ARC_OFFLOAD_LSTATS=N, sparse_offload.py:210-211, :1302-1309; reads them back: a host synchronization)
+        if lstats_every is None:
+            lstats_every = int(os.environ.get("ARC_OFFLOAD_LSTATS", "0") or 0)
+        self.lstats_every = int(lstats_every)
+        self._lcall = 0
+        m = re.search(r"layers\.(\d+)\.", key or "")
+        self.layer = int(m.group(1)) if m else -1         # backbone layer id from the cache key, as the reference
         self.wc = None
         self.W = int(ways) if cache_mode == "ways" else 1
         if cache_mode == "ways":
@@ -284,6 +294,12 @@ class LayerOffload:
                 self._stat(idx)
         e0 = self.timer.begin(q.device)
         res = self._attend(q, idx, sm_scale, kv_scale, num_heads, ql, out, lse, return_lse)
+        if self.lstats_every and self.wc is not None:
+            self._lcall += 1
+            if self._lcall % self.lstats_every == 0:
+                st = self.wc.state.tolist()
+                self.log(f"[offl] L{self.layer} C={self.C} T={q.shape[0]} n={idx.numel()} hit={st[3]} miss={st[1]} "
+                         f"spill={st[2]}")
         if e0 is not None:
             packed = self.packed and ql is not None and 1 < int(ql) <= 6 and q.shape[0] % int(ql) == 0
             arm = "packed" if packed else ("ways" if self.wc is not None else ("tiers" if self.C else "host"))

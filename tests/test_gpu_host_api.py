@@ -384,6 +384,30 @@ def test_offload_hit_rate_stats(dev):
     assert lines == ["[offstats] C=800 rows=250 uniq=200 hit=0.600"]
 
 
+def test_offload_ways_call_stats(dev):
+    """lstats_every (ARC_OFFLOAD_LSTATS): the W-way cache's counts of the call (hits, distinct misses, spill rows)
+    with the layer id of the key: a first call misses every distinct valid row, a repeat of it hits every entry."""
+    from arcagi2_flashnext_dots3_amd.sparse_offload import LayerOffload
+    R, C, T, H, K = 3000, 1024, 2, 64, 256
+    lines = []
+    lo = LayerOffload(R, dev, key="model.layers.7.self_attn.indexer.k_cache", cache_rows=C, cache_mode="ways",
+                      ways=16, lstats_every=1, log=lines.append)
+    g = torch.Generator().manual_seed(27)
+    lo.store(torch.randn(R, 512, generator=g).to(torch.bfloat16).to(dev),
+             torch.randn(R, 64, generator=g).to(torch.bfloat16).to(dev), torch.arange(R, device=dev))
+    q = make_q(T, H, seed=28).to(dev)
+    idx = distinct_idx(T, K, 400, seed=29)                  # rows below 400: the two tokens share rows
+    idx[1, 200:] = -1
+    nvalid = int((idx >= 0).sum())
+    ndist = int(np.unique(idx.numpy()[idx.numpy() >= 0]).size)
+    print("[offload lstats]", flush=True)
+    lo.attend(q, idx.to(dev), SM, 1.0, H)
+    lo.attend(q, idx.to(dev), SM, 1.0, H)
+    torch.cuda.synchronize()
+    assert lines[0] == f"[offl] L7 C={C} T={T} n={T * K} hit=0 miss={ndist} spill=0"
+    assert lines[1] == f"[offl] L7 C={C} T={T} n={T * K} hit={nvalid} miss=0 spill=0"
+
+
 def test_portable_impl_offload_decode_and_prefill(dev):
     """Offload mode: decode tokens via LayerOffload.attend, one prefill chunk via staged (compacted) rows; both
     against the oracle over the same rows."""
